@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the gfx950 FlashAttention-2 hot path.
+
+Metric: causal fwd+bwd TFLOP/s at B=4, H=16, N=4096, D=64,
+fp16, and the fraction of MI355X's fp16 dense MFMA peak. One step is the
+reference benchmark's forward_backward runner (benchmark_attention.py:109-111):
+clear the input grads, run the public API forward with backend="triton", and
+backward a fixed dO. Inputs are synthetic (seeded N(0,1), fp32 -> fp16) and
+resident in HBM before timing starts.
+
+Prints ONE JSON line with the driver's fields plus
+  roofline:     the dominant kernel's algorithmic TFLOP/s (HIP events around
+                each launch on the launch stream) against the MFMA peak;
+  cpu_baseline: the reference's CPU path (its public API on CPU tensors
+                dispatches to torch SDPA, attention.py:647-648 -> 774-786)
+                timed on this host over the same workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "triton-flash-attention_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "causal fwd+bwd TFLOP/s, B4 H16 N4096 D64 fp16; % of fp16 MFMA peak"
+PEAK_FP16_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+# The reference's only published figure for this exact metric and shape
+# (Triton path, RTX 5050 Laptop GPU; README.md:159, benchmarks/results/rtx5050.csv:3).
+REFERENCE_PUBLISHED_TFLOPS = 13.283
+
+WORKLOADS = {
+    # name: (B, Hq, Hkv, N, D, causal, input scale, seed)
+    "c2": (4, 16, 16, 4096, 64, True, 1.0, 1002),
+    "c3": (2, 16, 4, 2049, 64, True, 1.0, 1003),
+    "c4-bidir": (2, 32, 32, 8192, 128, False, 0.5, 1004),
+    "c4-causal": (2, 32, 32, 8192, 128, True, 0.5, 1004),
+    "c5": (1, 8, 2, 16381, 32, True, 1.0, 1005),
+}
+
+
+def make_inputs(B, Hq, Hkv, N, D, seed, mult):
+    import torch
+
+    g = torch.Generator("cpu").manual_seed(seed)
+    shapes = ((B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D))
+    return [(torch.randn(s, generator=g, dtype=torch.float32) * mult).half() for s in shapes]
+
+
+def kernel_flops(kernel: str, B: int, Hq: int, N: int, D: int, causal: bool) -> int:
+    """Algorithmic FLOPs one launch performs, in the reference convention where
+    one N x N x D matmul over the visible pairs costs 2 * B * Hq * pairs * D:
+    fwd = 2 matmuls (QK^T, PV); dkdv = 4 (S recompute, dP, dV, dK);
+    dq = 1 (dQ; its S and dP recomputes are already counted under dkdv).
+    fwd + dkdv + dq = 7 matmuls = 3.5 x forward, the reference's fwd+bwd count."""
+    pairs = N * (N + 1) // 2 if causal else N * N
+    per_matmul = 2 * B * Hq * pairs * D
+    return {"fwd": 2, "dkdv": 4, "dq": 1}[kernel] * per_matmul
+
+
+def cpu_baseline(inputs, causal: bool, budget_s: float):
+    """The reference's CPU path on the same workload: the public API with CPU
+    tensors falls back to torch SDPA. Median of repetitions after one warmup,
+    repeated until ``budget_s`` of CPU work has been spent."""
+    import torch
+
+    from triton_flash_attention import scaled_dot_product_attention
+
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, 16)  # the GPU box's CPU share
+    torch.set_num_threads(threads)
+    q, k, v, do = (t.clone() for t in inputs)
+    gqa = q.shape[1] != k.shape[1]
+    q.requires_grad_()
+    k.requires_grad_()
+    v.requires_grad_()
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa).backward(do)
+
+    t0 = time.perf_counter()
+    step()  # warmup
+    times = []
+    spent = time.perf_counter() - t0
+    while spent < budget_s and len(times) < 7:
+        t1 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t1)
+        spent = time.perf_counter() - t0
+        print(f"[bench] cpu baseline rep {len(times)}: {times[-1]:.3f} s", file=sys.stderr,
+              flush=True)
+    times.sort()
+    return times[len(times) // 2], threads, len(times)
+
+
+def load_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` measured with rocprofv3 PMC counters
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size), as
+    committed under profiles/; None if not measured for this workload."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        return data.get(workload, {}).get(kernel, {}).get("hbm_bytes_per_launch")
+    except (ValueError, AttributeError):
+        return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="gfx950 FlashAttention-2 headline benchmark")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2",
+                    help="c2 is the metric's configuration; the others are for exploration")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="CPU-work budget of the CPU baseline (0 disables it)")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every "
+              "(batch, head) is independent; see DESIGN.md for how it would shard). "
+              f"Requested --gpus {args.gpus} / WORLD_SIZE {world}.", file=sys.stderr)
+        return 2
+    if args.steps <= 0 or args.warmup < 0:
+        print("--steps must be > 0 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X)", file=sys.stderr)
+        return 2
+    from benchmarks.benchmark_attention import attention_flops
+    from triton_flash_attention import _ops, explain_dispatch, scaled_dot_product_attention
+
+    B, Hq, Hkv, N, D, causal, mult, seed = WORKLOADS[args.workload]
+    cpu_inputs = make_inputs(B, Hq, Hkv, N, D, seed, mult)
+    q, k, v, do = (t.to("cuda") for t in cpu_inputs)
+    decision = explain_dispatch(q, k, v, enable_gqa=Hq != Hkv)
+    if decision.backend != "triton":
+        print(f"custom kernel not selected: {decision.reason}", file=sys.stderr)
+        return 1
+    q.requires_grad_()
+    k.requires_grad_()
+    v.requires_grad_()
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=Hq != Hkv,
+                                           backend="triton")
+        out.backward(do)
+
+    print(f"[bench] {args.workload}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal}; "
+          f"warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with _ops.LaunchTimer() as timer:
+        for i in range(args.steps):
+            starts[i].record()
+            step()
+            ends[i].record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    step_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    total_ms = starts[0].elapsed_time(ends[-1])
+    ms_per_step = total_ms / args.steps
+    print(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step (wall {wall_s:.3f} s)",
+          file=sys.stderr, flush=True)
+
+    flops = attention_flops(batch=B, query_heads=Hq, sequence=N, head_dim=D, causal=causal,
+                            mode="forward-backward")
+    value = flops / (ms_per_step * 1e-3) / 1e12
+
+    kernels = {}
+    for name in ("fwd", "preprocess", "dkdv", "dq"):
+        mean = timer.mean_ms(name)
+        entry = {"mean_ms": round(mean, 5), "launches": len(timer.durations_ms(name))}
+        if name != "preprocess":
+            f = kernel_flops(name, B, Hq, N, D, causal)
+            entry["tflops"] = round(f / (mean * 1e-3) / 1e12, 2)
+        kernels[name] = entry
+    dominant = max(("fwd", "dkdv", "dq"), key=lambda n: kernels[n]["mean_ms"])
+    dom_flops = kernel_flops(dominant, B, Hq, N, D, causal)
+    achieved = dom_flops / (kernels[dominant]["mean_ms"] * 1e-3) / 1e12
+
+    record = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REFERENCE_PUBLISHED_TFLOPS, 2)
+        if args.workload == "c2" else None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) fp32 -> fp16, resident in HBM)",
+        "config": {
+            "workload": f"{args.workload}: {'causal' if causal else 'bidirectional'} "
+                        f"fwd+bwd B={B} Hq={Hq} Hkv={Hkv} N={N} D={D}",
+            "batch": B, "q_heads": Hq, "kv_heads": Hkv, "seq_len": N, "head_dim": D,
+            "causal": causal, "seed": seed, "input_scale": mult,
+            "parallelism": "single GPU",
+        },
+        "pct_of_peak": round(100.0 * value / PEAK_FP16_TFLOPS, 2),
+        "step_ms_p20_p50_p80": [round(step_ms[int(0.2 * (len(step_ms) - 1))], 5),
+                                round(step_ms[(len(step_ms) - 1) // 2], 5),
+                                round(step_ms[int(0.8 * (len(step_ms) - 1))], 5)],
+        "kernels": kernels,
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": load_traffic(args.workload, dominant),
+        },
+        "baseline_note": "vs_baseline divides by the reference's published 13.283 TFLOP/s "
+                         "(Triton path, RTX 5050 Laptop GPU, README.md:159)",
+        "device": torch.cuda.get_device_name(),
+    }
+
+    if args.cpu_seconds > 0:
+        median_s, threads, reps = cpu_baseline(cpu_inputs, causal, args.cpu_seconds)
+        record["cpu_baseline"] = {
+            "value": round(flops / median_s / 1e12, 4),
+            "unit": "TFLOP/s",
+            "cores": threads,
+            "kind": "reference",
+            "sample": (f"full {args.workload} workload (fwd+bwd, {flops / 1e9:.1f} GFLOP) through "
+                       "the public API on CPU fp16 tensors, which is the reference's CPU path "
+                       f"(torch SDPA); median of {reps} reps after 1 warmup, "
+                       f"{median_s:.3f} s/rep, host {platform.processor() or platform.machine()}"),
+        }
+    else:
+        record["cpu_baseline"] = None
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,118 @@
+/*
+ * fa_gfx950.h — C ABI of the MI355X (gfx950) FlashAttention-2 library
+ * (libfa_gfx950.so).
+ *
+ * This is the drop-in boundary for the hot path of
+ * triton_flash_attention (reference: triton_flash_attention/attention.py).
+ * The reference launches three Triton kernels from Python; each entry point
+ * below replaces one of those launches (or one half of the fused backward
+ * launch) and keeps its argument meaning:
+ *
+ *   fa_fwd             replaces  _attn_fwd[grid](...)             attention.py:690-718
+ *   fa_bwd_preprocess  replaces  _attn_bwd_preprocess[grid](...)  attention.py:736-744
+ *   fa_bwd_dkdv        replaces  _attn_bwd[grid](...) phase 1     attention.py:754-770 (kernel 428-505)
+ *   fa_bwd_dq          replaces  _attn_bwd[grid](...) phase 2     attention.py:754-770 (kernel 507-573)
+ *
+ * Conventions shared by every entry point
+ *   - Tensors are caller-owned device memory, contiguous, row-major:
+ *       q, o, dO, dq   : [B, Hq,  N, D]  IEEE binary16
+ *       k, v, dk, dv   : [B, Hkv, N, D]  IEEE binary16
+ *       lse, delta     : [B, Hq,  N]     float32
+ *     (the reference forces the same layout with .contiguous(),
+ *      attention.py:727, 841-843, and indexes it that way, 251, 412-414).
+ *   - lse is the base-2 log-sum-exp of the scaled scores of each query row,
+ *     lse = log2(sum_j exp2(scale*log2(e)*q.k_j)), the quantity the reference
+ *     stores at attention.py:230.
+ *   - Causal masking is top-left: query i sees keys j <= i (attention.py:65).
+ *   - GQA: query head h reads key/value head h / (Hq / Hkv) (attention.py:128-131).
+ *     dk/dv are the sums over the Hq/Hkv query heads of a group, reduced in
+ *     fp32 inside the kernel (no atomics, deterministic).
+ *   - Supported head_dim D: 32, 64, 128 (attention.py:21). N >= 1, any value.
+ *   - Every tensor pointer must be 16-byte aligned (the kernels move 128-bit
+ *     vectors); fresh allocations from any HIP allocator are.
+ *   - `stream` is a hipStream_t (NULL = the null stream). Calls are
+ *     asynchronous on that stream; nothing allocates, frees or synchronizes.
+ *   - Return value: 0 on success; a negative FA_ERR_* code when an argument is
+ *     rejected before any HIP call; otherwise the hipError_t of the launch.
+ *     fa_last_error() returns a thread-local message describing the last
+ *     failure of the calling thread.
+ */
+#ifndef FA_GFX950_H
+#define FA_GFX950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+/* Error codes returned before any HIP call is made. */
+#define FA_OK 0
+#define FA_ERR_NULL_POINTER (-1)       /* a required pointer is NULL            */
+#define FA_ERR_BAD_SHAPE (-2)          /* B, H, N <= 0 or Hq % Hkv != 0          */
+#define FA_ERR_HEAD_DIM (-3)           /* D not in {32, 64, 128}                 */
+#define FA_ERR_TOO_LARGE (-4)          /* a head slab exceeds 2^31 bytes or the  */
+                                       /* launch grid exceeds 2^31 work-groups   */
+#define FA_ERR_BAD_SCALE (-5)          /* scale not finite or not > 0            */
+#define FA_ERR_BAD_TILING (-6)         /* no compiled kernel for this tiling     */
+#define FA_ERR_MISALIGNED (-7)         /* a tensor pointer is not 16-byte aligned */
+
+/* 16-bit storage type of IEEE binary16 elements. */
+typedef uint16_t fa_half_t;
+
+/* Forward: o = softmax(scale * q k^T [+ causal mask]) v, and lse (base 2).
+ * Replaces the _attn_fwd launch, attention.py:690-718 (kernel 90-234). */
+int fa_fwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+           fa_half_t* o, float* lse,
+           int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+           float scale, int causal, void* stream);
+
+/* delta[b,h,i] = sum_d o[b,h,i,d] * dO[b,h,i,d] in fp32.
+ * Replaces the _attn_bwd_preprocess launch, attention.py:736-744 (kernel 237-255). */
+int fa_bwd_preprocess(const fa_half_t* o, const fa_half_t* dO, float* delta,
+                      int64_t B, int64_t Hq, int64_t N, int64_t D, void* stream);
+
+/* dk, dv (fully overwritten; no zero-fill needed). Recomputes P from lse.
+ * Replaces phase 1 of the _attn_bwd launch, attention.py:754-770 (kernel 428-505). */
+int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                const fa_half_t* dO, const float* lse, const float* delta,
+                fa_half_t* dk, fa_half_t* dv,
+                int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                float scale, int causal, void* stream);
+
+/* dq (fully overwritten). Recomputes P from lse.
+ * Replaces phase 2 of the _attn_bwd launch, attention.py:754-770 (kernel 507-573). */
+int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+              const fa_half_t* dO, const float* lse, const float* delta,
+              fa_half_t* dq,
+              int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+              float scale, int causal, void* stream);
+
+/* Thread-local description of the last failure on the calling thread
+ * ("" if none). The pointer stays valid until the next call on the thread. */
+const char* fa_last_error(void);
+
+/* FA_ABI_VERSION of the loaded library. */
+int fa_abi_version(void);
+
+/* Tiling table (replaces the Triton autotuner, attention.py:82-90, 353-381).
+ * kernel: 0 = fwd, 1 = bwd_dkdv, 2 = bwd_dq.
+ * fa_get_tiling writes the entry used for (kernel, D, causal):
+ *   out[0] = waves per work-group, out[1] = rows per work-group,
+ *   out[2] = streamed tile length (keys for fwd/dq, queries for dkdv),
+ *   out[3] = variant index.
+ * fa_num_tiling_variants / fa_describe_tiling_variant enumerate the compiled
+ * variants for (kernel, D, causal); fa_set_tiling selects one for the
+ * process (variant < 0 restores the default). Used by tuning sweeps. */
+int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);
+int fa_num_tiling_variants(int kernel, int64_t D, int causal);
+int fa_describe_tiling_variant(int kernel, int64_t D, int causal, int variant, int* out4);
+int fa_set_tiling(int kernel, int64_t D, int causal, int variant);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_GFX950_H */

@@ -1,0 +1,68 @@
+"""Known answers for the FLOP and memory model (reference
+tests/test_benchmark_model.py:4-42) and the BASELINE configuration counts."""
+
+from __future__ import annotations
+
+import importlib.util
+from pathlib import Path
+
+from benchmarks.benchmark_attention import attention_flops, memory_model
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_causal_forward_counts_only_visible_pairs() -> None:
+    assert attention_flops(batch=1, query_heads=1, sequence=4, head_dim=8, causal=True,
+                           mode="forward") == 4 * 10 * 8
+
+
+def test_backward_is_two_and_a_half_forward_passes() -> None:
+    kw = dict(batch=2, query_heads=4, sequence=16, head_dim=32, causal=False)
+    assert attention_flops(mode="backward", **kw) == int(2.5 * attention_flops(mode="forward", **kw))
+
+
+def test_memory_model_is_linear_for_saved_lse() -> None:
+    small = memory_model(batch=1, query_heads=1, sequence=128)
+    large = memory_model(batch=1, query_heads=1, sequence=256)
+    assert large["saved_lse_mib"] == 2 * small["saved_lse_mib"]
+    assert large["naive_score_mib"] == 4 * small["naive_score_mib"]
+
+
+def test_baseline_configuration_flop_counts() -> None:
+    """fwd+bwd algorithmic FLOPs quoted for the BASELINE configurations."""
+    fb = "forward-backward"
+    assert attention_flops(batch=4, query_heads=16, sequence=4096, head_dim=64, causal=True,
+                           mode=fb) == 481_153_777_664
+    assert attention_flops(batch=4, query_heads=16, sequence=4096, head_dim=64, causal=True,
+                           mode="forward") == 137_472_507_904
+    assert attention_flops(batch=2, query_heads=16, sequence=2049, head_dim=64, causal=True,
+                           mode=fb) == 60_217_651_200
+    assert attention_flops(batch=2, query_heads=32, sequence=8192, head_dim=128, causal=False,
+                           mode=fb) == 7_696_581_394_432
+    assert attention_flops(batch=2, query_heads=32, sequence=8192, head_dim=128, causal=True,
+                           mode=fb) == 3_848_760_459_264
+    assert attention_flops(batch=1, query_heads=8, sequence=16381, head_dim=32, causal=True,
+                           mode=fb) == 480_889_547_264
+    # the published RTX 5050 figure: 4.8115e11 FLOP / 36.22221 ms = 13.283 TFLOP/s
+    assert round(481_153_777_664 / 36.22221e-3 / 1e12, 3) == 13.283
+    # the reference memory model at that shape: 2048 MiB of scores vs 1 MiB of LSE
+    m = memory_model(batch=4, query_heads=16, sequence=4096)
+    assert m == {"naive_score_mib": 2048.0, "saved_lse_mib": 1.0}
+
+
+def test_per_kernel_flops_sum_to_the_fwd_bwd_convention() -> None:
+    spec = importlib.util.spec_from_file_location("bench", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for causal in (False, True):
+        total = sum(bench.kernel_flops(k, 4, 16, 4096, 64, causal) for k in ("fwd", "dkdv", "dq"))
+        assert total == attention_flops(batch=4, query_heads=16, sequence=4096, head_dim=64,
+                                        causal=causal, mode="forward-backward")
+
+
+def test_bench_refuses_more_than_one_gpu(capsys) -> None:
+    spec = importlib.util.spec_from_file_location("bench", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    assert bench.main(["--gpus", "8"]) == 2
+    assert "one GPU" in capsys.readouterr().err

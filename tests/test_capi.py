@@ -1,0 +1,145 @@
+"""C-ABI checks that need no GPU: the built library loads, exports every
+function include/fa_gfx950.h declares, and rejects bad arguments with the
+documented FA_ERR_* codes and messages before making any HIP call."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from triton_flash_attention import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "fa_gfx950.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def header_constants() -> dict[str, int]:
+    text = HEADER.read_text()
+    return {m.group(1): int(m.group(2)) for m in
+            re.finditer(r"#define\s+(FA_[A-Z0-9_]+)\s+\(?(-?\d+)\)?", text)}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    ok, why = _lib.available()
+    assert ok, why
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared_functions()
+    assert {"fa_fwd", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dq", "fa_last_error",
+            "fa_abi_version"} <= set(names)
+    raw = ctypes.CDLL(str(_lib.library_path()))
+    for name in names:
+        assert hasattr(raw, name), f"{name} declared in {HEADER.name} but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature in _lib.py"
+
+
+def test_error_codes_match_header(lib):
+    consts = header_constants()
+    assert consts["FA_ABI_VERSION"] == _lib.ABI_VERSION == lib.fa_abi_version()
+    for name in ("FA_OK", "FA_ERR_NULL_POINTER", "FA_ERR_BAD_SHAPE", "FA_ERR_HEAD_DIM",
+                 "FA_ERR_TOO_LARGE", "FA_ERR_BAD_SCALE", "FA_ERR_BAD_TILING",
+                 "FA_ERR_MISALIGNED"):
+        assert consts[name] == getattr(_lib, name), name
+
+
+# Fake device addresses: never dereferenced, because every call below is
+# rejected by argument checks that run before any HIP call.
+P = 0x10000
+
+
+def _fwd(lib, q=P, k=P, v=P, o=P, lse=P, B=1, Hq=2, Hkv=2, N=64, D=64, scale=0.125, causal=1):
+    return lib.fa_fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, scale, causal, None)
+
+
+@pytest.mark.parametrize(
+    ("kwargs", "code", "message"),
+    [
+        (dict(q=None), "FA_ERR_NULL_POINTER", "null pointer"),
+        (dict(B=0), "FA_ERR_BAD_SHAPE", "must be positive"),
+        (dict(N=-3), "FA_ERR_BAD_SHAPE", "must be positive"),
+        (dict(Hq=3, Hkv=2), "FA_ERR_BAD_SHAPE", "divisible"),
+        (dict(D=48), "FA_ERR_HEAD_DIM", "head_dim must be one of (32, 64, 128)"),
+        (dict(D=256), "FA_ERR_HEAD_DIM", "head_dim"),
+        (dict(N=1 << 24, D=128), "FA_ERR_TOO_LARGE", "too large"),
+        (dict(q=P + 2), "FA_ERR_MISALIGNED", "16-byte aligned"),
+        (dict(lse=P + 4), "FA_ERR_MISALIGNED", "16-byte aligned"),
+        (dict(scale=0.0), "FA_ERR_BAD_SCALE", "scale"),
+        (dict(scale=-1.0), "FA_ERR_BAD_SCALE", "scale"),
+        (dict(scale=float("nan")), "FA_ERR_BAD_SCALE", "scale"),
+    ],
+)
+def test_fwd_rejects_bad_arguments(lib, kwargs, code, message):
+    rc = _fwd(lib, **kwargs)
+    assert rc == getattr(_lib, code)
+    assert message in _lib.last_error()
+    with pytest.raises(_lib.FlashAttentionError, match=re.escape(message)):
+        _lib.check(rc)
+
+
+def test_backward_entry_points_reject_bad_arguments(lib):
+    args = [P] * 7
+    rc = lib.fa_bwd_dkdv(*args, None, 1, 4, 2, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_NULL_POINTER
+    rc = lib.fa_bwd_dkdv(*args, P, 1, 4, 3, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE
+    rc = lib.fa_bwd_dq(*args, 1, 4, 2, 64, 96, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_HEAD_DIM
+    rc = lib.fa_bwd_dq(P, P, P, P, P, P + 8, P, 1, 4, 2, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_MISALIGNED
+    rc = lib.fa_bwd_preprocess(P, P, None, 1, 1, 8, 64, None)
+    assert rc == _lib.FA_ERR_NULL_POINTER
+    rc = lib.fa_bwd_preprocess(P, P, P, 1, 1, 8, 40, None)
+    assert rc == _lib.FA_ERR_HEAD_DIM
+
+
+def test_tiling_table_is_complete(lib):
+    for kernel in (_lib.KERNEL_FWD, _lib.KERNEL_DKDV, _lib.KERNEL_DQ):
+        for D in (32, 64, 128):
+            for causal in (False, True):
+                t = _lib.get_tiling(kernel, D, causal)
+                variants = _lib.tiling_variants(kernel, D, causal)
+                assert 0 <= t["variant"] < len(variants)
+                assert variants[t["variant"]] == t
+                assert t["rows"] == 32 * t["waves"] and t["tile"] % 32 == 0
+    with pytest.raises(_lib.FlashAttentionError):
+        _lib.get_tiling(7, 64, True)
+    with pytest.raises(_lib.FlashAttentionError):
+        _lib.get_tiling(0, 48, True)
+
+
+def test_tiling_override_round_trip(lib):
+    default = _lib.get_tiling(_lib.KERNEL_FWD, 64, True)
+    n = len(_lib.tiling_variants(_lib.KERNEL_FWD, 64, True))
+    try:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, n - 1)
+        assert _lib.get_tiling(_lib.KERNEL_FWD, 64, True)["variant"] == n - 1
+        with pytest.raises(_lib.FlashAttentionError):
+            _lib.set_tiling(_lib.KERNEL_FWD, 64, True, n)
+    finally:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, -1)
+    assert _lib.get_tiling(_lib.KERNEL_FWD, 64, True) == default
+
+
+def test_launch_without_a_device_reports_the_hip_error(lib):
+    """On a host with no GPU, a well-formed call reaches the launch and the HIP
+    runtime's error comes back as a positive code with its message (the fake
+    pointers are never touched: no kernel can run without a device)."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("only meaningful on a host without a GPU")
+    rc = _fwd(lib)
+    assert rc > 0
+    assert "fa_fwd launch" in _lib.last_error()

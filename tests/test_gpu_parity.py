@@ -1,0 +1,274 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle and the reference path.
+
+Everything here goes through the product path (libfa_gfx950.so via the public
+API with ``backend="triton"``, which raises instead of falling back) and is
+compared with:
+  * the fp64 CPU oracle (oracle/fa_oracle.c) at sizes it finishes in seconds,
+    and on head slices of the full BASELINE configurations;
+  * a plain PyTorch fp32 reference on the GPU at the full configurations;
+  * PyTorch SDPA (the reference's own path on ROCm, attention.py:774-786) at
+    the reference test shapes and tolerances (tests/test_cuda_correctness.py).
+Tolerances: O, dQ, dK, dV max-abs <= 2e-2 and
+relative L2 <= 5e-3; base-2 LSE max-abs <= 1e-4.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from fa_testutil import (
+    CONFIGS,
+    LSE_TOL,
+    assert_close,
+    errors,
+    make_inputs,
+    torch_reference_fp32,
+)
+from oracle import oracle
+from triton_flash_attention import _lib, _ops, explain_dispatch, scaled_dot_product_attention
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _note(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _library_loaded():
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ok, why = _lib.available()
+    assert ok, f"libfa_gfx950.so must load on the GPU box: {why}"
+    props = torch.cuda.get_device_properties(0)
+    _note(f"device: {props.name} {getattr(props, 'gcnArchName', '?')} CUs={props.multi_processor_count}")
+
+
+def run_kernel(q, k, v, do, causal, scale=None):
+    """Forward + backward through the public API on the GPU; LSE from the same
+    forward kernel via the op layer. Returns CPU float64 numpy arrays."""
+    enable_gqa = q.shape[1] != k.shape[1]
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    dod = do.to(DEV)
+    out = scaled_dot_product_attention(
+        qd, kd, vd, is_causal=causal, enable_gqa=enable_gqa, scale=scale, backend="triton"
+    )
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), dod)
+    s = q.shape[-1] ** -0.5 if scale is None else scale
+    o2, lse = _ops.flash_fwd(qd.detach().contiguous(), kd.detach().contiguous(),
+                             vd.detach().contiguous(), causal, s)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, out.detach()), "public API and op layer disagree"
+    return {
+        "o16": out.detach().cpu(),
+        "o": out.detach().double().cpu().numpy(),
+        "lse": lse.double().cpu().numpy(),
+        "dq": dq.double().cpu().numpy(),
+        "dk": dk.double().cpu().numpy(),
+        "dv": dv.double().cpu().numpy(),
+    }
+
+
+def check_against_oracle(got, q, k, v, do, causal, scale=None, tag=""):
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
+                           o16=got["o16"].numpy())
+    report = {}
+    for name in ("o", "dq", "dk", "dv"):
+        report[name] = assert_close(f"{tag} {name}", got[name], ref[name])
+    lse_err = float(np.max(np.abs(got["lse"] - ref["lse"])))
+    assert lse_err <= LSE_TOL, f"{tag} lse: max-abs {lse_err:.3e} (tol {LSE_TOL:.0e})"
+    report["lse"] = lse_err
+    _note(f"{tag}: " + ", ".join(
+        f"{k}={v[0]:.2e}/{v[1]:.2e}" if isinstance(v, tuple) else f"{k}={v:.2e}"
+        for k, v in report.items()))
+    return report
+
+
+# ---------------------------------------------------------------------------
+# Reference test shapes (tests/test_cuda_correctness.py:87-101) plus D=128.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sequence", [17, 129])
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_reference_shapes_match_oracle(sequence, head_dim, causal):
+    q, k, v, do = make_inputs(1, 2, 2, sequence, head_dim, seed=123, mult=0.5, do_mult=0.1)
+    got = run_kernel(q, k, v, do, causal)
+    check_against_oracle(got, q, k, v, do, causal, tag=f"N={sequence} D={head_dim} causal={causal}")
+
+
+def test_reference_gqa_shape_matches_oracle():
+    q, k, v, do = make_inputs(1, 4, 2, 65, 64, seed=123, mult=0.5, do_mult=0.1)
+    got = run_kernel(q, k, v, do, True)
+    check_against_oracle(got, q, k, v, do, True, tag="GQA 4->2 N=65 D=64 causal")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sequence", [17, 129])
+@pytest.mark.parametrize("head_dim", [32, 64])
+def test_matches_torch_sdpa_like_reference_suite(sequence, head_dim, causal):
+    """The reference's own differential test, against PyTorch SDPA evaluated
+    in fp32 on the GPU (atol 2e-2 for O, 3e-2 for grads, rtol 0)."""
+    torch.manual_seed(123)
+    q = (torch.randn(1, 2, sequence, head_dim, device=DEV, dtype=torch.float16) * 0.5)
+    k = (torch.randn(1, 2, sequence, head_dim, device=DEV, dtype=torch.float16) * 0.5)
+    v = (torch.randn(1, 2, sequence, head_dim, device=DEV, dtype=torch.float16) * 0.5)
+    do = torch.randn_like(q) * 0.1
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    actual = scaled_dot_product_attention(qa, ka, va, is_causal=causal, backend="triton")
+    qe, ke, ve = (t.float().requires_grad_() for t in (q, k, v))
+    expected = torch.nn.functional.scaled_dot_product_attention(qe, ke, ve, is_causal=causal)
+    torch.testing.assert_close(actual.float(), expected, atol=2e-2, rtol=0)
+    ga = torch.autograd.grad(actual, (qa, ka, va), do)
+    ge = torch.autograd.grad(expected, (qe, ke, ve), do.float())
+    for a, e in zip(ga, ge):
+        torch.testing.assert_close(a.float(), e, atol=3e-2, rtol=0)
+
+
+# ---------------------------------------------------------------------------
+# Tails and tile boundaries, GQA groups, custom scale.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("sequence", [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 255, 256, 257, 300])
+def test_tails_match_oracle(sequence):
+    for causal in (False, True):
+        q, k, v, do = make_inputs(2, 2, 2, sequence, 64, seed=7 + sequence)
+        got = run_kernel(q, k, v, do, causal)
+        check_against_oracle(got, q, k, v, do, causal, tag=f"tail N={sequence} causal={causal}")
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("heads", [(4, 1), (8, 2), (6, 3), (3, 3)])
+def test_gqa_groups_match_oracle(head_dim, heads):
+    hq, hkv = heads
+    for causal in (False, True):
+        q, k, v, do = make_inputs(2, hq, hkv, 150, head_dim, seed=11 * hq + hkv)
+        got = run_kernel(q, k, v, do, causal)
+        check_against_oracle(got, q, k, v, do, causal,
+                             tag=f"GQA {hq}->{hkv} D={head_dim} causal={causal}")
+
+
+def test_custom_scale_matches_oracle():
+    q, k, v, do = make_inputs(1, 2, 2, 200, 64, seed=5)
+    for scale in (0.05, 0.25, 1.0):
+        got = run_kernel(q, k, v, do, True, scale=scale)
+        check_against_oracle(got, q, k, v, do, True, scale=scale, tag=f"scale={scale}")
+
+
+# ---------------------------------------------------------------------------
+# Closed-form special cases (values fixed by the mathematics).
+# ---------------------------------------------------------------------------
+def test_causal_row_zero_sees_only_key_zero():
+    q, k, v, do = make_inputs(1, 2, 2, 300, 64, seed=3)
+    got = run_kernel(q, k, v, do, True)
+    np.testing.assert_allclose(got["o"][:, :, 0, :], v.double().numpy()[:, :, 0, :],
+                               rtol=1e-3, atol=1e-6)
+    s00 = (q.double()[:, :, 0, :] * k.double()[:, :, 0, :]).sum(-1) * 64 ** -0.5 / np.log(2.0)
+    assert np.max(np.abs(got["lse"][:, :, 0] - s00.numpy())) < LSE_TOL
+
+
+def test_zero_query_gives_uniform_attention():
+    q, k, v, do = make_inputs(1, 2, 2, 190, 32, seed=4)
+    q = torch.zeros_like(q)
+    for causal in (False, True):
+        got = run_kernel(q, k, v, do, causal)
+        vd = v.double().numpy()
+        if causal:
+            expected = np.cumsum(vd, axis=2) / np.arange(1, 191)[None, None, :, None]
+            lse = np.log2(np.arange(1, 191, dtype=np.float64))
+        else:
+            expected = np.broadcast_to(vd.mean(axis=2, keepdims=True), vd.shape)
+            lse = np.full(190, np.log2(190.0))
+        assert_close(f"uniform causal={causal}", got["o"], expected)
+        assert np.max(np.abs(got["lse"] - lse[None, None, :])) < LSE_TOL
+
+
+def test_constant_value_rows_give_zero_qk_gradients():
+    q, k, v, do = make_inputs(1, 2, 2, 160, 64, seed=8)
+    v = v[:, :, :1, :].expand_as(v).contiguous()
+    got = run_kernel(q, k, v, do, True)
+    np.testing.assert_allclose(got["o"], v.double().numpy(), atol=1e-3)
+    assert np.max(np.abs(got["dq"])) < 2e-3 and np.max(np.abs(got["dk"])) < 2e-3
+
+
+def test_deterministic_backward():
+    q, k, v, do = make_inputs(2, 8, 2, 333, 64, seed=9)
+    a = run_kernel(q, k, v, do, True)
+    b = run_kernel(q, k, v, do, True)
+    for name in ("o", "lse", "dq", "dk", "dv"):
+        assert np.array_equal(a[name], b[name]), f"{name} differs between identical runs"
+
+
+def test_strided_inputs_are_made_contiguous():
+    q, k, v, do = make_inputs(1, 2, 2, 96, 64, seed=10)
+    qs = q.transpose(1, 2).contiguous().transpose(1, 2)  # same values, non-contiguous
+    assert not qs.is_contiguous()
+    got = run_kernel(qs, k, v, do, False)
+    check_against_oracle(got, q, k, v, do, False, tag="strided q")
+
+
+def test_dispatch_selects_custom_kernel_on_gfx950():
+    q = torch.randn(1, 2, 64, 64, device=DEV, dtype=torch.float16)
+    decision = explain_dispatch(q, q, q)
+    assert decision.backend == "triton", decision.reason
+    q32 = q.float()
+    assert explain_dispatch(q32, q32, q32).backend == "torch"
+    q48 = torch.randn(1, 2, 64, 48, device=DEV, dtype=torch.float16)
+    assert explain_dispatch(q48, q48, q48).backend == "torch"
+    out = scaled_dot_product_attention(q32, q32, q32)  # auto falls back to SDPA
+    ref = torch.nn.functional.scaled_dot_product_attention(q32, q32, q32)
+    torch.testing.assert_close(out, ref)
+    with pytest.raises(RuntimeError, match="float16"):
+        scaled_dot_product_attention(q32, q32, q32, backend="triton")
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configurations at full size.
+# ---------------------------------------------------------------------------
+def _config_cases():
+    for name in ("c2", "c3", "c4", "c5"):
+        for causal in CONFIGS[name]["causal"]:
+            yield pytest.param(name, causal, id=f"{name}-{'causal' if causal else 'bidir'}")
+
+
+@pytest.mark.parametrize("name,causal", list(_config_cases()))
+def test_full_config_matches_fp32_reference(name, causal):
+    cfg = CONFIGS[name]
+    B, Hq, Hkv, N, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["N"], cfg["D"]
+    _note(f"{name} causal={causal}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D}")
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, cfg["seed"], cfg["mult"])
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    qa, ka, va = (t.clone().requires_grad_() for t in (qd, kd, vd))
+    out = scaled_dot_product_attention(qa, ka, va, is_causal=causal, enable_gqa=Hq != Hkv,
+                                       backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qa, ka, va), dod)
+    _, lse = _ops.flash_fwd(qd, kd, vd, causal, D ** -0.5)
+    torch.cuda.synchronize()
+    ref = torch_reference_fp32(qd, kd, vd, dod, causal, o16=out.detach())
+    torch.cuda.synchronize()
+    for tname, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert torch.isfinite(t).all(), f"{name} {tname} has non-finite values"
+        ma, rl = assert_close(f"{name} {tname}", t.float(), ref[tname])
+        _note(f"  {tname}: max-abs {ma:.3e} rel-L2 {rl:.3e}")
+    lse_err = float((lse - ref["lse"]).abs().max())
+    _note(f"  lse: max-abs {lse_err:.3e}")
+    assert lse_err <= LSE_TOL
+
+    # fp64 oracle on one key/value head's group of query heads (full N).
+    G = Hq // Hkv
+    sl = slice(0, G)
+    qs, ks, vs, dos = q[:1, sl], k[:1, :1], v[:1, :1], do[:1, sl]
+    got = {
+        "o16": out.detach()[:1, sl].cpu(),
+        "o": out.detach()[:1, sl].double().cpu().numpy(),
+        "lse": lse[:1, sl].double().cpu().numpy(),
+        "dq": dq[:1, sl].double().cpu().numpy(),
+        "dk": dk[:1, :1].double().cpu().numpy(),
+        "dv": dv[:1, :1].double().cpu().numpy(),
+    }
+    if N * N * D * G <= 2 ** 32:
+        check_against_oracle(got, qs, ks, vs, dos, causal, tag=f"{name} oracle slice")

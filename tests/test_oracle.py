@@ -1,0 +1,264 @@
+"""Pins the CPU oracle (oracle/fa_oracle.c) before it is trusted as the checker.
+
+Every oracle function is checked against something independent of it:
+  * PyTorch fp64 SDPA + autograd + logsumexp (the library routine the
+    reference falls back to, attention.py:786), live and through the committed
+    golden fixtures (tests/golden/attention_fp64.npz, made by
+    tests/golden/make_golden.py with torch only);
+  * closed forms the mathematics fixes (causal row 0, Q = 0, constant V, N = 1,
+    the GQA group-sum identity, integer dot products);
+  * numpy's float16 conversion for the fp16 rounding helper;
+and planted mistakes (a doubled scale, a flipped mask, a dropped GQA sum, a
+missing Delta term) are shown to fail those checks, so the checks have teeth.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "attention_fp64.npz"
+
+
+def _inputs(B, Hq, Hkv, N, D, seed, mult=1.0):
+    g = torch.Generator("cpu").manual_seed(seed)
+    q = (torch.randn((B, Hq, N, D), generator=g) * mult).half()
+    k = (torch.randn((B, Hkv, N, D), generator=g) * mult).half()
+    v = (torch.randn((B, Hkv, N, D), generator=g) * mult).half()
+    do = (torch.randn((B, Hq, N, D), generator=g) * mult).half()
+    return q, k, v, do
+
+
+def _torch_fp64(q, k, v, do, causal, scale=None):
+    Hq, Hkv, N, D = q.shape[1], k.shape[1], q.shape[2], q.shape[3]
+    q64, k64, v64 = (t.double().requires_grad_() for t in (q, k, v))
+    o = torch.nn.functional.scaled_dot_product_attention(
+        q64, k64, v64, is_causal=causal, scale=scale, enable_gqa=Hq != Hkv)
+    dq, dk, dv = torch.autograd.grad(o, (q64, k64, v64), do.double())
+    sc = D ** -0.5 if scale is None else scale
+    with torch.no_grad():
+        s = q64 @ k64.repeat_interleave(Hq // Hkv, 1).transpose(-1, -2) * sc
+        if causal:
+            s = s.masked_fill(torch.ones(N, N, dtype=torch.bool).triu(1), -math.inf)
+        lse2 = torch.logsumexp(s, -1) / math.log(2.0)
+    exact_delta = (o.detach() * do.double()).sum(-1)
+    return {"o": o.detach().numpy(), "lse": lse2.numpy(), "dq": dq.numpy(),
+            "dk": dk.numpy(), "dv": dv.numpy(), "delta": exact_delta.numpy()}
+
+
+def _maxdiff(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+# ---------------------------------------------------------------------------
+# fp16 rounding
+# ---------------------------------------------------------------------------
+def test_round_half_matches_numpy_float16():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal(100_000) * np.logspace(-9, 5.2, 100_000)
+    # exact ties between neighbouring fp16 values, subnormals and the overflow edge
+    halves = np.arange(0, 0x7C00, 7, dtype=np.uint16).view(np.float16).astype(np.float64)
+    nxt = (np.arange(0, 0x7C00, 7, dtype=np.uint16) + 1).view(np.float16).astype(np.float64)
+    ties = (halves + nxt) / 2
+    edge = np.array([65504.0, 65519.999, 65520.0, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 0.0])
+    for arr in (x, -x, ties, -ties, edge, -edge):
+        with np.errstate(over="ignore"):
+            expected = arr.astype(np.float16).astype(np.float64)
+        np.testing.assert_array_equal(oracle.round_half(arr), expected)
+
+
+# ---------------------------------------------------------------------------
+# Forward
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 2, 2, 17, 32), (2, 4, 2, 65, 64), (1, 3, 1, 50, 128),
+                                   (1, 1, 1, 1, 64), (2, 2, 2, 130, 32)])
+def test_forward_matches_torch_fp64(shape, causal):
+    B, Hq, Hkv, N, D = shape
+    q, k, v, do = _inputs(B, Hq, Hkv, N, D, seed=N + D)
+    ref = _torch_fp64(q, k, v, do, causal)
+    o, lse = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    assert _maxdiff(o, ref["o"]) < 1e-12
+    assert _maxdiff(lse, ref["lse"]) < 1e-12
+
+
+def test_forward_custom_scale_matches_torch_fp64():
+    q, k, v, do = _inputs(1, 2, 2, 33, 64, seed=3)
+    for scale in (0.01, 0.3, 2.0):
+        ref = _torch_fp64(q, k, v, do, True, scale)
+        o, lse = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), True, scale)
+        assert _maxdiff(o, ref["o"]) < 1e-12
+        assert _maxdiff(lse, ref["lse"]) < 1e-12
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_online_recurrence_equals_closed_form(causal):
+    """The reference's tiled online softmax is tiling-independent in exact
+    arithmetic: in fp64 it must equal the two-pass closed form for any tiles."""
+    q, k, v, _ = _inputs(2, 2, 2, 301, 64, seed=5)
+    o, lse = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    for bm, bn in ((64, 32), (128, 32), (128, 64), (16, 16)):
+        oo, ll = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal, online=True,
+                            block_m=bm, block_n=bn, round_p=False)
+        assert _maxdiff(oo, o) < 1e-12 and _maxdiff(ll, lse) < 1e-12
+
+
+def test_online_fp16_p_rounding_stays_within_half_ulp_bound():
+    """With P rounded to fp16 for P.V (attention.py:73) each term moves by at
+    most 2^-11 relative, so |O_fp16P - O| <= 2^-11 * max|v| (weights sum to 1)."""
+    q, k, v, _ = _inputs(1, 2, 2, 200, 64, seed=6)
+    o, _ = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), True)
+    oo, _ = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), True, online=True, round_p=True)
+    bound = 2.0 ** -11 * float(np.abs(v.numpy()).max())
+    diff = _maxdiff(oo, o)
+    assert 0 < diff <= bound
+
+
+def test_forward_closed_forms():
+    q, k, v, _ = _inputs(1, 2, 2, 120, 64, seed=7)
+    qn, kn, vn = q.numpy(), k.numpy(), v.numpy()
+    # causal row 0 sees only key 0: O[0] = V[0], LSE2 = s00 / ln 2
+    o, lse = oracle.fwd(qn, kn, vn, True)
+    np.testing.assert_allclose(o[:, :, 0], vn[:, :, 0].astype(np.float64), atol=1e-14)
+    s00 = (qn[:, :, 0].astype(np.float64) * kn[:, :, 0]).sum(-1) / 8.0
+    np.testing.assert_allclose(lse[:, :, 0], s00 / math.log(2.0), atol=1e-12)
+    # Q = 0: uniform weights over the visible keys
+    z = np.zeros_like(qn)
+    o, lse = oracle.fwd(z, kn, vn, True)
+    counts = np.arange(1, 121, dtype=np.float64)
+    np.testing.assert_allclose(o, np.cumsum(vn.astype(np.float64), 2) / counts[:, None], atol=1e-13)
+    np.testing.assert_allclose(lse, np.broadcast_to(np.log2(counts), lse.shape), atol=1e-13)
+    o, lse = oracle.fwd(z, kn, vn, False)
+    np.testing.assert_allclose(lse, np.log2(120.0), atol=1e-13)
+    # N = 1: O = V
+    o, _ = oracle.fwd(qn[:, :, :1], kn[:, :, :1], vn[:, :, :1], False)
+    np.testing.assert_allclose(o, vn[:, :, :1].astype(np.float64), atol=1e-15)
+
+
+# ---------------------------------------------------------------------------
+# Delta and backward
+# ---------------------------------------------------------------------------
+def test_preprocess_exact_on_integers():
+    rng = np.random.default_rng(1)
+    o = rng.integers(-8, 8, size=(2, 3, 5, 32)).astype(np.float64)
+    do = rng.integers(-8, 8, size=(2, 3, 5, 32)).astype(np.float64)
+    np.testing.assert_array_equal(oracle.bwd_preprocess(o, do), (o * do).sum(-1))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 2, 2, 17, 32), (2, 4, 2, 65, 64), (1, 4, 1, 40, 128),
+                                   (1, 6, 3, 33, 64)])
+def test_backward_matches_torch_autograd_fp64(shape, causal):
+    B, Hq, Hkv, N, D = shape
+    q, k, v, do = _inputs(B, Hq, Hkv, N, D, seed=2 * N + D)
+    ref = _torch_fp64(q, k, v, do, causal)
+    _, lse = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    dq, dk, dv = oracle.bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), lse, ref["delta"], causal)
+    assert _maxdiff(dq, ref["dq"]) < 1e-12
+    assert _maxdiff(dk, ref["dk"]) < 1e-12
+    assert _maxdiff(dv, ref["dv"]) < 1e-12
+
+
+def test_backward_closed_forms():
+    q, k, v, do = _inputs(1, 2, 2, 90, 64, seed=8)
+    qn, kn, vn, don = q.numpy(), k.numpy(), v.numpy(), do.numpy()
+    # constant V rows: dP_ij = dO_i . v0 = Delta_i so dS = 0 -> dQ = dK = 0
+    vc = np.broadcast_to(vn[:, :, :1], vn.shape).copy()
+    r = oracle.attention(qn, kn, vc, don, True, o16=np.broadcast_to(vc, qn.shape))
+    assert np.max(np.abs(r["dq"])) < 1e-12 and np.max(np.abs(r["dk"])) < 1e-12
+    # dV = P^T dO: with Q = 0 and causal, dV_j = sum_{i>=j} dO_i / (i+1)
+    z = np.zeros_like(qn)
+    r = oracle.attention(z, kn, vn, don, True)
+    w = 1.0 / np.arange(1, 91, dtype=np.float64)
+    expected = np.flip(np.cumsum(np.flip(don.astype(np.float64) * w[:, None], 2), 2), 2)
+    np.testing.assert_allclose(r["dv"], expected, atol=1e-12)
+    # N = 1: P = 1, dS = dO.v - Delta = 0 when Delta uses the exact O (= V)
+    r = oracle.attention(qn[:, :, :1], kn[:, :, :1], vn[:, :, :1], don[:, :, :1], False,
+                         o16=vn[:, :, :1])
+    assert np.max(np.abs(r["dq"])) < 1e-15 and np.max(np.abs(r["dk"])) < 1e-15
+    np.testing.assert_allclose(r["dv"], don[:, :, :1].astype(np.float64), atol=1e-15)
+
+
+def test_gqa_group_sum_identity():
+    """dK/dV of a shared K/V head equal the sum over its query heads of the
+    MHA gradients computed with K/V repeated per query head."""
+    q, k, v, do = _inputs(1, 6, 2, 70, 32, seed=9)
+    r = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), True)
+    kr, vr = k.repeat_interleave(3, 1), v.repeat_interleave(3, 1)
+    m = oracle.attention(q.numpy(), kr.numpy(), vr.numpy(), do.numpy(), True)
+    for name in ("o", "lse", "dq"):
+        assert _maxdiff(r[name], m[name]) < 1e-12
+    assert _maxdiff(r["dk"], m["dk"].reshape(1, 2, 3, 70, 32).sum(2)) < 1e-12
+    assert _maxdiff(r["dv"], m["dv"].reshape(1, 2, 3, 70, 32).sum(2)) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# Golden fixtures (torch fp64, committed)
+# ---------------------------------------------------------------------------
+def _golden_cases():
+    data = np.load(GOLDEN)
+    names = sorted({k.split("/")[0] for k in data.files if "/" in k})
+    return data, names
+
+
+def test_golden_fixtures_match_oracle():
+    data, names = _golden_cases()
+    assert len(names) >= 14
+    for name in names:
+        g = {k.split("/")[1]: data[k] for k in data.files if k.startswith(name + "/")}
+        B, Hq, Hkv, N, D, causal = (int(x) for x in g["meta"])
+        assert g["q"].dtype == np.float16
+        o, lse = oracle.fwd(g["q"], g["k"], g["v"], bool(causal))
+        assert _maxdiff(o, g["o"]) < 1e-6, name
+        assert _maxdiff(lse, g["lse2"]) < 1e-12, name
+        if "do" not in g:
+            continue
+        np.testing.assert_array_equal(oracle.round_half(g["o16"]), g["o16"].astype(np.float64))
+        delta16 = oracle.bwd_preprocess(g["o16"], g["do"])
+        assert _maxdiff(delta16, g["delta"]) < 1e-12, name
+        exact_delta = oracle.bwd_preprocess(o, g["do"])
+        dq, dk, dv = oracle.bwd(g["q"], g["k"], g["v"], g["do"], lse, exact_delta, bool(causal))
+        for key, val in (("dq", dq), ("dk", dk), ("dv", dv)):
+            scale = max(1.0, float(np.abs(g[key]).max()))
+            assert _maxdiff(val, g[key]) < 1e-6 * scale, f"{name} {key}"
+
+
+def test_golden_config1_cpu_fallback_is_close_to_fp64():
+    """Configuration 1 runs the reference's CPU fallback (fp16 torch SDPA); its
+    fp16 output agrees with the fp64 oracle to fp16 accuracy."""
+    data = np.load(GOLDEN)
+    name = "config1_b1_h4_n257_d64_bidir"
+    o, _ = oracle.fwd(data[name + "/q"], data[name + "/k"], data[name + "/v"], False)
+    assert _maxdiff(o, data[name + "/o_cpu_fp16_sdpa"]) < 2e-3
+
+
+# ---------------------------------------------------------------------------
+# Planted mistakes: each variant of the oracle must fail the checks above.
+# ---------------------------------------------------------------------------
+def test_planted_mistakes_are_caught():
+    q, k, v, do = _inputs(1, 4, 2, 48, 64, seed=10)
+    ref = _torch_fp64(q, k, v, do, True)
+    qn, kn, vn, don = q.numpy(), k.numpy(), v.numpy(), do.numpy()
+    # doubled softmax scale
+    o, _ = oracle.fwd(qn, kn, vn, True, scale=2 * 64 ** -0.5)
+    assert _maxdiff(o, ref["o"]) > 1e-3
+    # mask flipped to bidirectional
+    o, _ = oracle.fwd(qn, kn, vn, False)
+    assert _maxdiff(o, ref["o"]) > 1e-3
+    # wrong GQA map (query head h reads K/V head h % Hkv instead of h // group)
+    perm = np.array([0, 2, 1, 3])
+    o, _ = oracle.fwd(qn[:, perm], kn, vn, True)
+    assert _maxdiff(o[:, np.argsort(perm)], ref["o"]) > 1e-3
+    # Delta term dropped from dS
+    _, lse = oracle.fwd(qn, kn, vn, True)
+    dq, dk, _ = oracle.bwd(qn, kn, vn, don, lse, np.zeros_like(ref["delta"]), True)
+    assert _maxdiff(dq, ref["dq"]) > 1e-3 and _maxdiff(dk, ref["dk"]) > 1e-3
+    # natural-log LSE fed where the base-2 LSE is expected
+    dq, _, dv = oracle.bwd(qn, kn, vn, don, lse * math.log(2.0), ref["delta"], True)
+    assert _maxdiff(dv, ref["dv"]) > 1e-3

@@ -1,0 +1,271 @@
+// fa_capi.hip — extern "C" entry points of libfa_gfx950.so (declared in
+// include/fa_gfx950.h). Argument checks happen here, before any HIP call, so
+// an unsupported request never reaches the device; a rejected call returns a
+// negative FA_ERR_* code and records a message for fa_last_error().
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <initializer_list>
+
+#include "../../include/fa_gfx950.h"
+#include "fa_kernels.hpp"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_result(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_last_error[0] = '\0';
+    return FA_OK;
+  }
+  return fail((int)e, "%s: %s (hipError %d)", what, hipGetErrorString(e), (int)e);
+}
+
+// Process-wide tiling choice per (kernel, D index, causal); -1 = table default.
+int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
+                                       {{-1, -1}, {-1, -1}, {-1, -1}},
+                                       {{-1, -1}, {-1, -1}, {-1, -1}}};
+
+// Static tiling table (replaces the Triton autotuner). Values are variant
+// indices into the registries of fa_fwd.hip / fa_bwd.hip:
+//   fwd : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 8 waves, 64; 2 = 4 waves, 32
+//   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64
+//   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64
+const int kDefault[fa::kNumKinds][3][2] = {
+    // D=32     D=64     D=128   (each: {bidirectional, causal})
+    {{0, 0}, {0, 0}, {0, 0}},  // fwd
+    {{0, 0}, {0, 0}, {1, 1}},  // dkdv
+    {{0, 0}, {0, 0}, {0, 0}},  // dq
+};
+
+const fa::Variant* registry(int kind, int* count) {
+  switch (kind) {
+    case fa::kFwd:
+      return fa::fwd_variants(count);
+    case fa::kDkdv:
+      return fa::dkdv_variants(count);
+    case fa::kDq:
+      return fa::dq_variants(count);
+    default:
+      *count = 0;
+      return nullptr;
+  }
+}
+
+const fa::Variant* select(int kind, int di, int causal, int* index) {
+  int count = 0;
+  const fa::Variant* vs = registry(kind, &count);
+  if (!vs) return nullptr;
+  int v = g_override[kind][di][causal ? 1 : 0];
+  if (v < 0) v = kDefault[kind][di][causal ? 1 : 0];
+  if (v >= count) return nullptr;
+  if (index) *index = v;
+  return &vs[v];
+}
+
+int check_common(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0)
+    return fail(FA_ERR_BAD_SHAPE, "B, Hq, Hkv and N must be positive (got %lld, %lld, %lld, %lld)",
+                (long long)B, (long long)Hq, (long long)Hkv, (long long)N);
+  if (Hq % Hkv != 0)
+    return fail(FA_ERR_BAD_SHAPE,
+                "the number of query heads (%lld) must be divisible by the number of key/value "
+                "heads (%lld)",
+                (long long)Hq, (long long)Hkv);
+  if (fa::head_dim_index(D) < 0)
+    return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128); got %lld", (long long)D);
+  // Per-head slabs are addressed with 32-bit byte offsets (buffer range check).
+  if (N * D * 2 + 4096 * D * 2 >= ((int64_t)1 << 31))
+    return fail(FA_ERR_TOO_LARGE, "sequence length %lld is too large for head_dim %lld",
+                (long long)N, (long long)D);
+  if (B * Hq >= ((int64_t)1 << 31) / 2)
+    return fail(FA_ERR_TOO_LARGE, "batch * heads (%lld) is too large", (long long)(B * Hq));
+  return FA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_aligned(const char* fn, std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs)
+    if (!aligned16(p))
+      return fail(FA_ERR_MISALIGNED, "%s: tensor pointer %p is not 16-byte aligned", fn, p);
+  return FA_OK;
+}
+
+int check_scale(float scale) {
+  if (!isfinite(scale) || !(scale > 0.f))
+    return fail(FA_ERR_BAD_SCALE, "scale must be finite and > 0 (got %g)", (double)scale);
+  return FA_OK;
+}
+
+fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                     const fa_half_t* dO, const float* lse, const float* delta, int64_t B,
+                     int64_t Hq, int64_t Hkv, int64_t N, float scale) {
+  fa::BwdArgs a;
+  a.q = reinterpret_cast<const fa::half_t*>(q);
+  a.k = reinterpret_cast<const fa::half_t*>(k);
+  a.v = reinterpret_cast<const fa::half_t*>(v);
+  a.dO = reinterpret_cast<const fa::half_t*>(dO);
+  a.lse = lse;
+  a.delta = delta;
+  a.dq = nullptr;
+  a.dk = nullptr;
+  a.dv = nullptr;
+  a.N = (int)N;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.group = (int)(Hq / Hkv);
+  a.BH = (int)(B * Hq);
+  a.BHkv = (int)(B * Hkv);
+  a.num_tiles = 0;
+  a.c = scale * fa::kLog2e;
+  a.scale = scale;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_last_error(void) { return g_last_error; }
+
+int fa_fwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o, float* lse,
+           int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+           void* stream) {
+  if (!q || !k || !v || !o || !lse) return fail(FA_ERR_NULL_POINTER, "fa_fwd: null pointer");
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  if ((rc = check_aligned("fa_fwd", {q, k, v, o, lse}))) return rc;
+  if ((rc = check_scale(scale))) return rc;
+  const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd: no kernel for the selected tiling");
+  fa::FwdArgs a;
+  a.q = reinterpret_cast<const fa::half_t*>(q);
+  a.k = reinterpret_cast<const fa::half_t*>(k);
+  a.v = reinterpret_cast<const fa::half_t*>(v);
+  a.o = reinterpret_cast<fa::half_t*>(o);
+  a.lse = lse;
+  a.N = (int)N;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.group = (int)(Hq / Hkv);
+  a.BH = (int)(B * Hq);
+  a.num_tiles = 0;
+  a.c = scale * fa::kLog2e;
+  auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
+  return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_fwd launch");
+}
+
+int fa_bwd_preprocess(const fa_half_t* o, const fa_half_t* dO, float* delta, int64_t B,
+                      int64_t Hq, int64_t N, int64_t D, void* stream) {
+  if (!o || !dO || !delta) return fail(FA_ERR_NULL_POINTER, "fa_bwd_preprocess: null pointer");
+  int rc = check_common(B, Hq, 1, N, D);
+  if (rc) return rc;
+  if ((rc = check_aligned("fa_bwd_preprocess", {o, dO, delta}))) return rc;
+  return hip_result(fa::launch_preprocess(reinterpret_cast<const fa::half_t*>(o),
+                                          reinterpret_cast<const fa::half_t*>(dO), delta,
+                                          B * Hq * N, (int)D, static_cast<hipStream_t>(stream)),
+                    "fa_bwd_preprocess launch");
+}
+
+int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
+                const float* lse, const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B,
+                int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+                void* stream) {
+  if (!q || !k || !v || !dO || !lse || !delta || !dk || !dv)
+    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dkdv: null pointer");
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  if ((rc = check_aligned("fa_bwd_dkdv", {q, k, v, dO, lse, delta, dk, dv}))) return rc;
+  if ((rc = check_scale(scale))) return rc;
+  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dkdv: no kernel for the selected tiling");
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  a.dk = reinterpret_cast<fa::half_t*>(dk);
+  a.dv = reinterpret_cast<fa::half_t*>(dv);
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
+  return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_bwd_dkdv launch");
+}
+
+int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
+              const float* lse, const float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
+              int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
+  if (!q || !k || !v || !dO || !lse || !delta || !dq)
+    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dq: null pointer");
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  if ((rc = check_aligned("fa_bwd_dq", {q, k, v, dO, lse, delta, dq}))) return rc;
+  if ((rc = check_scale(scale))) return rc;
+  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq: no kernel for the selected tiling");
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  a.dq = reinterpret_cast<fa::half_t*>(dq);
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
+  return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_bwd_dq launch");
+}
+
+int fa_get_tiling(int kernel, int64_t D, int causal, int* out4) {
+  if (!out4) return fail(FA_ERR_NULL_POINTER, "fa_get_tiling: null pointer");
+  const int di = fa::head_dim_index(D);
+  if (di < 0) return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128)");
+  if (kernel < 0 || kernel >= fa::kNumKinds)
+    return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
+  int index = -1;
+  const fa::Variant* var = select(kernel, di, causal, &index);
+  if (!var) return fail(FA_ERR_BAD_TILING, "no tiling for kernel %d", kernel);
+  out4[0] = var->waves;
+  out4[1] = var->rows;
+  out4[2] = var->tile;
+  out4[3] = index;
+  return FA_OK;
+}
+
+int fa_num_tiling_variants(int kernel, int64_t D, int causal) {
+  (void)causal;
+  if (fa::head_dim_index(D) < 0) return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128)");
+  int count = 0;
+  if (!registry(kernel, &count)) return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
+  return count;
+}
+
+int fa_describe_tiling_variant(int kernel, int64_t D, int causal, int variant, int* out4) {
+  (void)causal;
+  if (!out4) return fail(FA_ERR_NULL_POINTER, "fa_describe_tiling_variant: null pointer");
+  if (fa::head_dim_index(D) < 0) return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128)");
+  int count = 0;
+  const fa::Variant* vs = registry(kernel, &count);
+  if (!vs) return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
+  if (variant < 0 || variant >= count)
+    return fail(FA_ERR_BAD_TILING, "variant %d out of range [0, %d)", variant, count);
+  out4[0] = vs[variant].waves;
+  out4[1] = vs[variant].rows;
+  out4[2] = vs[variant].tile;
+  out4[3] = variant;
+  return FA_OK;
+}
+
+int fa_set_tiling(int kernel, int64_t D, int causal, int variant) {
+  const int di = fa::head_dim_index(D);
+  if (di < 0) return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128)");
+  int count = 0;
+  if (!registry(kernel, &count)) return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
+  if (variant >= count)
+    return fail(FA_ERR_BAD_TILING, "variant %d out of range [0, %d)", variant, count);
+  g_override[kernel][di][causal ? 1 : 0] = variant < 0 ? -1 : variant;
+  return FA_OK;
+}
+
+}  // extern "C"

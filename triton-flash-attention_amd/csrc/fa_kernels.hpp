@@ -1,0 +1,78 @@
+// fa_kernels.hpp — argument blocks and launcher registry shared by the
+// kernel translation units and the C ABI (fa_capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 half_t;
+
+// 1 / ln(2): converts natural-log scores to the base-2 domain (attention.py:20).
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Arguments of one forward launch (the values _attn_fwd receives at
+// attention.py:690-718, minus strides: every tensor is contiguous).
+struct FwdArgs {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  half_t* o;
+  float* lse;
+  int N;           // sequence length (queries == keys)
+  int Hq, Hkv;     // query heads, key/value heads
+  int group;       // Hq / Hkv
+  int BH;          // B * Hq
+  int num_tiles;   // filled in by the launcher
+  float c;         // scale * log2(e)
+};
+
+// Arguments of the backward launches (attention.py:736-770).
+struct BwdArgs {
+  const half_t* q;
+  const half_t* k;
+  const half_t* v;
+  const half_t* dO;
+  const float* lse;
+  const float* delta;
+  half_t* dq;
+  half_t* dk;
+  half_t* dv;
+  int N;
+  int Hq, Hkv, group;
+  int BH;          // B * Hq
+  int BHkv;        // B * Hkv
+  int num_tiles;   // filled in by the launcher
+  float c;         // scale * log2(e)
+  float scale;
+};
+
+enum KernelKind { kFwd = 0, kDkdv = 1, kDq = 2, kNumKinds = 3 };
+
+typedef hipError_t (*fwd_launch_fn)(const FwdArgs&, hipStream_t);
+typedef hipError_t (*bwd_launch_fn)(const BwdArgs&, hipStream_t);
+
+// One compiled tiling of a kernel, for every (D, causal).
+// rows = rows owned by a work-group (queries for fwd/dq, keys for dkdv),
+// tile = length of the streamed tile (keys for fwd/dq, queries for dkdv).
+struct Variant {
+  int waves;
+  int rows;
+  int tile;
+  void* fn[3][2];  // [D index: 32, 64, 128][causal]
+};
+
+// Registries defined in the kernel translation units.
+const Variant* fwd_variants(int* count);
+const Variant* dkdv_variants(int* count);
+const Variant* dq_variants(int* count);
+
+hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
+                             int D, hipStream_t stream);
+
+inline int head_dim_index(int64_t D) {
+  return D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : -1;
+}
+
+}  // namespace fa

@@ -1,0 +1,209 @@
+"""Tensor-level calls into libfa_gfx950.so.
+
+PyTorch only provides device memory and the current HIP stream here: each
+function checks layout on the host (the C ABI sees raw pointers), allocates
+its outputs with the caching allocator, and launches one C-ABI entry point on
+``torch.cuda.current_stream(device)``. There is no fallback: if the library
+is missing these functions raise.
+
+Reference launches replaced (triton_flash_attention/attention.py):
+    flash_fwd            -> _attn_fwd[grid]              690-718
+    flash_bwd_preprocess -> _attn_bwd_preprocess[grid]   736-744
+    flash_bwd_dkdv       -> _attn_bwd[grid], phase 1     754-770 (428-505)
+    flash_bwd_dq         -> _attn_bwd[grid], phase 2     754-770 (507-573)
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+class LaunchTimer:
+    """Brackets every kernel launch made through this module with HIP events
+    recorded on the launch stream (torch's current stream), so per-kernel
+    average durations can be read after a timed region:
+
+        with LaunchTimer() as timer:
+            ...                      # any fwd/bwd calls
+        torch.cuda.synchronize()
+        timer.mean_ms("dkdv")
+    """
+
+    _active: "LaunchTimer | None" = None
+
+    def __init__(self) -> None:
+        self.events: dict[str, list[tuple[torch.cuda.Event, torch.cuda.Event]]] = {}
+
+    def __enter__(self) -> "LaunchTimer":
+        LaunchTimer._active = self
+        return self
+
+    def __exit__(self, *exc) -> None:
+        LaunchTimer._active = None
+
+    def _begin(self) -> torch.cuda.Event:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
+    def _end(self, name: str, start: torch.cuda.Event) -> None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.events.setdefault(name, []).append((start, ev))
+
+    def durations_ms(self, name: str) -> list[float]:
+        return [a.elapsed_time(b) for a, b in self.events.get(name, [])]
+
+    def mean_ms(self, name: str) -> float:
+        d = self.durations_ms(name)
+        return sum(d) / len(d) if d else float("nan")
+
+
+def _launch(name: str, fn, *args) -> int:
+    timer = LaunchTimer._active
+    if timer is None:
+        return fn(*args)
+    start = timer._begin()
+    rc = fn(*args)
+    timer._end(name, start)
+    return rc
+
+
+def _require(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor")
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """The kernels move 128-bit vectors: a view whose data pointer is not
+    16-byte aligned is copied into a fresh (aligned) allocation."""
+    return t if t.data_ptr() % 16 == 0 else t.clone(memory_format=torch.contiguous_format)
+
+
+def _qkv_dims(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, int, int, int, int]:
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, v must be 4-D [batch, heads, sequence, head_dim]")
+    B, Hq, N, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != N or k.shape[3] != D:
+        raise ValueError(
+            f"k and v must have shape [{B}, Hkv, {N}, {D}]; got {tuple(k.shape)}, {tuple(v.shape)}"
+        )
+    return B, Hq, k.shape[1], N, D
+
+
+def flash_fwd(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """O [B,Hq,N,D] fp16 and base-2 LSE [B,Hq,N] fp32."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require(t, name, torch.float16, q.device)
+    B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    lib = _lib.load()
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        rc = _launch(
+            "fwd", lib.fa_fwd,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+        )
+    _lib.check(rc)
+    return o, lse
+
+
+def flash_bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
+    """Delta [B,H,N] fp32 = rowsum(O * dO)."""
+    _require(o, "o", torch.float16, o.device)
+    _require(do, "dO", torch.float16, o.device)
+    if do.shape != o.shape or o.ndim != 4:
+        raise ValueError("o and dO must have the same 4-D shape")
+    B, H, N, D = o.shape
+    o, do = _aligned(o), _aligned(do)
+    lib = _lib.load()
+    delta = torch.empty((B, H, N), device=o.device, dtype=torch.float32)
+    with torch.cuda.device(o.device):
+        rc = _launch("preprocess", lib.fa_bwd_preprocess,
+                     o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, H, N, D, _stream(o))
+    _lib.check(rc)
+    return delta
+
+
+def _check_bwd_inputs(q, k, v, do, lse, delta):
+    for name, t in (("q", q), ("k", k), ("v", v), ("dO", do)):
+        _require(t, name, torch.float16, q.device)
+    for name, t in (("lse", lse), ("delta", delta)):
+        _require(t, name, torch.float32, q.device)
+    B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
+    if do.shape != q.shape:
+        raise ValueError("dO must have the shape of q")
+    if lse.shape != (B, Hq, N) or delta.shape != (B, Hq, N):
+        raise ValueError("lse and delta must have shape [B, Hq, N]")
+    return B, Hq, Hkv, N, D
+
+
+def _aligned_all(*tensors):
+    return tuple(_aligned(t) for t in tensors)
+
+
+def flash_bwd_dkdv(
+    q, k, v, do, lse, delta, causal: bool, scale: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """dK, dV [B,Hkv,N,D] fp16 (GQA groups reduced in fp32 in-kernel)."""
+    B, Hq, Hkv, N, D = _check_bwd_inputs(q, k, v, do, lse, delta)
+    q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
+    lib = _lib.load()
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    with torch.cuda.device(q.device):
+        rc = _launch(
+            "dkdv", lib.fa_bwd_dkdv,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
+            delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+        )
+    _lib.check(rc)
+    return dk, dv
+
+
+def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.Tensor:
+    """dQ [B,Hq,N,D] fp16."""
+    B, Hq, Hkv, N, D = _check_bwd_inputs(q, k, v, do, lse, delta)
+    q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
+    lib = _lib.load()
+    dq = torch.empty_like(q)
+    with torch.cuda.device(q.device):
+        rc = _launch(
+            "dq", lib.fa_bwd_dq,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
+            delta.data_ptr(), dq.data_ptr(),
+            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+        )
+    _lib.check(rc)
+    return dq
+
+
+def flash_bwd(
+    q, k, v, o, lse, do, causal: bool, scale: float
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """dQ, dK, dV: preprocess, then the dK/dV and dQ kernels."""
+    delta = flash_bwd_preprocess(o, do)
+    dk, dv = flash_bwd_dkdv(q, k, v, do, lse, delta, causal, scale)
+    dq = flash_bwd_dq(q, k, v, do, lse, delta, causal, scale)
+    return dq, dk, dv

@@ -1,0 +1,290 @@
+"""Public attention API: validation, backend dispatch and the autograd bridge.
+
+This mirrors the host side of the reference (triton_flash_attention/attention.py):
+the same public names, keyword-only signatures, defaults, validation order and
+messages, and the same PyTorch SDPA fallback. What changes is the device side:
+eligible inputs run the hand-written gfx950 HIP kernels of libfa_gfx950.so
+through :mod:`._ops` instead of Triton kernels.
+
+Dispatch rules (first match wins; reference rules at attention.py:629-670):
+  1. cross-attention (N_q != N_kv)          -> torch   (ref 639-642)
+  2. value head size != query head size     -> torch   (ref 643-646)
+  3. not a GPU ("cuda") tensor              -> torch   (ref 647-648)
+  4. dtype is not float16                   -> torch   (ref 653-656)
+  5. head_dim not in (32, 64, 128)          -> torch   (ref 657-661)
+  6. sequence too long for 32-bit offsets   -> torch   (no reference counterpart)
+  7. device is not gfx950                   -> torch   (replaces ref 662-666, SM >= 8)
+  8. libfa_gfx950.so not loadable           -> torch   (replaces ref 649-652, the ROCm
+                                                        reject); see below
+  9. otherwise                              -> "triton" (the custom kernel backend)
+
+The backend keeps the reference's name "triton" so existing call sites
+(``backend="triton"``) run unchanged; it now means "the custom fused kernel".
+On a gfx950 device an eligible input whose kernel library is missing is a
+broken install, not an unsupported input: ``scaled_dot_product_attention``
+raises instead of silently falling back (rule 8), unless ``backend="torch"``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, replace
+from numbers import Real
+from typing import Literal
+
+import torch
+
+from . import _lib, _ops
+
+_SUPPORTED_HEAD_DIMS = (32, 64, 128)
+_SUPPORTED_ARCH = "gfx950"
+# Per-head slabs are addressed with 32-bit byte offsets (include/fa_gfx950.h).
+_MAX_SLAB_BYTES = (1 << 31) - 4096 * 128 * 2
+Backend = Literal["auto", "triton", "torch"]
+
+_REASON_LIBRARY = "the gfx950 kernel library is not available"
+
+
+@dataclass(frozen=True)
+class DispatchDecision:
+    """The selected backend and the concrete reason for the decision."""
+
+    backend: Literal["triton", "torch"]
+    reason: str
+
+
+def _validate_inputs(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    enable_gqa: bool,
+) -> None:
+    """Shape/device/dtype contract of the public API (ref attention.py:584-626)."""
+    for name, tensor in (("query", query), ("key", key), ("value", value)):
+        if not isinstance(tensor, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if tensor.ndim != 4:
+            raise ValueError(
+                f"{name} must have shape (batch, heads, sequence, head_dim); "
+                f"got {tuple(tensor.shape)}"
+            )
+        if 0 in tensor.shape:
+            raise ValueError(f"{name} dimensions must all be greater than zero")
+
+    if not (query.device == key.device == value.device):
+        raise ValueError("query, key, and value must be on the same device")
+    if not (query.dtype == key.dtype == value.dtype):
+        raise ValueError("query, key, and value must have the same dtype")
+    if not (query.shape[0] == key.shape[0] == value.shape[0]):
+        raise ValueError("query, key, and value batch dimensions must match")
+    if key.shape[:3] != value.shape[:3]:
+        raise ValueError(
+            "key and value batch, head, and sequence dimensions must match"
+        )
+    if query.shape[3] != key.shape[3]:
+        raise ValueError("query and key head dimensions must match")
+
+    q_heads, kv_heads = query.shape[1], key.shape[1]
+    if q_heads != kv_heads and not enable_gqa:
+        raise ValueError(
+            "query has a different number of heads from key/value; pass "
+            "enable_gqa=True to use grouped-query attention"
+        )
+    if q_heads % kv_heads:
+        raise ValueError(
+            "the number of query heads must be divisible by the number of "
+            "key/value heads"
+        )
+
+
+_arch_cache: dict[int, str] = {}
+
+
+def _device_arch(device: torch.device) -> str:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    arch = _arch_cache.get(index)
+    if arch is None:
+        props = torch.cuda.get_device_properties(index)
+        arch = getattr(props, "gcnArchName", "") or ""
+        _arch_cache[index] = arch
+    return arch
+
+
+@dataclass(frozen=True)
+class _DispatchFacts:
+    """What the dispatch rules look at, gathered from already-validated inputs."""
+
+    q_len: int
+    kv_len: int
+    head_dim: int
+    value_head_dim: int
+    device_type: str
+    dtype: torch.dtype
+    arch: str | None = None          # filled in only for GPU tensors
+    library_error: str | None = None  # None when libfa_gfx950.so loaded
+
+
+def _decide(facts: _DispatchFacts) -> DispatchDecision:
+    """First-match dispatch rules (ref attention.py:639-670, module docstring)."""
+    if facts.q_len != facts.kv_len:
+        return DispatchDecision(
+            "torch", "the custom kernel currently specializes in self-attention"
+        )
+    if facts.value_head_dim != facts.head_dim:
+        return DispatchDecision(
+            "torch", "the custom kernel requires equal query/key and value head sizes"
+        )
+    if facts.device_type != "cuda":
+        return DispatchDecision("torch", "the Triton kernel requires a CUDA tensor")
+    if facts.dtype != torch.float16:
+        return DispatchDecision(
+            "torch", "the custom mixed-precision path currently supports float16"
+        )
+    if facts.head_dim not in _SUPPORTED_HEAD_DIMS:
+        supported = ", ".join(str(dim) for dim in _SUPPORTED_HEAD_DIMS)
+        return DispatchDecision(
+            "torch", f"head_dim must be one of ({supported}) for the Triton path"
+        )
+    if facts.q_len * facts.head_dim * 2 > _MAX_SLAB_BYTES:
+        return DispatchDecision(
+            "torch", "the sequence is too long for the 32-bit addressed gfx950 kernel"
+        )
+    arch = facts.arch or ""
+    if not arch.startswith(_SUPPORTED_ARCH):
+        return DispatchDecision(
+            "torch",
+            "the tuned kernel requires an AMD Instinct MI355X (gfx950) GPU; "
+            f"found {arch or 'an unknown device'}",
+        )
+    if facts.library_error is not None:
+        return DispatchDecision("torch", f"{_REASON_LIBRARY}: {facts.library_error}")
+    return DispatchDecision(
+        "triton",
+        "gfx950 float16 self-attention with a supported head dimension",
+    )
+
+
+def explain_dispatch(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    enable_gqa: bool = False,
+) -> DispatchDecision:
+    """Explain whether the custom gfx950 kernel can serve these inputs."""
+    _validate_inputs(query, key, value, enable_gqa=enable_gqa)
+    facts = _DispatchFacts(
+        q_len=query.shape[2],
+        kv_len=key.shape[2],
+        head_dim=query.shape[3],
+        value_head_dim=value.shape[3],
+        device_type=query.device.type,
+        dtype=query.dtype,
+    )
+    if facts.device_type == "cuda":
+        ok, why = _lib.available()
+        facts = replace(facts, arch=_device_arch(query.device),
+                        library_error=None if ok else why)
+    return _decide(facts)
+
+
+class TritonAttention(torch.autograd.Function):
+    """Low-level autograd bridge for the custom forward and backward kernels.
+
+    Same contract as the reference class (attention.py:673-771):
+    ``apply(query, key, value, causal, softmax_scale) -> output`` on contiguous
+    fp16 [B, H, N, D] tensors; backward returns ``(dQ, dK, dV, None, None)``.
+    """
+
+    @staticmethod
+    def forward(ctx, query, key, value, causal, softmax_scale):
+        output, lse = _ops.flash_fwd(query, key, value, bool(causal), float(softmax_scale))
+        ctx.save_for_backward(query, key, value, output, lse)
+        ctx.softmax_scale = float(softmax_scale)
+        ctx.causal = bool(causal)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        query, key, value, output, lse = ctx.saved_tensors
+        grad_output = grad_output.contiguous()
+        grad_query, grad_key, grad_value = _ops.flash_bwd(
+            query, key, value, output, lse, grad_output, ctx.causal, ctx.softmax_scale
+        )
+        return grad_query, grad_key, grad_value, None, None
+
+
+def _torch_sdpa(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    is_causal: bool,
+    scale: float | None,
+    enable_gqa: bool,
+) -> torch.Tensor:
+    """The reference's fallback (attention.py:774-786), unchanged in meaning."""
+    kwargs = {"is_causal": is_causal, "scale": scale}
+    if enable_gqa:
+        kwargs["enable_gqa"] = True
+    return torch.nn.functional.scaled_dot_product_attention(query, key, value, **kwargs)
+
+
+def scaled_dot_product_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    is_causal: bool = False,
+    scale: float | None = None,
+    enable_gqa: bool = False,
+    backend: Backend = "auto",
+) -> torch.Tensor:
+    """Compute scaled dot-product attention with safe backend selection.
+
+    The custom gfx950 path supports forward/backward, causal and bidirectional
+    attention, arbitrary positive sequence lengths, and GQA, for float16
+    self-attention with head_dim 32, 64 or 128. Other inputs fall back to
+    PyTorch when ``backend="auto"``; ``backend="triton"`` requires the custom
+    kernel and raises RuntimeError otherwise; ``backend="torch"`` always uses
+    PyTorch SDPA.
+    """
+    if backend not in ("auto", "triton", "torch"):
+        raise ValueError("backend must be one of: 'auto', 'triton', 'torch'")
+    if not isinstance(is_causal, bool):
+        raise TypeError("is_causal must be a bool")
+    if not isinstance(enable_gqa, bool):
+        raise TypeError("enable_gqa must be a bool")
+    if scale is not None and (
+        not isinstance(scale, Real) or not math.isfinite(float(scale))
+    ):
+        raise ValueError("scale must be a finite real number or None")
+    _validate_inputs(query, key, value, enable_gqa=enable_gqa)
+
+    if backend == "torch":
+        return _torch_sdpa(
+            query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
+        )
+
+    decision = explain_dispatch(query, key, value, enable_gqa=enable_gqa)
+    if decision.backend == "torch":
+        if backend == "triton" or decision.reason.startswith(_REASON_LIBRARY):
+            raise RuntimeError(f"Triton backend is unavailable: {decision.reason}")
+        return _torch_sdpa(
+            query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
+        )
+
+    softmax_scale = float(scale) if scale is not None else query.shape[-1] ** -0.5
+    if not softmax_scale > 0.0:
+        # The kernels fold the scale into a base-2 exponent and require scale > 0.
+        if backend == "triton":
+            raise RuntimeError(
+                "Triton backend is unavailable: the gfx950 kernel requires scale > 0"
+            )
+        return _torch_sdpa(
+            query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
+        )
+    return TritonAttention.apply(
+        query.contiguous(), key.contiguous(), value.contiguous(), is_causal, softmax_scale
+    )
