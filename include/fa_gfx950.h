@@ -103,8 +103,9 @@ int fa_abi_version(void);
  *   out[0] = waves per work-group, out[1] = rows per work-group,
  *   out[2] = streamed tile length (keys for fwd/dq, queries for dkdv),
  *   out[3] = variant index.
- * fa_num_tiling_variants / fa_describe_tiling_variant enumerate the compiled
- * variants for (kernel, D, causal); fa_set_tiling selects one for the
+ * fa_num_tiling_variants / fa_describe_tiling_variant enumerate the
+ * variants of a kernel (describe returns FA_ERR_BAD_TILING for one that is
+ * not compiled for this head_dim); fa_set_tiling selects one for the
  * process (variant < 0 restores the default). Used by tuning sweeps. */
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);
 int fa_num_tiling_variants(int kernel, int64_t D, int causal);

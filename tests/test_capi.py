@@ -109,8 +109,7 @@ def test_tiling_table_is_complete(lib):
         for D in (32, 64, 128):
             for causal in (False, True):
                 t = _lib.get_tiling(kernel, D, causal)
-                variants = _lib.tiling_variants(kernel, D, causal)
-                assert 0 <= t["variant"] < len(variants)
+                variants = {v["variant"]: v for v in _lib.tiling_variants(kernel, D, causal)}
                 assert variants[t["variant"]] == t
                 assert t["rows"] == 32 * t["waves"] and t["tile"] % 32 == 0
     with pytest.raises(_lib.FlashAttentionError):
@@ -121,10 +120,11 @@ def test_tiling_table_is_complete(lib):
 
 def test_tiling_override_round_trip(lib):
     default = _lib.get_tiling(_lib.KERNEL_FWD, 64, True)
-    n = len(_lib.tiling_variants(_lib.KERNEL_FWD, 64, True))
+    n = lib.fa_num_tiling_variants(_lib.KERNEL_FWD, 64, 1)
+    last = _lib.tiling_variants(_lib.KERNEL_FWD, 64, True)[-1]["variant"]
     try:
-        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, n - 1)
-        assert _lib.get_tiling(_lib.KERNEL_FWD, 64, True)["variant"] == n - 1
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, last)
+        assert _lib.get_tiling(_lib.KERNEL_FWD, 64, True)["variant"] == last
         with pytest.raises(_lib.FlashAttentionError):
             _lib.set_tiling(_lib.KERNEL_FWD, 64, True, n)
     finally:

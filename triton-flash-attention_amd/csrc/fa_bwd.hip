@@ -202,7 +202,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const int ntiles = (N - q_begin + QT - 1) / QT;
 
   TileStager<D, QT, T::NT, true> sq, sdo;
-  float lse_reg = 0.f, delta_reg = 0.f;
+  // Threads [0, QT) carry the tile's LSE values, [QT, 2 QT) its Delta values
+  // (Ls and Ds are adjacent in LDS, so both land at Ls[tid]).
+  float aux_reg = 0.f;
+  static_assert(2 * QT <= T::NT, "one LSE/Delta value per thread");
 
   for (int gi = 0; gi < a.group; ++gi) {
     const int head = b * a.Hq + hkv * a.group + gi;
@@ -214,14 +217,16 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
     auto load_tile = [&](int qt0) {
       sq.load(rq, qt0, tid);
       sdo.load(rdo, qt0, tid);
-      if (tid < QT) lse_reg = buf_load_f32(rl, (uint32_t)(qt0 + tid) * 4u);
-      else if (tid < 2 * QT) delta_reg = buf_load_f32(rd, (uint32_t)(qt0 + tid - QT) * 4u);
+      if (tid < 2 * QT) {
+        const bool is_lse = tid < QT;
+        const int row = qt0 + (is_lse ? tid : tid - QT);
+        aux_reg = buf_load_f32(is_lse ? rl : rd, (uint32_t)row * 4u);
+      }
     };
     auto store_tile = [&]() {
       sq.store(Qs, Qt, tid);
       sdo.store(dOs, dOt, tid);
-      if (tid < QT) Ls[tid] = lse_reg;
-      else if (tid < 2 * QT) Ds[tid - QT] = delta_reg;
+      if (tid < 2 * QT) Ls[tid] = aux_reg;
     };
 
     if (gi > 0) __syncthreads();  // previous head's last tile fully consumed

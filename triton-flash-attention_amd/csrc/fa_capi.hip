@@ -39,12 +39,13 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 
 // Static tiling table (replaces the Triton autotuner). Values are variant
 // indices into the registries of fa_fwd.hip / fa_bwd.hip:
-//   fwd : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 8 waves, 64; 2 = 4 waves, 32
+//   fwd : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 8 waves, 64; 2 = 4 waves, 32;
+//         3 = 2 waves, 64; 4 = 4 waves, 128 (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
-    {{0, 0}, {0, 0}, {0, 0}},  // fwd
+    {{0, 0}, {2, 2}, {2, 2}},  // fwd
     {{0, 0}, {0, 0}, {1, 1}},  // dkdv
     {{0, 0}, {0, 0}, {0, 0}},  // dq
 };
@@ -63,13 +64,16 @@ const fa::Variant* registry(int kind, int* count) {
   }
 }
 
+// A variant is usable for (D, causal) when it was compiled for that head_dim.
+bool usable(const fa::Variant& v, int di, int causal) { return v.fn[di][causal ? 1 : 0] != nullptr; }
+
 const fa::Variant* select(int kind, int di, int causal, int* index) {
   int count = 0;
   const fa::Variant* vs = registry(kind, &count);
   if (!vs) return nullptr;
   int v = g_override[kind][di][causal ? 1 : 0];
   if (v < 0) v = kDefault[kind][di][causal ? 1 : 0];
-  if (v >= count) return nullptr;
+  if (v >= count || !usable(vs[v], di, causal)) return nullptr;
   if (index) *index = v;
   return &vs[v];
 }
@@ -242,14 +246,17 @@ int fa_num_tiling_variants(int kernel, int64_t D, int causal) {
 }
 
 int fa_describe_tiling_variant(int kernel, int64_t D, int causal, int variant, int* out4) {
-  (void)causal;
   if (!out4) return fail(FA_ERR_NULL_POINTER, "fa_describe_tiling_variant: null pointer");
-  if (fa::head_dim_index(D) < 0) return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128)");
+  const int di = fa::head_dim_index(D);
+  if (di < 0) return fail(FA_ERR_HEAD_DIM, "head_dim must be one of (32, 64, 128)");
   int count = 0;
   const fa::Variant* vs = registry(kernel, &count);
   if (!vs) return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
   if (variant < 0 || variant >= count)
     return fail(FA_ERR_BAD_TILING, "variant %d out of range [0, %d)", variant, count);
+  if (!usable(vs[variant], di, causal))
+    return fail(FA_ERR_BAD_TILING, "variant %d is not compiled for head_dim %lld", variant,
+                (long long)D);
   out4[0] = vs[variant].waves;
   out4[1] = vs[variant].rows;
   out4[2] = vs[variant].tile;
@@ -264,6 +271,9 @@ int fa_set_tiling(int kernel, int64_t D, int causal, int variant) {
   if (!registry(kernel, &count)) return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
   if (variant >= count)
     return fail(FA_ERR_BAD_TILING, "variant %d out of range [0, %d)", variant, count);
+  if (variant >= 0 && !usable(registry(kernel, &count)[variant], di, causal))
+    return fail(FA_ERR_BAD_TILING, "variant %d is not compiled for head_dim %lld", variant,
+                (long long)D);
   g_override[kernel][di][causal ? 1 : 0] = variant < 0 ? -1 : variant;
   return FA_OK;
 }

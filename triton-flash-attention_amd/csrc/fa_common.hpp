@@ -77,6 +77,40 @@ __device__ __forceinline__ float swap_halves(float x) {
   return __shfl_xor(x, 32, 64);
 }
 
+// x[l] and x[l ^ 32] via v_permlane32_swap (VALU only, no LDS round trip).
+// The swap exchanges the upper half of its first operand with the lower half
+// of its second; applied to two copies of x the results are {x[l], x[l^32]}
+// in some order per lane, so any symmetric combination is the half-pair
+// reduction. Written as assembly because the compiler folds the two results
+// of the builtin when both inputs are the same value; the s_nop pairs cover
+// the VALU-write -> permlane-read and permlane-write -> VALU-read hazards.
+__device__ __forceinline__ void halves_pair(float x, float& a, float& b) {
+  a = x;
+  asm volatile(
+      "v_mov_b32 %1, %0\n\t"
+      "s_nop 1\n\t"
+      "v_permlane32_swap_b32 %0, %1\n\t"
+      "s_nop 1"
+      : "+v"(a), "=&v"(b));
+}
+__device__ __forceinline__ float halves_max(float x) {
+  float a, b;
+  halves_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  float a, b;
+  halves_pair(x, a, b);
+  return a + b;
+}
+
+// Wait for all of this wave's outstanding vector-memory loads, visibly to the
+// compiler (so it stops tracking them; asm waits are invisible to it).
+__device__ __forceinline__ void wait_all_vm() {
+  // vmcnt = 0 (bits 3:0 and 15:14), expcnt = 7 and lgkmcnt = 15 (no wait).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
 __device__ __forceinline__ half8 to_half8(const float* p) {
   half8 h;
 #pragma unroll
@@ -101,6 +135,200 @@ __device__ __forceinline__ u32x2 pack4_half(float a, float b, float c, float d) 
   h[3] = (half_t)d;
   return __builtin_bit_cast(u32x2, h);
 }
+
+// ---------------------------------------------------------------------------
+// LDS tiles: [rows][D] fp16, row-major, no padding, with the 16-byte chunks of
+// each row XOR-permuted. The permutation is chosen per head_dim so that the
+// three access patterns the kernels use are free of LDS bank conflicts
+// (64 banks x 4 bytes):
+//   * staging writes: 16 consecutive lanes write consecutive 16-byte chunks
+//     of consecutive rows;
+//   * row reads (ds_read_b128): 16 lanes read one logical chunk of 16
+//     consecutive rows (any order inside the 16);
+//   * transposed reads (ds_read_b64_tr_b16): 32 lanes read 4 consecutive rows
+//     (first row a multiple of 4) x 32 consecutive bytes.
+// D=32  (64 B rows):  chunk c of row r at c ^ ((r >> 2) & 3)
+// D=64  (128 B rows): chunk c of row r at c ^ bitrev3((r >> 1) & 7)
+// D=128 (256 B rows): chunk c of row r at c ^ bitrev4(r & 15)
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ int swz_chunk(int row, int c) {
+  static_assert(D == 32 || D == 64 || D == 128, "head_dim");
+  if constexpr (D == 32) {
+    return c ^ ((row >> 2) & 3);
+  } else if constexpr (D == 64) {
+    const int u = (row >> 1) & 7;
+    return c ^ (((u & 1) << 2) | (u & 2) | (u >> 2));
+  } else {
+    const int u = row & 15;
+    return c ^ (((u & 1) << 3) | ((u & 2) << 1) | ((u & 4) >> 1) | (u >> 3));
+  }
+}
+// Offset (in halves) of the 8 halves [8c, 8c+8) of row `row`.
+template <int D>
+__device__ __forceinline__ int swz_offset(int row, int c) {
+  return row * D + 8 * swz_chunk<D>(row, c);
+}
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
+// MFMA operand whose k-axis runs DOWN the rows of an LDS tile:
+//   value e (0..7) of lane l = tile[k0 + 8*(l/32) + e][m0 + (l % 32)],
+// i.e. the A operand of X with X[m][k] = tile[k][m] (or the B operand with
+// n in place of m). Two ds_read_b64_tr_b16: inside each 16-lane group, source
+// lane 4r+q addresses row k0 + 8g + r (+4), columns m0 + 16*(group&1) + 4q..+3,
+// and lane i receives rows +0..3 of column m0 + 16*(group&1) + i.
+template <int D>
+__device__ __forceinline__ half8 read_tr(const half_t* tile, int k0, int m0, int lane) {
+  const int grp = lane >> 4;
+  const int i = lane & 15;
+  const int g = lane >> 5;
+  const int r = i >> 2, q = i & 3;
+  const int col = m0 + 16 * (grp & 1) + 4 * q;  // multiple of 4
+  const int c = col >> 3, sub = col & 7;        // chunk, 0 or 4 inside it
+  const int row0 = k0 + 8 * g + r;
+  const int row1 = row0 + 4;
+  const half_t* p0 = tile + row0 * D + 8 * swz_chunk<D>(row0, c) + sub;
+  const half_t* p1 = tile + row1 * D + 8 * swz_chunk<D>(row1, c) + sub;
+  const half4 lo =
+      __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p0)));
+  const half4 hi =
+      __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p1)));
+  half8 out;
+  out[0] = lo[0];
+  out[1] = lo[1];
+  out[2] = lo[2];
+  out[3] = lo[3];
+  out[4] = hi[0];
+  out[5] = hi[1];
+  out[6] = hi[2];
+  out[7] = hi[3];
+  return out;
+}
+
+// MFMA operand whose k-axis runs ALONG a row: value e of lane l =
+// tile[row][k0 + 8*(l/32) + e] with `row` chosen by the caller.
+template <int D>
+__device__ __forceinline__ half8 read_row(const half_t* tile, int row, int k0, int lane) {
+  const int c = (k0 >> 3) + (lane >> 5);
+  return *reinterpret_cast<const half8*>(tile + swz_offset<D>(row, c));
+}
+
+// Global -> registers -> LDS staging of an R x D tile (16-byte chunks;
+// consecutive threads take consecutive chunks of a row, so global reads
+// coalesce and LDS writes are conflict-free).
+template <int D, int R, int NT>
+struct Stager {
+  static constexpr int DC = D / 8;
+  static constexpr int CHUNKS = R * DC;
+  static constexpr int PER_T = (CHUNKS + NT - 1) / NT;
+  u32x4 reg[PER_T];
+
+  __device__ __forceinline__ void load(rsrc_t r, int row0, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int ci = tid + i * NT;
+      if (CHUNKS % NT == 0 || ci < CHUNKS) {
+        const int row = ci / DC, c = ci - row * DC;
+        reg[i] = buf_load_b128(r, (uint32_t)((row0 + row) * D + 8 * c) * 2u);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(half_t* tile, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int ci = tid + i * NT;
+      if (CHUNKS % NT == 0 || ci < CHUNKS) {
+        const int row = ci / DC, c = ci - row * DC;
+        *reinterpret_cast<u32x4*>(tile + swz_offset<D>(row, c)) = reg[i];
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Global -> LDS direct (DMA) staging with buffer_load_dwordx4 ... lds.
+// One wave instruction writes 1 KiB of LDS contiguously (lane l at M0 + 16 l),
+// so each lane picks the global chunk that the swizzled layout keeps at its
+// LDS slot. No VGPRs and no LDS write instructions are spent on staging.
+//
+// The load is issued through inline assembly on purpose: the compiler's own
+// wait insertion treats every LDS read after an LDS-DMA as dependent on it and
+// would drain all outstanding loads (vmcnt(0)), which defeats a multi-tile
+// prefetch ring. Completion is instead tracked explicitly: the issuing wave
+// waits with vmcnt(n) (loads retire in order), then a work-group barrier
+// publishes the tile (wait_vm_and_barrier).
+// ---------------------------------------------------------------------------
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor as four SGPR words (for the inline-assembly loads).
+__device__ __forceinline__ int4v make_rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  int4v r;
+  r[0] = (int)(uint32_t)p;
+  r[1] = (int)(uint32_t)(p >> 32);  // stride 0
+  r[2] = (int)bytes;
+  r[3] = kRsrcWord3;
+  return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p);
+}
+
+// 16 bytes per lane from byte offset `voff` of the buffer to LDS[m0 + 16 lane].
+// M0 is reserved by the compiler, so the block restores it before returning.
+__device__ __forceinline__ void dma_b128(int4v rsrc, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(rsrc), "s"(lds_base)
+      : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are in flight,
+// then synchronise the work-group. Both are opaque to the compiler (memory
+// clobber), so no LDS access moves across them.
+template <int N>
+__device__ __forceinline__ void wait_vm_and_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+template <int D, int R, int NW>
+struct DmaStager {
+  static constexpr int BYTES = R * D * 2;
+  static constexpr int INSTR = BYTES / 1024;  // wave instructions per tile
+  static constexpr int PER_WAVE = INSTR / NW;
+  static_assert(BYTES % 1024 == 0, "tile must be a multiple of 1 KiB");
+  static_assert(INSTR % NW == 0, "tile instructions must split evenly over the waves");
+
+  // Per-lane byte offsets inside the tile's global rows (loop-invariant).
+  uint32_t voff[PER_WAVE];
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int byte = (wave * PER_WAVE + i) * 1024 + lane * 16;
+      const int row = byte / (D * 2);
+      const int pc = (byte % (D * 2)) / 16;
+      const int c = swz_chunk<D>(row, pc);  // XOR swizzle is an involution
+      voff[i] = (uint32_t)(row * D + 8 * c) * 2u;
+    }
+  }
+  // Tile rows [row0, row0 + R) of the buffer -> LDS tile at `tile`.
+  __device__ __forceinline__ void issue(int4v rsrc, int row0, const half_t* tile, int wave) const {
+    const uint32_t base = lds_addr(tile) + (uint32_t)(wave * PER_WAVE) * 1024u;
+    const uint32_t roff = (uint32_t)row0 * D * 2u;
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) dma_b128(rsrc, roff + voff[i], base + 1024u * i);
+  }
+};
 
 // Work-group order: tile-major, head-minor. With B*H a multiple of 8 every
 // tile of head h lands on XCD (h % 8) (work-groups are dealt to the 8 XCDs

@@ -24,6 +24,8 @@ SOURCES = ("fa_fwd.hip", "fa_bwd.hip", "fa_capi.hip")
 HEADERS = ("fa_common.hpp", "fa_kernels.hpp")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators live in ordinary VGPRs, so the
+#   per-row rescales of the accumulators need no AGPR<->VGPR copies.
 HIPCC_FLAGS = (
     "--offload-arch=gfx950",
     "-O3",
@@ -34,6 +36,8 @@ HIPCC_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 )
 
 

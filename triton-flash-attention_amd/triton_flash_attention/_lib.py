@@ -151,7 +151,10 @@ def tiling_variants(kernel: int, head_dim: int, causal: bool) -> list[dict[str, 
     result = []
     for index in range(count):
         out = (ctypes.c_int * 4)()
-        check(lib.fa_describe_tiling_variant(kernel, head_dim, int(causal), index, out))
+        rc = lib.fa_describe_tiling_variant(kernel, head_dim, int(causal), index, out)
+        if rc == FA_ERR_BAD_TILING:
+            continue  # not compiled for this head_dim
+        check(rc)
         result.append({"waves": out[0], "rows": out[1], "tile": out[2], "variant": out[3]})
     return result
 
