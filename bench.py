@@ -127,6 +127,10 @@ def main(argv=None) -> int:
                     help="c2 is the metric's configuration; the others are for exploration")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU-work budget of the CPU baseline (0 disables it)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after timing, copy a device buffer of this many MiB once (a "
+                         "plain copy of known size that calibrates rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters in the same run)")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -242,6 +246,15 @@ def main(argv=None) -> int:
                          "(Triton path, RTX 5050 Laptop GPU, README.md:159)",
         "device": torch.cuda.get_device_name(),
     }
+
+    if args.calibrate_copy_mib > 0:
+        src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        record["calibration_copy_bytes"] = args.calibrate_copy_mib << 20
+        del src, dst
 
     if args.cpu_seconds > 0:
         median_s, threads, reps = cpu_baseline(cpu_inputs, causal, args.cpu_seconds)

@@ -23,6 +23,8 @@
 //   * every MFMA result layout is chosen so that the next MFMA consumes the
 //     lane's own values (row_perm on the LDS reads), and results are written
 //     as 8-byte runs along the head dimension.
+#include <type_traits>
+
 #include "fa_common.hpp"
 #include "fa_kernels.hpp"
 
@@ -77,85 +79,51 @@ hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, in
   return hipGetLastError();
 }
 
-// --------------------------------------------------------------------------
-// Staging of a [R x D] fp16 tile into LDS, both row-major (stride D+8) and,
-// optionally, transposed (d-major, stride R+8). Each thread moves
-// (row pair, 16-byte chunk) units; the transposition packs the two rows'
-// halves pairwise into dwords.
-// --------------------------------------------------------------------------
-template <int D, int R, int NT, bool TRANSPOSE>
-struct TileStager {
-  static constexpr int DC = D / 8;
-  static constexpr int RS = D + 8;
-  static constexpr int TS = R + 8;
-  static constexpr int UNITS = (R / 2) * DC;
-  static constexpr int PER_T = (UNITS + NT - 1) / NT;
-  u32x4 reg[PER_T][2];
-
-  __device__ __forceinline__ void load(rsrc_t r, int row0, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (UNITS % NT == 0 || u < UNITS) {
-        const int p = u / DC, cc = u - p * DC;
-        reg[i][0] = buf_load_b128(r, (uint32_t)((row0 + 2 * p) * D + 8 * cc) * 2u);
-        reg[i][1] = buf_load_b128(r, (uint32_t)((row0 + 2 * p + 1) * D + 8 * cc) * 2u);
-      }
-    }
-  }
-  __device__ __forceinline__ void store(half_t* rowmajor, half_t* transposed, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (UNITS % NT == 0 || u < UNITS) {
-        const int p = u / DC, cc = u - p * DC;
-        *reinterpret_cast<u32x4*>(&rowmajor[(2 * p) * RS + 8 * cc]) = reg[i][0];
-        *reinterpret_cast<u32x4*>(&rowmajor[(2 * p + 1) * RS + 8 * cc]) = reg[i][1];
-        if (TRANSPOSE) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const unsigned r0 = reg[i][0][e], r1 = reg[i][1][e];
-            *reinterpret_cast<unsigned*>(&transposed[(8 * cc + 2 * e) * TS + 2 * p]) =
-                pack_lo(r0, r1);
-            *reinterpret_cast<unsigned*>(&transposed[(8 * cc + 2 * e + 1) * TS + 2 * p]) =
-                pack_hi(r0, r1);
-          }
-        }
-      }
-    }
-  }
-};
+template <int V>
+using ic = std::integral_constant<int, V>;
 
 // --------------------------------------------------------------------------
 // dK / dV
+//
+// Work-group: NW waves x 32 keys (K, V resident in VGPRs as MFMA B operands).
+// Streams (query head of the GQA group, 64-query tile) steps through a
+// 3-slot LDS ring filled by DMA: Q tile, dO tile (row-major, swizzled) and
+// the tile's LSE / Delta values. Per 32-query block:
+//   S = Q K^T, dP = dO V^T                  (row reads, result: lane = key)
+//   P = exp2(S c - LSE), dS = P (dP - Delta)
+//   dV^T += dO^T P, dK^T += Q^T dS          (dO^T / Q^T via transposing reads)
+// S and dP of every block of the tile are issued before the first block's
+// vector work, so matrix and vector work overlap.
 // --------------------------------------------------------------------------
 template <int D, int NW, int QT>
 struct DkdvTile {
   static constexpr int BKV = 32 * NW;  // keys per work-group
   static constexpr int NT = 64 * NW;
-  static constexpr int RS = D + 8;
-  static constexpr int TS = QT + 8;
-  static constexpr int MAT = QT * RS + D * TS;  // one tensor, both layouts
-  static constexpr int LDS_HALVES = 2 * MAT;
-  static constexpr int LDS_BYTES = LDS_HALVES * 2 + 2 * QT * 4;
-  static_assert(QT % 32 == 0, "query tile must be a multiple of 32");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static constexpr int TILE = QT * D;              // halves of the Q (or dO) tile
+  static constexpr int AUX = 128;                  // floats: LSE[64], Delta[64]
+  static constexpr int STAGE = 2 * TILE + 2 * AUX;  // halves per ring slot
+  static constexpr int NSTAGE = 3;
+  static constexpr int AHEAD = NSTAGE - 1;
+  static_assert(QT == 32 || QT == 64, "query tile");
 };
+
+template <int D, int NW, int QT>
+constexpr bool dkdv_tiling_ok() {
+  return (QT * D * 2) % 1024 == 0 && ((QT * D * 2) / 1024) % NW == 0 &&
+         3 * (2 * QT * D + 256) * 2 <= 160 * 1024;
+}
 
 template <int D, bool CAUSAL, int NW, int QT>
 __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   using T = DkdvTile<D, NW, QT>;
-  __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALVES + 4 * QT];
-  half_t* Qs = lds;
-  half_t* Qt = lds + QT * T::RS;
-  half_t* dOs = lds + T::MAT;
-  half_t* dOt = dOs + QT * T::RS;
-  float* Ls = reinterpret_cast<float*>(lds + T::LDS_HALVES);
-  float* Ds = Ls + QT;
+  using Dma = DmaStager<D, QT, NW>;
+  constexpr int NB = QT / 32;                 // 32-query blocks per tile
+  constexpr int IPT = 2 * Dma::PER_WAVE + 1;  // this wave's DMA instructions per step
+  __shared__ __attribute__((aligned(16))) half_t lds[T::NSTAGE * T::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ql = lane & 31;
   const int g = lane >> 5;
 
@@ -166,9 +134,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const int kvh = th.head;
   const int b = kvh / a.Hkv;
   const int hkv = kvh - b * a.Hkv;
+  const int G = a.group;
   const int N = a.N;
   const uint32_t slab = (uint32_t)N * D * 2u;
-  const uint32_t aux = (uint32_t)N * 4u;
+  const uint32_t aux_bytes = (uint32_t)N * 4u;
   const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * N * D, slab);
   const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * N * D, slab);
 
@@ -176,7 +145,8 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const int k0w = k0 + 32 * wave;
   const int krow = k0w + ql;
 
-  // K and V as B-operands (column = key ql, d = 16*kk + 8*g .. +7).
+  // K and V as B-operands (column = key ql, d = 16*kk + 8*g .. +7), completed
+  // before the first DMA.
   half8 kf[D / 16], vf[D / 16];
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
@@ -184,6 +154,64 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
     kf[kk] = __builtin_bit_cast(half8, buf_load_b128(rk, off));
     vf[kk] = __builtin_bit_cast(half8, buf_load_b128(rv, off));
   }
+  wait_all_vm();
+
+  const int q_begin = CAUSAL ? (k0 / QT) * QT : 0;
+  const int ntq = (N - q_begin + QT - 1) / QT;
+  const int nsteps = G * ntq;
+
+  // Step s streams query tile (s % ntq) of query head (s / ntq) of the group.
+  // Steps past the end load harmless data (rows past N read as zeros), so
+  // every step issues the same number of DMA instructions.
+  Dma dma;
+  dma.init(wave, lane);
+  auto issue_step = [&](int st, int slot) {
+    const int gi = min(st / ntq, G - 1);
+    const int qt0 = q_begin + (st - gi * ntq) * QT;
+    const int head = b * a.Hq + hkv * G + gi;
+    half_t* base = lds + slot * T::STAGE;
+    dma.issue(make_rsrc_words(a.q + (int64_t)head * N * D, slab), qt0, base, wave);
+    dma.issue(make_rsrc_words(a.dO + (int64_t)head * N * D, slab), qt0, base + T::TILE, wave);
+    // Even waves fetch LSE[qt0 .. qt0+64), odd waves Delta (duplicates of the
+    // same bytes are harmless); lane l -> float l of the 64-entry table.
+    const bool is_lse = (wave & 1) == 0;
+    const float* src = (is_lse ? a.lse : a.delta) + (int64_t)head * N;
+    dma_b32(make_rsrc_words(src, aux_bytes), (uint32_t)(qt0 + lane) * 4u,
+            lds_addr(base + 2 * T::TILE + (is_lse ? 0 : 2 * 64)));
+  };
+#pragma unroll
+  for (int st = 0; st < T::AHEAD; ++st) issue_step(st, st);
+
+  // Loop-invariant per-lane LDS offsets (halves).
+  int r_off[D / 16];  // row reads: row row_perm(ql), chunk 2*kk + g
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) r_off[kk] = swz_offset<D>(row_perm(ql), 2 * kk + g);
+  int t_off[D / 32][2];  // transposed reads (see read_tr)
+  {
+    const int grp = lane >> 4, i = lane & 15, r = i >> 2, qq = i & 3;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int col = 32 * db + 16 * (grp & 1) + 4 * qq;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 8 * g + r + 4 * h2;
+        t_off[db][h2] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
+      }
+    }
+  }
+  auto tr8 = [&](const half_t* base, int db) {
+    const half4 lo = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][0])));
+    const half4 hi = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][1])));
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
+    return v;
+  };
 
   // dK^T, dV^T accumulators: lane (key ql), rows d = 32*db + 8*(j/4) + 4*g + j%4.
   float16v dk[D / 32], dv[D / 32];
@@ -196,117 +224,101 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
     }
 
   const float c = a.c;
-  const int prow = row_perm(ql);
   const bool wave_live = k0w < N;
-  const int q_begin = CAUSAL ? (k0 / QT) * QT : 0;
-  const int ntiles = (N - q_begin + QT - 1) / QT;
 
-  TileStager<D, QT, T::NT, true> sq, sdo;
-  // Threads [0, QT) carry the tile's LSE values, [QT, 2 QT) its Delta values
-  // (Ls and Ds are adjacent in LDS, so both land at Ls[tid]).
-  float aux_reg = 0.f;
-  static_assert(2 * QT <= T::NT, "one LSE/Delta value per thread");
+  auto step = [&](auto slot_c, int st) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    issue_step(st + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
+    const int gi = st / ntq;
+    const int qt0 = q_begin + (st - gi * ntq) * QT;
+    const half_t* Qs = lds + SLOT * T::STAGE;
+    const half_t* dOs = Qs + T::TILE;
+    const float* Ls = reinterpret_cast<const float*>(Qs + 2 * T::TILE);
+    const float* Ds = Ls + 64;
 
-  for (int gi = 0; gi < a.group; ++gi) {
-    const int head = b * a.Hq + hkv * a.group + gi;
-    const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
-    const rsrc_t rdo = make_rsrc(a.dO + (int64_t)head * N * D, slab);
-    const rsrc_t rl = make_rsrc(a.lse + (int64_t)head * N, aux);
-    const rsrc_t rd = make_rsrc(a.delta + (int64_t)head * N, aux);
-
-    auto load_tile = [&](int qt0) {
-      sq.load(rq, qt0, tid);
-      sdo.load(rdo, qt0, tid);
-      if (tid < 2 * QT) {
-        const bool is_lse = tid < QT;
-        const int row = qt0 + (is_lse ? tid : tid - QT);
-        aux_reg = buf_load_f32(is_lse ? rl : rd, (uint32_t)row * 4u);
-      }
-    };
-    auto store_tile = [&]() {
-      sq.store(Qs, Qt, tid);
-      sdo.store(dOs, dOt, tid);
-      if (tid < 2 * QT) Ls[tid] = aux_reg;
-    };
-
-    if (gi > 0) __syncthreads();  // previous head's last tile fully consumed
-    load_tile(q_begin);
-    store_tile();
-    __syncthreads();
-
-    for (int t = 0; t < ntiles; ++t) {
-      const int qt0 = q_begin + t * QT;
-      const bool more = t + 1 < ntiles;
-      if (more) load_tile(qt0 + QT);
-
+    bool act[NB];
+    float16v s[NB], dp[NB];
 #pragma unroll
-      for (int qb = 0; qb < QT / 32; ++qb) {
-        const int qa = qt0 + 32 * qb;
-        const bool active = wave_live && qa < N && !(CAUSAL && qa + 31 < k0w);
-        if (!active) continue;
-        float16v s, dp;
+    for (int qb = 0; qb < NB; ++qb) {
+      const int qa = qt0 + 32 * qb;
+      act[qb] = wave_live && qa < N && !(CAUSAL && qa + 31 < k0w);
+      if (act[qb]) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          s[j] = 0.f;
-          dp[j] = 0.f;
+          s[qb][j] = 0.f;
+          dp[qb][j] = 0.f;
         }
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
-          const int off = (32 * qb + prow) * T::RS + 16 * kk + 8 * g;
-          s = mfma32(*reinterpret_cast<const half8*>(&Qs[off]), kf[kk], s);
-          dp = mfma32(*reinterpret_cast<const half8*>(&dOs[off]), vf[kk], dp);
+          const int off = 32 * qb * D + r_off[kk];
+          s[qb] = mfma32(*reinterpret_cast<const half8*>(Qs + off), kf[kk], s[qb]);
+          dp[qb] = mfma32(*reinterpret_cast<const half8*>(dOs + off), vf[kk], dp[qb]);
         }
-        // Lane's queries: local 32*qb + 16*h + 8*g + e, e = 0..7 (value j = 8h + e).
-        float lse_v[16], del_v[16];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int base = 32 * qb + 16 * h + 8 * g;
-          const float4v l0 = *reinterpret_cast<const float4v*>(&Ls[base]);
-          const float4v l1 = *reinterpret_cast<const float4v*>(&Ls[base + 4]);
-          const float4v d0 = *reinterpret_cast<const float4v*>(&Ds[base]);
-          const float4v d1 = *reinterpret_cast<const float4v*>(&Ds[base + 4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            lse_v[8 * h + e] = l0[e];
-            lse_v[8 * h + 4 + e] = l1[e];
-            del_v[8 * h + e] = d0[e];
-            del_v[8 * h + 4 + e] = d1[e];
-          }
-        }
-        const bool need_mask = (CAUSAL && qa < k0w + 31) || (qa + 32 > N);
-        float p[16], ds[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float pj = exp2_fast(fmaf(s[j], c, -lse_v[j]));
-          if (need_mask) {
-            const int q = qa + result_row(j, g);
-            if (q >= N || (CAUSAL && q < krow)) pj = 0.f;
-          }
-          p[j] = pj;
-          ds[j] = pj * (dp[j] - del_v[j]);
-        }
-        half8 pa[2], sa[2];
-        pa[0] = to_half8(p);
-        pa[1] = to_half8(p + 8);
-        sa[0] = to_half8(ds);
-        sa[1] = to_half8(ds + 8);
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int db = 0; db < D / 32; ++db) {
-            const int off = (32 * db + ql) * T::TS + 32 * qb + 16 * h + 8 * g;
-            dv[db] = mfma32(*reinterpret_cast<const half8*>(&dOt[off]), pa[h], dv[db]);
-            dk[db] = mfma32(*reinterpret_cast<const half8*>(&Qt[off]), sa[h], dk[db]);
-          }
-      }
-
-      if (more) {
-        __syncthreads();
-        store_tile();
-        __syncthreads();
       }
     }
+#pragma unroll
+    for (int qb = 0; qb < NB; ++qb) {
+      if (!act[qb]) continue;
+      const int qa = qt0 + 32 * qb;
+      // The lane's queries: local 32*qb + 16*h + 8*g + e (value j = 8h + e).
+      float lse_v[16], del_v[16];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int base = 32 * qb + 16 * h + 8 * g;
+        const float4v l0 = *reinterpret_cast<const float4v*>(&Ls[base]);
+        const float4v l1 = *reinterpret_cast<const float4v*>(&Ls[base + 4]);
+        const float4v d0 = *reinterpret_cast<const float4v*>(&Ds[base]);
+        const float4v d1 = *reinterpret_cast<const float4v*>(&Ds[base + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lse_v[8 * h + e] = l0[e];
+          lse_v[8 * h + 4 + e] = l1[e];
+          del_v[8 * h + e] = d0[e];
+          del_v[8 * h + 4 + e] = d1[e];
+        }
+      }
+      // Transposed operands of this block, read ahead of the vector work.
+      half8 dot_f[2][D / 32], qt_f[2][D / 32];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          dot_f[h][db] = tr8(dOs + (32 * qb + 16 * h) * D, db);
+          qt_f[h][db] = tr8(Qs + (32 * qb + 16 * h) * D, db);
+        }
+      const bool need_mask = (CAUSAL && qa < k0w + 31) || (qa + 32 > N);
+      half8 pa[2], sa[2];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float pj = exp2_fast(fmaf(s[qb][j], c, -lse_v[j]));
+        if (need_mask) {
+          const int q = qa + result_row(j, g);
+          if (q >= N || (CAUSAL && q < krow)) pj = 0.f;
+        }
+        pa[j >> 3][j & 7] = (half_t)pj;
+        sa[j >> 3][j & 7] = (half_t)(pj * (dp[qb][j] - del_v[j]));
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          dv[db] = mfma32(dot_f[h][db], pa[h], dv[db]);
+          dk[db] = mfma32(qt_f[h][db], sa[h], dk[db]);
+        }
+    }
+    // Step st+1's tile complete for this wave, then published; slot st is free.
+    wait_vm_and_barrier<(T::AHEAD - 1) * IPT>();
+  };
+
+  wait_vm_and_barrier<(T::AHEAD - 1) * IPT>();  // step 0's tile
+  for (int st = 0; st < nsteps; st += T::NSTAGE) {
+    step(ic<0>{}, st);
+    if (st + 1 >= nsteps) break;
+    step(ic<1>{}, st + 1);
+    if (st + 2 >= nsteps) break;
+    step(ic<2>{}, st + 2);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const float scale = a.scale;
   const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * N * D, slab);
@@ -339,29 +351,42 @@ hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
 
 // --------------------------------------------------------------------------
 // dQ
+//
+// Work-group: NW waves x 32 queries (Q, dO resident in VGPRs as B operands,
+// LSE / Delta one per lane). Streams 64-key tiles (K, V row-major, swizzled)
+// through a 3-slot DMA ring. Per 32-key block:
+//   S^T = K Q^T, dP^T = V dO^T               (row reads, result: lane = query)
+//   P^T = exp2(S^T c - LSE), dS^T = P^T (dP^T - Delta)
+//   dQ^T += K^T dS^T                          (K^T via transposing reads)
 // --------------------------------------------------------------------------
 template <int D, int NW, int KT>
 struct DqTile {
   static constexpr int BQ = 32 * NW;  // queries per work-group
   static constexpr int NT = 64 * NW;
-  static constexpr int RS = D + 8;
-  static constexpr int TS = KT + 8;
-  static constexpr int LDS_HALVES = 2 * KT * RS + D * TS;  // K, V row-major + K^T
+  static constexpr int TILE = KT * D;
+  static constexpr int STAGE = 2 * TILE;  // K tile, V tile
+  static constexpr int NSTAGE = 3;
+  static constexpr int AHEAD = NSTAGE - 1;
   static_assert(KT % 32 == 0, "key tile must be a multiple of 32");
-  static_assert(LDS_HALVES * 2 <= 160 * 1024, "LDS budget");
 };
+
+template <int D, int NW, int KT>
+constexpr bool dq_tiling_ok() {
+  return (KT * D * 2) % 1024 == 0 && ((KT * D * 2) / 1024) % NW == 0 &&
+         3 * (2 * KT * D) * 2 <= 160 * 1024;
+}
 
 template <int D, bool CAUSAL, int NW, int KT>
 __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   using T = DqTile<D, NW, KT>;
-  __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALVES];
-  half_t* Ks = lds;
-  half_t* Kt = lds + KT * T::RS;
-  half_t* Vs = Kt + D * T::TS;
+  using Dma = DmaStager<D, KT, NW>;
+  constexpr int NB = KT / 32;
+  constexpr int IPT = 2 * Dma::PER_WAVE;
+  __shared__ __attribute__((aligned(16))) half_t lds[T::NSTAGE * T::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ql = lane & 31;
   const int g = lane >> 5;
 
@@ -376,10 +401,10 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   const uint32_t aux = (uint32_t)N * 4u;
   const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
   const rsrc_t rdo = make_rsrc(a.dO + (int64_t)head * N * D, slab);
-  const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * N * D, slab);
-  const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * N * D, slab);
   const rsrc_t rl = make_rsrc(a.lse + (int64_t)head * N, aux);
   const rsrc_t rd = make_rsrc(a.delta + (int64_t)head * N, aux);
+  const int4v rk = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
+  const int4v rv = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
 
   const int q0 = qtile * T::BQ;
   const int q0w = q0 + 32 * wave;
@@ -394,6 +419,50 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   }
   const float lse = buf_load_f32(rl, (uint32_t)qrow * 4u);
   const float delta = buf_load_f32(rd, (uint32_t)qrow * 4u);
+  wait_all_vm();
+
+  const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
+  const int ntiles = (kv_end + KT - 1) / KT;
+
+  Dma dma;
+  dma.init(wave, lane);
+  auto issue_tile = [&](int t, int slot) {
+    const half_t* base = lds + slot * T::STAGE;
+    dma.issue(rk, t * KT, base, wave);
+    dma.issue(rv, t * KT, base + T::TILE, wave);
+  };
+#pragma unroll
+  for (int t = 0; t < T::AHEAD; ++t) issue_tile(t, t);
+
+  int r_off[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) r_off[kk] = swz_offset<D>(row_perm(ql), 2 * kk + g);
+  int t_off[D / 32][2];
+  {
+    const int grp = lane >> 4, i = lane & 15, r = i >> 2, qq = i & 3;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int col = 32 * db + 16 * (grp & 1) + 4 * qq;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 8 * g + r + 4 * h2;
+        t_off[db][h2] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
+      }
+    }
+  }
+  auto tr8 = [&](const half_t* base, int db) {
+    const half4 lo = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][0])));
+    const half4 hi = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][1])));
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
+    return v;
+  };
 
   // dQ^T accumulator: lane (query ql), rows d = 32*db + 8*(j/4) + 4*g + j%4.
   float16v dq[D / 32];
@@ -404,72 +473,70 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
 
   const float c = a.c;
   const float nl = -lse;
-  const int prow = row_perm(ql);
-  const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
-  const int ntiles = (kv_end + KT - 1) / KT;
 
-  TileStager<D, KT, T::NT, true> sk;
-  TileStager<D, KT, T::NT, false> sv;
-
-  sk.load(rk, 0, tid);
-  sv.load(rv, 0, tid);
-  sk.store(Ks, Kt, tid);
-  sv.store(Vs, nullptr, tid);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
+  auto step = [&](auto slot_c, int t) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    issue_tile(t + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
     const int kt0 = t * KT;
-    const bool more = t + 1 < ntiles;
-    if (more) {
-      sk.load(rk, kt0 + KT, tid);
-      sv.load(rv, kt0 + KT, tid);
+    const half_t* Ks = lds + SLOT * T::STAGE;
+    const half_t* Vs = Ks + T::TILE;
+    bool act[NB];
+    float16v s[NB], dp[NB];
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) {
+      const int ka = kt0 + 32 * kb;
+      act[kb] = q0w < N && ka < N && !(CAUSAL && ka > q0w + 31);
+      if (act[kb]) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          s[kb][j] = 0.f;
+          dp[kb][j] = 0.f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+          const int off = 32 * kb * D + r_off[kk];
+          s[kb] = mfma32(*reinterpret_cast<const half8*>(Ks + off), qf[kk], s[kb]);
+          dp[kb] = mfma32(*reinterpret_cast<const half8*>(Vs + off), dof[kk], dp[kb]);
+        }
+      }
     }
 #pragma unroll
-    for (int kb = 0; kb < KT / 32; ++kb) {
+    for (int kb = 0; kb < NB; ++kb) {
+      if (!act[kb]) continue;
       const int ka = kt0 + 32 * kb;
-      const bool active = q0w < N && ka < N && !(CAUSAL && ka > q0w + 31);
-      if (!active) continue;
-      float16v s, dp;
+      half8 kt_f[2][D / 32];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        s[j] = 0.f;
-        dp[j] = 0.f;
-      }
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-        const int off = (32 * kb + prow) * T::RS + 16 * kk + 8 * g;
-        s = mfma32(*reinterpret_cast<const half8*>(&Ks[off]), qf[kk], s);
-        dp = mfma32(*reinterpret_cast<const half8*>(&Vs[off]), dof[kk], dp);
-      }
+        for (int db = 0; db < D / 32; ++db) kt_f[h][db] = tr8(Ks + (32 * kb + 16 * h) * D, db);
       const bool need_mask = (CAUSAL && ka + 31 > q0w) || (ka + 32 > N);
-      float ds[16];
+      half8 sa[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float pj = exp2_fast(fmaf(s[j], c, nl));
+        float pj = exp2_fast(fmaf(s[kb][j], c, nl));
         if (need_mask) {
           const int key = ka + result_row(j, g);
           if (key >= N || (CAUSAL && key > qrow)) pj = 0.f;
         }
-        ds[j] = pj * (dp[j] - delta);
+        sa[j >> 3][j & 7] = (half_t)(pj * (dp[kb][j] - delta));
       }
-      half8 sa[2];
-      sa[0] = to_half8(ds);
-      sa[1] = to_half8(ds + 8);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          const int off = (32 * db + ql) * T::TS + 32 * kb + 16 * h + 8 * g;
-          dq[db] = mfma32(*reinterpret_cast<const half8*>(&Kt[off]), sa[h], dq[db]);
-        }
+        for (int db = 0; db < D / 32; ++db) dq[db] = mfma32(kt_f[h][db], sa[h], dq[db]);
     }
-    if (more) {
-      __syncthreads();
-      sk.store(Ks, Kt, tid);
-      sv.store(Vs, nullptr, tid);
-      __syncthreads();
-    }
+    wait_vm_and_barrier<(T::AHEAD - 1) * IPT>();
+  };
+
+  wait_vm_and_barrier<(T::AHEAD - 1) * IPT>();
+  for (int t = 0; t < ntiles; t += T::NSTAGE) {
+    step(ic<0>{}, t);
+    if (t + 1 >= ntiles) break;
+    step(ic<1>{}, t + 1);
+    if (t + 2 >= ntiles) break;
+    step(ic<2>{}, t + 2);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const float scale = a.scale;
   const rsrc_t rdq = make_rsrc(a.dq + (int64_t)head * N * D, slab);
@@ -496,26 +563,43 @@ hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-#define FA_BWD_VARIANT(LAUNCH, ROWS_PER_WAVE, NW, TILE)                                   \
-  {                                                                                       \
-    NW, ROWS_PER_WAVE * NW, TILE,                                                         \
-    {                                                                                     \
-      {(void*)&LAUNCH<32, false, NW, TILE>, (void*)&LAUNCH<32, true, NW, TILE>},          \
-      {(void*)&LAUNCH<64, false, NW, TILE>, (void*)&LAUNCH<64, true, NW, TILE>},          \
-      {(void*)&LAUNCH<128, false, NW, TILE>, (void*)&LAUNCH<128, true, NW, TILE>},        \
-    }                                                                                     \
+template <int D, bool CAUSAL, int NW, int TILE>
+constexpr void* dkdv_entry() {
+  if constexpr (dkdv_tiling_ok<D, NW, TILE>())
+    return (void*)&dkdv_launch<D, CAUSAL, NW, TILE>;
+  else
+    return nullptr;
+}
+template <int D, bool CAUSAL, int NW, int TILE>
+constexpr void* dq_entry() {
+  if constexpr (dq_tiling_ok<D, NW, TILE>())
+    return (void*)&dq_launch<D, CAUSAL, NW, TILE>;
+  else
+    return nullptr;
+}
+
+#define FA_BWD_VARIANT(ENTRY, NW, TILE)                                         \
+  {                                                                             \
+    NW, 32 * NW, TILE,                                                          \
+    {                                                                           \
+      {ENTRY<32, false, NW, TILE>(), ENTRY<32, true, NW, TILE>()},              \
+      {ENTRY<64, false, NW, TILE>(), ENTRY<64, true, NW, TILE>()},              \
+      {ENTRY<128, false, NW, TILE>(), ENTRY<128, true, NW, TILE>()},            \
+    }                                                                           \
   }
 
 static const Variant kDkdvVariants[] = {
-    FA_BWD_VARIANT(dkdv_launch, 32, 4, 64),
-    FA_BWD_VARIANT(dkdv_launch, 32, 4, 32),
-    FA_BWD_VARIANT(dkdv_launch, 32, 2, 64),
+    FA_BWD_VARIANT(dkdv_entry, 4, 64),
+    FA_BWD_VARIANT(dkdv_entry, 4, 32),
+    FA_BWD_VARIANT(dkdv_entry, 2, 64),
+    FA_BWD_VARIANT(dkdv_entry, 8, 64),
 };
 
 static const Variant kDqVariants[] = {
-    FA_BWD_VARIANT(dq_launch, 32, 4, 64),
-    FA_BWD_VARIANT(dq_launch, 32, 4, 32),
-    FA_BWD_VARIANT(dq_launch, 32, 2, 64),
+    FA_BWD_VARIANT(dq_entry, 4, 64),
+    FA_BWD_VARIANT(dq_entry, 4, 32),
+    FA_BWD_VARIANT(dq_entry, 2, 64),
+    FA_BWD_VARIANT(dq_entry, 8, 64),
 };
 
 const Variant* dkdv_variants(int* count) {

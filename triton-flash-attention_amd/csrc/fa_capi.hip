@@ -38,16 +38,20 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
                                        {{-1, -1}, {-1, -1}, {-1, -1}}};
 
 // Static tiling table (replaces the Triton autotuner). Values are variant
-// indices into the registries of fa_fwd.hip / fa_bwd.hip:
+// indices into the registries of fa_fwd.hip / fa_bwd.hip, chosen from
+// per-kernel sweeps on MI355X at the BASELINE shapes (D=32: N=16381 GQA;
+// D=64: B4 H16 N4096; D=128: B2 H32 N8192):
 //   fwd : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 8 waves, 64; 2 = 4 waves, 32;
 //         3 = 2 waves, 64; 4 = 4 waves, 128 (not every variant exists for every D)
-//   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64
-//   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64
+//   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
+//         3 = 8 waves, 64
+//   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
+//         3 = 8 waves, 64
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
-    {{0, 0}, {2, 2}, {2, 2}},  // fwd
-    {{0, 0}, {0, 0}, {1, 1}},  // dkdv
-    {{0, 0}, {0, 0}, {0, 0}},  // dq
+    {{4, 4}, {2, 2}, {2, 2}},  // fwd
+    {{2, 2}, {3, 3}, {1, 1}},  // dkdv
+    {{0, 0}, {1, 1}, {1, 1}},  // dq
 };
 
 const fa::Variant* registry(int kind, int* count) {

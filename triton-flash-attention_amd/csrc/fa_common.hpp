@@ -291,6 +291,19 @@ __device__ __forceinline__ void dma_b128(int4v rsrc, uint32_t voff, uint32_t lds
       : "memory");
 }
 
+// 4 bytes per lane from byte offset `voff` to LDS[m0 + 4 lane] (256 B per wave).
+__device__ __forceinline__ void dma_b32(int4v rsrc, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(rsrc), "s"(lds_base)
+      : "memory");
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight,
 // then synchronise the work-group. Both are opaque to the compiler (memory
 // clobber), so no LDS access moves across them.
