@@ -82,6 +82,27 @@ int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                 float scale, int causal, void* stream);
 
+/* Workspace bytes fa_bwd_dkdv_ws needs for this shape (0: it runs as one
+ * pass and needs none); negative FA_ERR_* for rejected arguments. No
+ * reference counterpart: the reference reduces GQA groups with fp16 atomics. */
+int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                     int causal);
+
+/* fa_bwd_dkdv with a caller-provided device workspace (16-byte aligned).
+ * When the shape has too few (key tile, KV head) work-groups to fill the GPU
+ * (GQA with few KV heads, long causal sequences), each key tile's steps are
+ * split over several work-groups that write fp32 partials into the workspace,
+ * and a second kernel sums them in a fixed order into dk, dv (deterministic).
+ * workspace may be NULL when fa_bwd_dkdv_workspace_bytes returned 0; a
+ * non-NULL workspace smaller than required is rejected (FA_ERR_BAD_SHAPE).
+ * Replaces phase 1 of the _attn_bwd launch, attention.py:754-770 (kernel 428-505). */
+int fa_bwd_dkdv_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   const fa_half_t* dO, const float* lse, const float* delta,
+                   fa_half_t* dk, fa_half_t* dv,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                   float scale, int causal, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
 /* dq (fully overwritten). Recomputes P from lse.
  * Replaces phase 2 of the _attn_bwd launch, attention.py:754-770 (kernel 507-573). */
 int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,

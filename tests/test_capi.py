@@ -143,3 +143,17 @@ def test_launch_without_a_device_reports_the_hip_error(lib):
     rc = _fwd(lib)
     assert rc > 0
     assert "fa_fwd launch" in _lib.last_error()
+
+
+def test_dkdv_workspace_sizing_and_rejection(lib):
+    # MHA with many key tiles: single pass, no workspace
+    assert lib.fa_bwd_dkdv_workspace_bytes(4, 16, 16, 4096, 64, 1) == 0
+    # GQA with 2 KV heads: split into partials; size = nsplit * 2 planes * B*Hkv*N*D * 4 bytes
+    plane = 1 * 2 * 16381 * 32
+    ws = lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 16381, 32, 1)
+    assert ws > 0 and ws % (2 * plane * 4) == 0 and ws // (2 * plane * 4) <= 8
+    assert lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 16381, 48, 1) == _lib.FA_ERR_HEAD_DIM
+    # a workspace smaller than required is rejected before any launch
+    rc = lib.fa_bwd_dkdv_ws(P, P, P, P, P, P, P, P, 1, 8, 2, 16381, 32, 0.17, 1, P, ws - 16, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE
+    assert "smaller than" in _lib.last_error()

@@ -195,6 +195,27 @@ def test_constant_value_rows_give_zero_qk_gradients():
     assert np.max(np.abs(got["dq"])) < 2e-3 and np.max(np.abs(got["dk"])) < 2e-3
 
 
+def test_split_dkdv_matches_single_pass():
+    """The split-and-reduce dK/dV (few key tiles per KV head) agrees with the
+    single-pass kernel up to fp32 summation order."""
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 8, 2, 700, 64, seed=12))
+    for causal in (False, True):
+        o, lse = _ops.flash_fwd(q, k, v, causal, 0.125)
+        delta = _ops.flash_bwd_preprocess(o, do)
+        lib = _lib.load()
+        assert lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 700, 64, int(causal)) > 0
+        dk1, dv1 = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, 0.125)  # split
+        dk2, dv2 = torch.empty_like(k), torch.empty_like(v)
+        rc = lib.fa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                             lse.data_ptr(), delta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
+                             1, 8, 2, 700, 64, 0.125, int(causal),
+                             torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc)
+        torch.cuda.synchronize()
+        assert_close("split dk", dk1.float(), dk2.float(), max_abs=2e-3, rel_l2=1e-3)
+        assert_close("split dv", dv1.float(), dv2.float(), max_abs=2e-3, rel_l2=1e-3)
+
+
 def test_deterministic_backward():
     q, k, v, do = make_inputs(2, 8, 2, 333, 64, seed=9)
     a = run_kernel(q, k, v, do, True)

@@ -83,6 +83,36 @@ template <int V>
 using ic = std::integral_constant<int, V>;
 
 // --------------------------------------------------------------------------
+// dK/dV split reduction: out[i] = fp16(sum_s part[s][i]) in split order.
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
+                                                           half_t* __restrict__ dk,
+                                                           half_t* __restrict__ dv,
+                                                           int64_t plane4, int nsplit) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index in 2 planes
+  if (i >= 2 * plane4) return;
+  const bool is_v = i >= plane4;
+  const int64_t j = is_v ? i - plane4 : i;
+  const float4v* src = reinterpret_cast<const float4v*>(part) + (is_v ? plane4 : 0) + j;
+  float4v acc = src[0];
+  for (int sp = 1; sp < nsplit; ++sp) acc += src[(int64_t)sp * 2 * plane4];
+  half4 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) h[e] = (half_t)acc[e];
+  *reinterpret_cast<half4*>((is_v ? dv : dk) + 4 * j) = h;
+}
+
+hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_t plane_elems,
+                               int nsplit, hipStream_t stream) {
+  const int64_t plane4 = plane_elems / 4;
+  const int64_t blocks = (2 * plane4 + 255) / 256;
+  if (plane_elems % 4 != 0 || blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, part, dk,
+                     dv, plane4, nsplit);
+  return hipGetLastError();
+}
+
+// --------------------------------------------------------------------------
 // dK / dV
 //
 // Work-group: NW waves x 32 keys (K, V resident in VGPRs as MFMA B operands).
@@ -128,8 +158,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const int g = lane >> 5;
 
   // Key tiles near the start see the most queries under the causal mask:
-  // ascending tile order is heavy-first.
-  const TileHead th = decode_block(blockIdx.x, a.BHkv);
+  // ascending tile order is heavy-first. Split mode: the split index is the
+  // slowest-varying part of the block index.
+  const int split = blockIdx.x / (a.num_tiles * a.BHkv);
+  const TileHead th = decode_block(blockIdx.x - split * a.num_tiles * a.BHkv, a.BHkv);
   const int kvtile = th.tile_rank;
   const int kvh = th.head;
   const int b = kvh / a.Hkv;
@@ -158,14 +190,19 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
 
   const int q_begin = CAUSAL ? (k0 / QT) * QT : 0;
   const int ntq = (N - q_begin + QT - 1) / QT;
-  const int nsteps = G * ntq;
+  // This work-group's chunk [s_lo, s_lo + nsteps) of the tile's G * ntq steps.
+  const int total_steps = G * ntq;
+  const int chunk = (total_steps + a.nsplit - 1) / a.nsplit;
+  const int s_lo = min(split * chunk, total_steps);
+  const int nsteps = min(chunk, total_steps - s_lo);
 
   // Step s streams query tile (s % ntq) of query head (s / ntq) of the group.
   // Steps past the end load harmless data (rows past N read as zeros), so
   // every step issues the same number of DMA instructions.
   Dma dma;
   dma.init(wave, lane);
-  auto issue_step = [&](int st, int slot) {
+  auto issue_step = [&](int u, int slot) {
+    const int st = s_lo + u;
     const int gi = min(st / ntq, G - 1);
     const int qt0 = q_begin + (st - gi * ntq) * QT;
     const int head = b * a.Hq + hkv * G + gi;
@@ -226,9 +263,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const float c = a.c;
   const bool wave_live = k0w < N;
 
-  auto step = [&](auto slot_c, int st) {
+  auto step = [&](auto slot_c, int u) {
     constexpr int SLOT = decltype(slot_c)::value;
-    issue_step(st + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
+    issue_step(u + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
+    const int st = s_lo + u;
     const int gi = st / ntq;
     const int qt0 = q_begin + (st - gi * ntq) * QT;
     const half_t* Qs = lds + SLOT * T::STAGE;
@@ -311,16 +349,39 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   };
 
   wait_vm_and_barrier<(T::AHEAD - 1) * IPT>();  // step 0's tile
-  for (int st = 0; st < nsteps; st += T::NSTAGE) {
-    step(ic<0>{}, st);
-    if (st + 1 >= nsteps) break;
-    step(ic<1>{}, st + 1);
-    if (st + 2 >= nsteps) break;
-    step(ic<2>{}, st + 2);
+  for (int u = 0; u < nsteps; u += T::NSTAGE) {
+    step(ic<0>{}, u);
+    if (u + 1 >= nsteps) break;
+    step(ic<1>{}, u + 1);
+    if (u + 2 >= nsteps) break;
+    step(ic<2>{}, u + 2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const float scale = a.scale;
+  if (a.nsplit > 1) {
+    // fp32 partials (dK already scaled); an empty chunk writes zeros.
+    const int64_t plane = (int64_t)a.BHkv * N * D;
+    float* pk = a.part + (int64_t)split * 2 * plane + (int64_t)kvh * N * D;
+    float* pv = pk + plane;
+    if (krow < N) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int64_t e0 = (int64_t)krow * D + 32 * db + 8 * jq + 4 * g;
+          float4v kq, vq;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            kq[e] = dk[db][4 * jq + e] * scale;
+            vq[e] = dv[db][4 * jq + e];
+          }
+          *reinterpret_cast<float4v*>(pk + e0) = kq;
+          *reinterpret_cast<float4v*>(pv + e0) = vq;
+        }
+    }
+    return;
+  }
   const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * N * D, slab);
   const rsrc_t rdv = make_rsrc(a.dv + (int64_t)kvh * N * D, slab);
 #pragma unroll
@@ -342,7 +403,8 @@ hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DkdvTile<D, NW, QT>;
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BKV - 1) / T::BKV;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BHkv;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((dkdv_kernel<D, CAUSAL, NW, QT>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);

@@ -50,7 +50,7 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
     {{4, 4}, {2, 2}, {2, 2}},  // fwd
-    {{2, 2}, {3, 3}, {1, 1}},  // dkdv
+    {{0, 0}, {3, 3}, {1, 1}},  // dkdv
     {{0, 0}, {1, 1}, {1, 1}},  // dq
 };
 
@@ -139,7 +139,28 @@ fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
   a.num_tiles = 0;
   a.c = scale * fa::kLog2e;
   a.scale = scale;
+  a.nsplit = 1;
+  a.part = nullptr;
   return a;
+}
+
+// dK/dV split factor: key tiles x KV heads below ~3 work-groups per CU (GQA
+// with few KV heads, or long causal sequences with few heads) split each key
+// tile's step sequence into up to 8 chunks that run as separate work-groups.
+constexpr int64_t kSplitTargetWorkgroups = 768;
+constexpr int kMaxSplit = 8;
+
+int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hkv, int64_t N) {
+  const int64_t tiles = (N + var.rows - 1) / var.rows;
+  const int64_t wgs = tiles * B * Hkv;
+  if (wgs >= kSplitTargetWorkgroups) return 1;
+  int64_t s = (kSplitTargetWorkgroups + wgs - 1) / wgs;
+  if (s > kMaxSplit) s = kMaxSplit;
+  return (int)s;
+}
+
+int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t N, int64_t D) {
+  return nsplit > 1 ? (int64_t)nsplit * 2 * B * Hkv * N * D * 4 : 0;
 }
 
 }  // namespace
@@ -206,6 +227,51 @@ int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, cons
   a.dv = reinterpret_cast<fa::half_t*>(dv);
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
   return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_bwd_dkdv launch");
+}
+
+int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                     int causal) {
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dkdv_workspace_bytes: no kernel for the selected tiling");
+  return split_workspace_bytes(dkdv_split(*var, B, Hkv, N), B, Hkv, N, D);
+}
+
+int fa_bwd_dkdv_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dk,
+                   fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                   float scale, int causal, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
+  if (!q || !k || !v || !dO || !lse || !delta || !dk || !dv)
+    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dkdv_ws: null pointer");
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  if ((rc = check_aligned("fa_bwd_dkdv_ws", {q, k, v, dO, lse, delta, dk, dv}))) return rc;
+  if ((rc = check_scale(scale))) return rc;
+  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dkdv_ws: no kernel for the selected tiling");
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  a.dk = reinterpret_cast<fa::half_t*>(dk);
+  a.dv = reinterpret_cast<fa::half_t*>(dv);
+  const int nsplit = dkdv_split(*var, B, Hkv, N);
+  const int64_t need = split_workspace_bytes(nsplit, B, Hkv, N, D);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
+  if (need == 0 || workspace == nullptr || workspace_bytes < need) {
+    if (need > 0 && workspace != nullptr)
+      return fail(FA_ERR_BAD_SHAPE, "fa_bwd_dkdv_ws: workspace of %lld bytes is smaller than the "
+                  "%lld bytes fa_bwd_dkdv_workspace_bytes reports", (long long)workspace_bytes,
+                  (long long)need);
+    return hip_result(fn(a, s), "fa_bwd_dkdv_ws launch");
+  }
+  if ((rc = check_aligned("fa_bwd_dkdv_ws", {workspace}))) return rc;
+  a.nsplit = nsplit;
+  a.part = static_cast<float*>(workspace);
+  hipError_t e = fn(a, s);
+  if (e != hipSuccess) return hip_result(e, "fa_bwd_dkdv_ws launch");
+  return hip_result(fa::launch_split_reduce(a.part, a.dk, a.dv, B * Hkv * N * D, nsplit, s),
+                    "fa_bwd_dkdv_ws reduce launch");
 }
 
 int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,

@@ -46,6 +46,11 @@ struct BwdArgs {
   int num_tiles;   // filled in by the launcher
   float c;         // scale * log2(e)
   float scale;
+  // dK/dV split mode (nsplit > 1): work-group (tile, head, split) covers one
+  // contiguous chunk of its key tile's (query head, query tile) steps and
+  // writes fp32 partials part[split][B*Hkv][N][D] (dK then dV planes).
+  int nsplit;
+  float* part;
 };
 
 enum KernelKind { kFwd = 0, kDkdv = 1, kDq = 2, kNumKinds = 3 };
@@ -67,6 +72,10 @@ struct Variant {
 const Variant* fwd_variants(int* count);
 const Variant* dkdv_variants(int* count);
 const Variant* dq_variants(int* count);
+
+// Sum of the nsplit fp32 partial planes into fp16 dK, dV (fixed order).
+hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_t plane_elems,
+                               int nsplit, hipStream_t stream);
 
 hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
                              int D, hipStream_t stream);

@@ -43,6 +43,11 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _INT,
         (_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P),
     ),
+    "fa_bwd_dkdv_workspace_bytes": (_I64, (_I64, _I64, _I64, _I64, _I64, _INT)),
+    "fa_bwd_dkdv_ws": (
+        _INT,
+        (_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P, _I64, _P),
+    ),
     "fa_bwd_dq": (
         _INT,
         (_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P),

@@ -165,18 +165,26 @@ def _aligned_all(*tensors):
 def flash_bwd_dkdv(
     q, k, v, do, lse, delta, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """dK, dV [B,Hkv,N,D] fp16 (GQA groups reduced in fp32 in-kernel)."""
+    """dK, dV [B,Hkv,N,D] fp16 (GQA groups reduced in fp32, deterministic).
+
+    Shapes with too few key tiles to fill the GPU get a workspace (from the
+    caching allocator) for the library's split-and-reduce mode."""
     B, Hq, Hkv, N, D = _check_bwd_inputs(q, k, v, do, lse, delta)
     q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
     lib = _lib.load()
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
+    ws_bytes = lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, int(bool(causal)))
+    if ws_bytes < 0:
+        _lib.check(ws_bytes)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
     with torch.cuda.device(q.device):
         rc = _launch(
-            "dkdv", lib.fa_bwd_dkdv,
+            "dkdv", lib.fa_bwd_dkdv_ws,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
             delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+            B, Hq, Hkv, N, D, float(scale), int(bool(causal)),
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q),
         )
     _lib.check(rc)
     return dk, dv
