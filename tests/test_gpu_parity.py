@@ -216,6 +216,60 @@ def test_split_dkdv_matches_single_pass():
         assert_close("split dv", dv1.float(), dv2.float(), max_abs=2e-3, rel_l2=1e-3)
 
 
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_every_tiling_variant_matches_oracle(head_dim, causal):
+    """Each compiled tiling of each kernel (fwd, dK/dV single-pass and split,
+    dQ) against the oracle on a ragged GQA shape, not only the defaults."""
+    B, Hq, Hkv, N, D = 1, 4, 2, 300, head_dim
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=77, mult=0.5)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    scale = D ** -0.5
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
+    delta = _ops.flash_bwd_preprocess(o, dod)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
+                           o16=o.cpu().numpy())
+
+    def close(tag, got, name):
+        assert_close(tag, torch.as_tensor(got).double().cpu().numpy(), ref[name])
+
+    kinds = ((_lib.KERNEL_FWD, "fwd"), (_lib.KERNEL_DKDV, "dkdv"), (_lib.KERNEL_DQ, "dq"))
+    for kind, kname in kinds:
+        for var in _lib.tiling_variants(kind, D, causal):
+            tag = f"D={D} causal={causal} {kname} variant {var['variant']} " \
+                  f"({var['waves']} waves, tile {var['tile']})"
+            _note(tag)
+            _lib.set_tiling(kind, D, causal, var["variant"])
+            try:
+                if kind == _lib.KERNEL_FWD:
+                    o2, lse2 = _ops.flash_fwd(qd, kd, vd, causal, scale)
+                    torch.cuda.synchronize()
+                    close(tag + " o", o2, "o")
+                    lse_err = float(np.max(np.abs(lse2.double().cpu().numpy() - ref["lse"])))
+                    assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"
+                elif kind == _lib.KERNEL_DKDV:
+                    dk1, dv1 = _ops.flash_bwd_dkdv(qd, kd, vd, dod, lse, delta, causal, scale)
+                    dk2, dv2 = torch.empty_like(kd), torch.empty_like(vd)
+                    _lib.check(lib.fa_bwd_dkdv(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                               dod.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+                                               dk2.data_ptr(), dv2.data_ptr(), B, Hq, Hkv, N, D,
+                                               scale, int(causal), stream))
+                    torch.cuda.synchronize()
+                    close(tag + " dk (split)", dk1, "dk")
+                    close(tag + " dv (split)", dv1, "dv")
+                    close(tag + " dk", dk2, "dk")
+                    close(tag + " dv", dv2, "dv")
+                else:
+                    dq = _ops.flash_bwd_dq(qd, kd, vd, dod, lse, delta, causal, scale)
+                    torch.cuda.synchronize()
+                    close(tag + " dq", dq, "dq")
+            finally:
+                _lib.set_tiling(kind, D, causal, -1)
+
+
 def test_deterministic_backward():
     q, k, v, do = make_inputs(2, 8, 2, 333, 64, seed=9)
     a = run_kernel(q, k, v, do, True)

@@ -82,6 +82,15 @@ hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, in
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// f(integral_constant<int, I>) for I = B .. E-1, fully unrolled.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // --------------------------------------------------------------------------
 // dK/dV split reduction: out[i] = fp16(sum_s part[s][i]) in split order.
 // --------------------------------------------------------------------------
@@ -412,6 +421,462 @@ hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
 }
 
 // --------------------------------------------------------------------------
+// dK / dV, software-pipelined over 32-query units.
+//
+// Same work decomposition as dkdv_kernel (NW waves x 32 keys, K and V held
+// as MFMA B operands, (query head, query tile) units streamed through an LDS
+// DMA ring), but the three stages of a unit are spread over consecutive
+// units so that each unit's body has matrix and vector work that do not
+// depend on each other:
+//   body of unit u:  vector work of unit u      P = exp2(S c - LSE'), dS' = P dPd
+//                    matrix work of unit u + 1  S = Q K^T, dPd = Delta - dO V^T
+//                    matrix work of unit u - 1  dV^T += dO^T P, dK^T += Q^T dS'
+// dPd starts from Delta in the accumulator and uses -V, so dS' = -dS and the
+// subtraction of Delta costs nothing; dK is negated once at the end.
+// Causal mask: units a wave sees entirely before its keys read LSE' = +inf
+// (P = 0 exactly) from a small table; the diagonal unit sets its masked S
+// values to -inf. Rows past N need no mask: their Q and dO rows load as
+// zeros, so their P (finite) multiplies zero in both updates.
+// A step is two units and ends with one work-group barrier. The ring has 8
+// unit slots: units 2s-1 .. 2s+2 are read in step s, 2s+3 and 2s+4 are in
+// flight and 2s+5, 2s+6 are issued. Every work-group runs its unit count
+// rounded up to the 8-unit unroll; the extra units stream rows past N
+// (zeros) and add nothing.
+// --------------------------------------------------------------------------
+template <int D, int NW>
+struct DkdvPipeTile {
+  static constexpr int BKV = 32 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int QT = 32;
+  static constexpr int TILE = QT * D;               // halves of the Q (or dO) unit
+  static constexpr int AUX = 128;                   // floats: LSE[64], Delta[64]
+  static constexpr int STAGE = 2 * TILE + 2 * AUX;  // halves per ring slot
+  static constexpr int NSTAGE = 8;
+  static constexpr int AHEAD = 5;                   // units issued before step 0
+  static constexpr int LDS_HALVES = NSTAGE * STAGE + 2 * 64;  // + 64 x +inf
+};
+
+template <int D, int NW>
+constexpr bool dkdv_pipe_tiling_ok() {
+  using T = DkdvPipeTile<D, NW>;
+  constexpr int instr = T::TILE * 2 / 1024;
+  // one 1 KiB piece per wave (duplicates allowed), and two work-groups per CU
+  return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
+         2 * T::LDS_HALVES * 2 <= 160 * 1024 && D <= 64;
+}
+
+// LDS reads of the pipelined dK/dV body are issued this many MFMA tasks
+// ahead of their consumer.
+#ifndef FA_DKDV_LEAD
+#define FA_DKDV_LEAD 3
+#endif
+
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+void dkdv_pipe_kernel(BwdArgs a) {
+  using T = DkdvPipeTile<D, NW>;
+  using Dma = DmaStager<D, T::QT, NW>;
+  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
+  constexpr int NS = T::NSTAGE;
+  constexpr int IPU = 3;  // this wave's DMA instructions per unit: Q, dO, LSE or Delta
+  __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALVES];
+  constexpr int kInfOff = NS * T::STAGE / 2;  // float offset of the +inf table
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ql = lane & 31;
+  const int g = lane >> 5;
+
+  const int split = blockIdx.x / (a.num_tiles * a.BHkv);
+  const TileHead th = decode_block(blockIdx.x - split * a.num_tiles * a.BHkv, a.BHkv);
+  const int kvh = th.head;
+  const int b = kvh / a.Hkv;
+  const int hkv = kvh - b * a.Hkv;
+  const int G = a.group;
+  const int N = a.N;
+  const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t aux_bytes = (uint32_t)N * 4u;
+  const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * N * D, slab);
+  const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * N * D, slab);
+
+  const int k0 = th.tile_rank * T::BKV;
+  const int k0w = k0 + 32 * wave;
+  const int krow = k0w + ql;
+
+  // K and -V as B operands (column = key ql, d = 16*kk + 8*g .. +7).
+  half8 kf[D / 16], vn[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    const uint32_t off = (uint32_t)(krow * D + 16 * kk + 8 * g) * 2u;
+    kf[kk] = __builtin_bit_cast(half8, buf_load_b128(rk, off));
+    vn[kk] = -__builtin_bit_cast(half8, buf_load_b128(rv, off));
+  }
+  wait_all_vm();
+  // Opaque from here on, so that -V is not recomputed from V inside the loop.
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(vn[kk]));
+
+  const int q_begin = CAUSAL ? k0 : 0;  // k0 is a multiple of 32
+  const int ntq = (N - q_begin + T::QT - 1) / T::QT;
+  const int total_units = G * ntq;
+  const int chunk = (total_units + a.nsplit - 1) / a.nsplit;
+  const int u_lo = min(split * chunk, total_units);
+  const int nunits = min(chunk, total_units - u_lo);
+  const int npad = (nunits + NS - 1) / NS * NS;
+
+  // Issue cursor: query head gi of the group and first row of the next unit
+  // to fetch; after the last unit the row is N (zeros from then on).
+  int i_gi = min(u_lo / ntq, G - 1);
+  int i_row = q_begin + (u_lo - i_gi * ntq) * T::QT;
+  int i_left = nunits;
+  int4v r_q, r_do, r_aux;
+  const bool is_lse = (wave & 1) == 0;  // even waves fetch LSE, odd waves Delta
+  auto set_head = [&]() {
+    const int head = b * a.Hq + hkv * G + i_gi;
+    r_q = make_rsrc_words(a.q + (int64_t)head * N * D, slab);
+    r_do = make_rsrc_words(a.dO + (int64_t)head * N * D, slab);
+    r_aux = make_rsrc_words((is_lse ? a.lse : a.delta) + (int64_t)head * N, aux_bytes);
+  };
+  set_head();
+
+  Dma dma;
+  dma.init(wave, lane);
+  const uint32_t lds0 = lds_addr(lds);
+  const uint32_t aux_lane = (uint32_t)lane * 4u;
+  const uint32_t aux_lds = 2u * T::TILE * 2u + (is_lse ? 0u : 64u * 4u);
+  auto issue = [&](int slot) {
+    const int row0 = i_left > 0 ? i_row : N;
+    const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
+    const uint32_t va = (uint32_t)row0 * 4u + aux_lane;
+    const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u);
+    const uint32_t piece = (uint32_t)dma.piece0 * 1024u;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %5\n\t"
+        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %6\n\t"
+        "buffer_load_dwordx4 %1, %4, 0 offen lds\n\t"
+        "s_mov_b32 m0, %8\n\t"
+        "buffer_load_dword %2, %7, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(vt), "v"(va), "s"(r_q), "s"(r_do), "s"(base + piece),
+          "s"(base + T::TILE * 2u + piece), "s"(r_aux), "s"(base + aux_lds)
+        : "memory");
+    --i_left;
+    i_row += T::QT;
+    if (i_row >= N && i_left > 0) {
+      ++i_gi;
+      i_row = q_begin;
+      set_head();
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < T::AHEAD; ++u) issue(u);
+
+  // The slot read as "unit -1" holds zeros (its P and dS' are zero too);
+  // the +inf table of fully masked units.
+  {
+    half_t* zs = lds + (NS - 1) * T::STAGE;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < 2 * T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
+    if (tid < 64) reinterpret_cast<float*>(lds)[kInfOff + tid] = __builtin_inff();
+  }
+  // Units 0, 1, 2 landed (3, 4 in flight), zeros and table written.
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
+
+  int r_off[D / 16];  // row reads: row row_perm(ql), chunk 2*kk + g
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) r_off[kk] = swz_offset<D>(row_perm(ql), 2 * kk + g);
+  int t_off[D / 32][2];  // transposed reads (see read_tr)
+  {
+    const int grp = lane >> 4, i = lane & 15, r = i >> 2, qq = i & 3;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int col = 32 * db + 16 * (grp & 1) + 4 * qq;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 8 * g + r + 4 * h2;
+        t_off[db][h2] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
+      }
+    }
+  }
+  auto tr8 = [&](const half_t* base, int db) {
+    const half4 lo = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][0])));
+    const half4 hi = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][1])));
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
+    return v;
+  };
+  // 16 per-query floats at tab[16h + e] (h = 0, 1; e = 0..7) for a table
+  // pointer that already includes the lane's 8g: value j = 8h + e of the
+  // lane's S values is query 16h + 8g + e.
+  auto table16 = [&](const float* tab) {
+    float16v r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float4v x0 = *reinterpret_cast<const float4v*>(&tab[16 * h]);
+      const float4v x1 = *reinterpret_cast<const float4v*>(&tab[16 * h + 4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[8 * h + e] = x0[e];
+        r[8 * h + 4 + e] = x1[e];
+      }
+    }
+    return r;
+  };
+
+  float16v dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      dk[db][j] = 0.f;
+      dv[db][j] = 0.f;
+    }
+
+  const float c = a.c;
+  const float* const fl = reinterpret_cast<const float*>(lds);
+  // Pipeline registers: S, dPd of the current unit; P, dS' of the previous one.
+  float16v s_cur, dp_cur;
+  {
+    dp_cur = table16(reinterpret_cast<const float*>(lds + 2 * T::TILE) + 64 + 8 * g);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s_cur[j] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      s_cur = mfma32(*reinterpret_cast<const half8*>(lds + r_off[kk]), kf[kk], s_cur);
+      dp_cur = mfma32(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), vn[kk], dp_cur);
+    }
+  }
+  half8 pa_prev[2], sa_prev[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pa_prev[h][e] = (half_t)0.f;
+      sa_prev[h][e] = (half_t)0.f;
+    }
+
+  auto dvdk = [&](const half_t* slot) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        dv[db] = mfma32(tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h], dv[db]);
+        dk[db] = mfma32(tr8(slot + 16 * h * D, db), sa_prev[h], dk[db]);
+      }
+  };
+
+  int c_row = q_begin + (u_lo - min(u_lo / ntq, G - 1) * ntq) * T::QT;  // compute cursor
+
+  // Body of one unit in ring slot SLOT (see the header comment).
+  auto body = [&](auto slot_c) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    const half_t* cur = lds + SLOT * T::STAGE;
+    const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
+    const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
+    const int qa = c_row;
+    c_row += T::QT;
+    if (c_row >= N) c_row = q_begin;  // next query head of the group
+
+    // Float offset (from lds) of the lane's LSE' values of this unit.
+    int ltab = (SLOT * T::STAGE + 2 * T::TILE) / 2 + 8 * g;
+    if constexpr (CAUSAL) {
+      if (qa < k0w) {
+        ltab = kInfOff + 8 * g;
+      } else if (qa == k0w) {
+        // diagonal unit: query 16h + 8g + e is kept iff it is >= key ql
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (16 * (j >> 3) + 8 * g + (j & 7) < ql) s_cur[j] = -__builtin_inff();
+      }
+    }
+
+    // Hand-ordered body: 16 (D = 64) or 8 (D = 32) MFMA tasks in the order
+    // dV, dK (unit u-1), S, dPd (unit u+1), repeated, so that no two
+    // adjacent tasks share an accumulator. Group i issues the LDS reads of
+    // task i + kLead, runs task i and part of unit u's vector work; fences
+    // keep the compiler from regrouping.
+    constexpr int NQ = D / 16;  // tasks of each kind
+    constexpr int NTASK = 4 * NQ;
+    constexpr int kLead = FA_DKDV_LEAD;
+    const half_t* q_nxt = nxt;
+    const half_t* do_nxt = nxt + T::TILE;
+    const half_t* q_prv = prv;
+    const half_t* do_prv = prv + T::TILE;
+    auto load_op = [&](auto t_c) -> half8 {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int kind = t % 4, q = t / 4;
+      constexpr int h = q / (D / 32), db = q % (D / 32);
+      if constexpr (kind == 0) return tr8(do_prv + 16 * h * D, db);
+      else if constexpr (kind == 1) return tr8(q_prv + 16 * h * D, db);
+      else if constexpr (kind == 2) return *reinterpret_cast<const half8*>(q_nxt + r_off[q]);
+      else return *reinterpret_cast<const half8*>(do_nxt + r_off[q]);
+    };
+    float16v s_nx, dp_nx;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s_nx[j] = 0.f;
+    auto run_task = [&](auto t_c, const half8& op) {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int kind = t % 4, q = t / 4;
+      constexpr int h = q / (D / 32), db = q % (D / 32);
+      if constexpr (kind == 0) dv[db] = mfma32(op, pa_prev[h], dv[db]);
+      else if constexpr (kind == 1) dk[db] = mfma32(op, sa_prev[h], dk[db]);
+      else if constexpr (kind == 2) s_nx = mfma32(op, kf[q], s_nx);
+      else dp_nx = mfma32(op, vn[q], dp_nx);
+    };
+    half8 pa[2], sa[2];
+    float16v lse;
+    // Vector work on value pairs (2pr, 2pr+1) in two stages placed in
+    // different groups, so that an MFMA separates each exp from its users:
+    //   A: p = exp2(s c - lse)      B: dS' = p dPd, both packed to fp16.
+    // The empty asm statements pin each stage to its fenced group (plain
+    // arithmetic would otherwise float).
+    float pexp[16];
+    auto stage_a = [&](int pr) {
+      float p2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -lse[2 * pr + e]));
+      asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
+      pexp[2 * pr] = p2[0];
+      pexp[2 * pr + 1] = p2[1];
+    };
+    auto stage_b = [&](int pr) {
+      half2v pp, ss;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int j = 2 * pr + e;
+        pp[e] = (half_t)pexp[j];
+        ss[e] = (half_t)(pexp[j] * dp_cur[j]);
+      }
+      asm volatile("" : "+v"(pp), "+v"(ss));
+      const int j = 2 * pr;
+      pa[j >> 3][j & 7] = pp[0];
+      pa[j >> 3][(j & 7) + 1] = pp[1];
+      sa[j >> 3][j & 7] = ss[0];
+      sa[j >> 3][(j & 7) + 1] = ss[1];
+    };
+
+    half8 op[NTASK];
+    // The LSE' offset as an opaque value, so that its loads stay after the
+    // fence instead of being split into the branches above.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(ltab));
+    static_for<0, kLead>([&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+    lse = table16(fl + ltab);
+    dp_nx = table16(reinterpret_cast<const float*>(nxt + 2 * T::TILE) + 64 + 8 * g);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NTASK>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(std::integral_constant<int, i + kLead>{});
+      run_task(i_c, op[i]);
+      // vector work of unit u: stage A of pair pr in group (2pr NTASK)/16,
+      // stage B one group later (B of the last pair shares the last group)
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr) {
+        constexpr int kSpan = NTASK;
+        const int ga = (2 * pr * kSpan) / 16;
+        const int gb = ga + 1 < NTASK ? ga + 1 : NTASK - 1;
+        if (ga == i) stage_a(pr);
+        if (gb == i) stage_b(pr);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+
+    s_cur = s_nx;
+    dp_cur = dp_nx;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      pa_prev[h] = pa[h];
+      sa_prev[h] = sa[h];
+    }
+  };
+
+  // Step p of the unrolled loop: units in slots 2p, 2p+1; issues the units
+  // 5 and 6 ahead (slots of the units finished before the last barrier).
+  auto step = [&](auto p_c) {
+    constexpr int P = decltype(p_c)::value;
+    issue((2 * P + 5) % NS);
+    issue((2 * P + 6) % NS);
+    body(std::integral_constant<int, 2 * P>{});
+    body(std::integral_constant<int, 2 * P + 1>{});
+    // Units up to 2s+4 landed for this wave, then published.
+    wait_vm_and_barrier<2 * IPU>();
+  };
+
+  static_assert(NS == 8, "the loop below is unrolled for 8 slots");
+  for (int u = 0; u < npad; u += NS) {
+    step(ic<0>{});
+    step(ic<1>{});
+    step(ic<2>{});
+    step(ic<3>{});
+  }
+  // dV/dK of the last unit (slot 7; zeros if it was a padding unit).
+  dvdk(lds + (NS - 1) * T::STAGE);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const float nscale = -a.scale;  // dK accumulated -dS
+  if (a.nsplit > 1) {
+    const int64_t plane = (int64_t)a.BHkv * N * D;
+    float* pk = a.part + (int64_t)split * 2 * plane + (int64_t)kvh * N * D;
+    float* pv = pk + plane;
+    if (krow < N) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+          const int64_t e0 = (int64_t)krow * D + 32 * db + 8 * jq + 4 * g;
+          float4v kq, vq;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            kq[e] = dk[db][4 * jq + e] * nscale;
+            vq[e] = dv[db][4 * jq + e];
+          }
+          *reinterpret_cast<float4v*>(pk + e0) = kq;
+          *reinterpret_cast<float4v*>(pv + e0) = vq;
+        }
+    }
+    return;
+  }
+  const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * N * D, slab);
+  const rsrc_t rdv = make_rsrc(a.dv + (int64_t)kvh * N * D, slab);
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const uint32_t off = (uint32_t)(krow * D + 32 * db + 8 * jq + 4 * g) * 2u;
+      buf_store_b64(rdk, off,
+                    pack4_half(dk[db][4 * jq] * nscale, dk[db][4 * jq + 1] * nscale,
+                               dk[db][4 * jq + 2] * nscale, dk[db][4 * jq + 3] * nscale));
+      buf_store_b64(rdv, off,
+                    pack4_half(dv[db][4 * jq], dv[db][4 * jq + 1], dv[db][4 * jq + 2],
+                               dv[db][4 * jq + 3]));
+    }
+}
+
+template <int D, bool CAUSAL, int NW>
+hipError_t dkdv_pipe_launch(const BwdArgs& a, hipStream_t stream) {
+  using T = DkdvPipeTile<D, NW>;
+  BwdArgs b = a;
+  b.num_tiles = (a.N + T::BKV - 1) / T::BKV;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((dkdv_pipe_kernel<D, CAUSAL, NW>), dim3((unsigned)blocks), dim3(T::NT), 0,
+                     stream, b);
+  return hipGetLastError();
+}
+
+// --------------------------------------------------------------------------
 // dQ
 //
 // Work-group: NW waves x 32 queries (Q, dO resident in VGPRs as B operands,
@@ -633,6 +1098,14 @@ constexpr void* dkdv_entry() {
     return nullptr;
 }
 template <int D, bool CAUSAL, int NW, int TILE>
+constexpr void* dkdv_pipe_entry() {
+  static_assert(TILE == 32, "the pipelined dK/dV kernel streams 32-query units");
+  if constexpr (dkdv_pipe_tiling_ok<D, NW>())
+    return (void*)&dkdv_pipe_launch<D, CAUSAL, NW>;
+  else
+    return nullptr;
+}
+template <int D, bool CAUSAL, int NW, int TILE>
 constexpr void* dq_entry() {
   if constexpr (dq_tiling_ok<D, NW, TILE>())
     return (void*)&dq_launch<D, CAUSAL, NW, TILE>;
@@ -655,6 +1128,7 @@ static const Variant kDkdvVariants[] = {
     FA_BWD_VARIANT(dkdv_entry, 4, 32),
     FA_BWD_VARIANT(dkdv_entry, 2, 64),
     FA_BWD_VARIANT(dkdv_entry, 8, 64),
+    FA_BWD_VARIANT(dkdv_pipe_entry, 4, 32),
 };
 
 static const Variant kDqVariants[] = {

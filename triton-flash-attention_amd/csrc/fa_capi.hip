@@ -44,13 +44,13 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //   fwd : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 8 waves, 64; 2 = 4 waves, 32;
 //         3 = 2 waves, 64; 4 = 4 waves, 128 (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
-//         3 = 8 waves, 64
+//         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (D <= 64)
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
     {{4, 4}, {2, 2}, {2, 2}},  // fwd
-    {{0, 0}, {3, 3}, {1, 1}},  // dkdv
+    {{4, 4}, {4, 4}, {1, 1}},  // dkdv
     {{0, 0}, {1, 1}, {1, 1}},  // dq
 };
 

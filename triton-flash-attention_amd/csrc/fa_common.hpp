@@ -69,6 +69,10 @@ __device__ __forceinline__ constexpr int result_row(int j, int g) {
   return 16 * (j >> 3) + 8 * g + (j & 7);
 }
 
+// A value the compiler must treat as wave-uniform (lives in an SGPR), so
+// branches on it are scalar branches rather than exec-masked regions.
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
 
@@ -313,21 +317,27 @@ __device__ __forceinline__ void wait_vm_and_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
+// When the tile has fewer 1 KiB pieces than the work-group has waves, wave w
+// loads piece w % INSTR: the duplicates write identical bytes, and every wave
+// still issues the same number of instructions per tile (uniform vmcnt).
 template <int D, int R, int NW>
 struct DmaStager {
   static constexpr int BYTES = R * D * 2;
   static constexpr int INSTR = BYTES / 1024;  // wave instructions per tile
-  static constexpr int PER_WAVE = INSTR / NW;
+  static constexpr int PER_WAVE = INSTR >= NW ? INSTR / NW : 1;
   static_assert(BYTES % 1024 == 0, "tile must be a multiple of 1 KiB");
-  static_assert(INSTR % NW == 0, "tile instructions must split evenly over the waves");
+  static_assert(INSTR % NW == 0 || NW % INSTR == 0,
+                "tile instructions must split evenly over the waves");
 
   // Per-lane byte offsets inside the tile's global rows (loop-invariant).
   uint32_t voff[PER_WAVE];
+  int piece0;  // first 1 KiB piece of this wave
 
   __device__ __forceinline__ void init(int wave, int lane) {
+    piece0 = INSTR >= NW ? wave * PER_WAVE : wave % INSTR;
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
-      const int byte = (wave * PER_WAVE + i) * 1024 + lane * 16;
+      const int byte = (piece0 + i) * 1024 + lane * 16;
       const int row = byte / (D * 2);
       const int pc = (byte % (D * 2)) / 16;
       const int c = swz_chunk<D>(row, pc);  // XOR swizzle is an involution
@@ -335,8 +345,8 @@ struct DmaStager {
     }
   }
   // Tile rows [row0, row0 + R) of the buffer -> LDS tile at `tile`.
-  __device__ __forceinline__ void issue(int4v rsrc, int row0, const half_t* tile, int wave) const {
-    const uint32_t base = lds_addr(tile) + (uint32_t)(wave * PER_WAVE) * 1024u;
+  __device__ __forceinline__ void issue(int4v rsrc, int row0, const half_t* tile, int) const {
+    const uint32_t base = lds_addr(tile) + (uint32_t)piece0 * 1024u;
     const uint32_t roff = (uint32_t)row0 * D * 2u;
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) dma_b128(rsrc, roff + voff[i], base + 1024u * i);

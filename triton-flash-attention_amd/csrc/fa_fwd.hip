@@ -139,7 +139,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
   // A wave takes part in tile t unless all its queries are past the end or,
   // causally, before every key of the tile (wave-uniform).
-  auto active = [&](int t) { return (q0w < N) && !(CAUSAL && t * BN > q0w + 31); };
+  auto active = [&](int t) { return uniform((q0w < N) && !(CAUSAL && t * BN > q0w + 31)) != 0; };
 
   float16v sbuf[2][KB];  // S^T of two consecutive tiles (software pipeline)
 
@@ -164,9 +164,10 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   };
 
   // One key tile: next DMA, next tile's scores, this tile's softmax + P.V.
-  auto step = [&](auto slot_c, auto sb_c, int t) {
+  auto step = [&](auto slot_c, auto sb_c, int t_in) {
     constexpr int SLOT = decltype(slot_c)::value;
     constexpr int SB = decltype(sb_c)::value;
+    const int t = uniform(t_in);
     const int kv0 = t * BN;
     // (1) tile t+AHEAD -> the slot tile t-1 used (released by the last barrier).
     issue_tile(t + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
     if (act) {
       float16v* sc = sbuf[SB];
-      const bool need_mask = (CAUSAL && kv0 + BN - 1 > q0w) || (kv0 + BN > N);
+      const bool need_mask = uniform((CAUSAL && kv0 + BN - 1 > q0w) || (kv0 + BN > N)) != 0;
       if (need_mask) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
