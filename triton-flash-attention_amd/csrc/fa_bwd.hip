@@ -1090,6 +1090,337 @@ hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// --------------------------------------------------------------------------
+// dQ, software-pipelined over 32-key units.
+//
+// Work-group: NW waves x 32 queries (Q, dO as MFMA B operands, LSE and Delta
+// one per lane), 32-key units (K, V rows) streamed through an 8-slot LDS DMA
+// ring, two units per barrier step. The body of unit u runs
+//   vector work of unit u      P^T = exp2(S^T c - LSE), dS'^T = P^T dPd^T
+//   matrix work of unit u + 1  S^T = K Q^T, dPd^T = Delta - V dO^T
+//   matrix work of unit u - 1  dQ^T += K^T dS'^T      (K^T via transposing reads)
+// with dPd^T started from Delta in the accumulator (operand -dO), so
+// dS' = -dS and dQ is negated once at the end. Keys past N need no mask:
+// their K and V rows load as zeros, so their P (finite) multiplies zero.
+// Causal: units of keys after all of a wave's queries use LSE = +inf (P = 0
+// exactly); the diagonal unit sets its masked S to -inf. Each work-group
+// rounds its unit count up to the 8-unit unroll (padding units are zeros).
+// --------------------------------------------------------------------------
+template <int D, int NW>
+struct DqPipeTile {
+  static constexpr int BQ = 32 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int KT = 32;
+  static constexpr int TILE = KT * D;   // halves of the K (or V) unit
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NSTAGE = 8;
+  static constexpr int AHEAD = 5;
+};
+
+template <int D, int NW>
+constexpr bool dq_pipe_tiling_ok() {
+  using T = DqPipeTile<D, NW>;
+  constexpr int instr = T::TILE * 2 / 1024;
+  return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
+         2 * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && D <= 64;
+}
+
+#ifndef FA_DQ_LEAD
+#define FA_DQ_LEAD 3
+#endif
+
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+void dq_pipe_kernel(BwdArgs a) {
+  using T = DqPipeTile<D, NW>;
+  using Dma = DmaStager<D, T::KT, NW>;
+  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
+  constexpr int NS = T::NSTAGE;
+  constexpr int IPU = 2;  // this wave's DMA instructions per unit: K, V
+  __shared__ __attribute__((aligned(16))) half_t lds[NS * T::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ql = lane & 31;
+  const int g = lane >> 5;
+
+  const TileHead th = decode_block(blockIdx.x, a.BH);
+  const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
+  const int head = th.head;
+  const int b = head / a.Hq;
+  const int hq = head - b * a.Hq;
+  const int kvh = b * a.Hkv + hq / a.group;
+  const int N = a.N;
+  const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t aux = (uint32_t)N * 4u;
+  const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
+  const rsrc_t rdo = make_rsrc(a.dO + (int64_t)head * N * D, slab);
+  const rsrc_t rl = make_rsrc(a.lse + (int64_t)head * N, aux);
+  const rsrc_t rd = make_rsrc(a.delta + (int64_t)head * N, aux);
+  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
+  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
+
+  const int q0 = qtile * T::BQ;
+  const int q0w = q0 + 32 * wave;
+  const int qrow = q0w + ql;
+
+  // Q and -dO as B operands (column = query ql, d = 16*kk + 8*g .. +7).
+  half8 qf[D / 16], don[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u;
+    qf[kk] = __builtin_bit_cast(half8, buf_load_b128(rq, off));
+    don[kk] = -__builtin_bit_cast(half8, buf_load_b128(rdo, off));
+  }
+  const float lse = buf_load_f32(rl, (uint32_t)qrow * 4u);
+  const float delta = buf_load_f32(rd, (uint32_t)qrow * 4u);
+  wait_all_vm();
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(don[kk]));
+
+  const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
+  const int nunits = (kv_end + T::KT - 1) / T::KT;
+  const int npad = (nunits + NS - 1) / NS * NS;
+
+  Dma dma;
+  dma.init(wave, lane);
+  const uint32_t lds0 = lds_addr(lds);
+  int i_row = 0;  // first key row of the next unit to fetch
+  auto issue = [&](int slot) {
+    const int row0 = i_row < kv_end ? i_row : N;  // past the end: zeros
+    const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
+    const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %4\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+        "s_mov_b32 m0, %5\n\t"
+        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
+        : "memory");
+    i_row += T::KT;
+  };
+#pragma unroll
+  for (int u = 0; u < T::AHEAD; ++u) issue(u);
+
+  // The slot read as "unit -1" holds zeros (its dS' is zero too).
+  {
+    half_t* zs = lds + (NS - 1) * T::STAGE;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
+  }
+  // Units 0, 1, 2 landed (3, 4 in flight), zeros written.
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
+
+  int r_off[D / 16];  // row reads: row row_perm(ql), chunk 2*kk + g
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) r_off[kk] = swz_offset<D>(row_perm(ql), 2 * kk + g);
+  int t_off[D / 32][2];  // transposed reads (see read_tr)
+  {
+    const int grp = lane >> 4, i = lane & 15, r = i >> 2, qq = i & 3;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int col = 32 * db + 16 * (grp & 1) + 4 * qq;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 8 * g + r + 4 * h2;
+        t_off[db][h2] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
+      }
+    }
+  }
+  auto tr8 = [&](const half_t* base, int db) {
+    const half4 lo = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][0])));
+    const half4 hi = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + t_off[db][1])));
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
+    return v;
+  };
+
+  float16v dq[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dq[db][j] = 0.f;
+
+  const float c = a.c;
+  const float inf = __builtin_inff();
+  // Pipeline registers: S^T, dPd^T of the current unit; dS'^T of the previous one.
+  float16v s_cur, dp_cur;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    s_cur[j] = 0.f;
+    dp_cur[j] = delta;
+  }
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    s_cur = mfma32(*reinterpret_cast<const half8*>(lds + r_off[kk]), qf[kk], s_cur);
+    dp_cur = mfma32(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), don[kk], dp_cur);
+  }
+  half8 sa_prev[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sa_prev[h][e] = (half_t)0.f;
+
+  auto dq_mm = [&](const half_t* slot) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+        dq[db] = mfma32(tr8(slot + 16 * h * D, db), sa_prev[h], dq[db]);
+  };
+
+  int c_key = 0;  // first key of the unit the body works on
+
+  auto body = [&](auto slot_c) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
+    const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
+    const int ka = c_key;
+    c_key += T::KT;
+
+    float lse_u = lse;
+    if constexpr (CAUSAL) {
+      if (ka > q0w) {
+        lse_u = inf;  // every key of the unit follows every query of the wave
+      } else if (ka == q0w) {
+        // diagonal unit: key 16h + 8g + e (value j = 8h + e) is kept iff <= query ql
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (16 * (j >> 3) + 8 * g + (j & 7) > ql) s_cur[j] = -inf;
+      }
+    }
+
+    // Hand-ordered body: 3 * D/16 MFMA tasks in the order dQ (unit u-1),
+    // S^T, dPd^T (unit u+1), repeated; group i issues the LDS reads of task
+    // i + kLead, runs task i and part of unit u's vector work.
+    constexpr int NQ = D / 16;
+    constexpr int NTASK = 3 * NQ;
+    constexpr int kLead = FA_DQ_LEAD;
+    const half_t* k_nxt = nxt;
+    const half_t* v_nxt = nxt + T::TILE;
+    auto load_op = [&](auto t_c) -> half8 {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int kind = t % 3, q = t / 3;
+      constexpr int h = q / (D / 32), db = q % (D / 32);
+      if constexpr (kind == 0) return tr8(prv + 16 * h * D, db);
+      else if constexpr (kind == 1) return *reinterpret_cast<const half8*>(k_nxt + r_off[q]);
+      else return *reinterpret_cast<const half8*>(v_nxt + r_off[q]);
+    };
+    float16v s_nx, dp_nx;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s_nx[j] = 0.f;
+    auto run_task = [&](auto t_c, const half8& op) {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int kind = t % 3, q = t / 3;
+      constexpr int h = q / (D / 32), db = q % (D / 32);
+      if constexpr (kind == 0) dq[db] = mfma32(op, sa_prev[h], dq[db]);
+      else if constexpr (kind == 1) s_nx = mfma32(op, qf[q], s_nx);
+      else dp_nx = mfma32(op, don[q], dp_nx);
+    };
+    half8 sa[2];
+    float pexp[16];
+    // Vector work on value pairs in two stages placed in different groups:
+    //   A: p = exp2(s c - lse)      B: dS' = p dPd, packed to fp16.
+    auto stage_a = [&](int pr) {
+      float p2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -lse_u));
+      asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
+      pexp[2 * pr] = p2[0];
+      pexp[2 * pr + 1] = p2[1];
+    };
+    auto stage_b = [&](int pr) {
+      half2v ss;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) ss[e] = (half_t)(pexp[2 * pr + e] * dp_cur[2 * pr + e]);
+      asm volatile("" : "+v"(ss));
+      const int j = 2 * pr;
+      sa[j >> 3][j & 7] = ss[0];
+      sa[j >> 3][(j & 7) + 1] = ss[1];
+    };
+
+    half8 op[NTASK];
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(lse_u));
+    static_for<0, kLead>([&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dp_nx[j] = delta;
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NTASK>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(std::integral_constant<int, i + kLead>{});
+      run_task(i_c, op[i]);
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr) {
+        const int ga = (2 * pr * NTASK) / 16;
+        const int gb = ga + 1 < NTASK ? ga + 1 : NTASK - 1;
+        if (ga == i) stage_a(pr);
+        if (gb == i) stage_b(pr);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+
+    s_cur = s_nx;
+    dp_cur = dp_nx;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sa_prev[h] = sa[h];
+  };
+
+  auto step = [&](auto p_c) {
+    constexpr int P = decltype(p_c)::value;
+    issue((2 * P + 5) % NS);
+    issue((2 * P + 6) % NS);
+    body(std::integral_constant<int, 2 * P>{});
+    body(std::integral_constant<int, 2 * P + 1>{});
+    wait_vm_and_barrier<2 * IPU>();
+  };
+
+  static_assert(NS == 8, "the loop below is unrolled for 8 slots");
+  for (int u = 0; u < npad; u += NS) {
+    step(ic<0>{});
+    step(ic<1>{});
+    step(ic<2>{});
+    step(ic<3>{});
+  }
+  dq_mm(lds + (NS - 1) * T::STAGE);  // dQ of the last unit (slot 7)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const float nscale = -a.scale;  // accumulated -dS
+  const rsrc_t rdq = make_rsrc(a.dq + (int64_t)head * N * D, slab);
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const uint32_t off = (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u;
+      buf_store_b64(rdq, off,
+                    pack4_half(dq[db][4 * jq] * nscale, dq[db][4 * jq + 1] * nscale,
+                               dq[db][4 * jq + 2] * nscale, dq[db][4 * jq + 3] * nscale));
+    }
+}
+
+template <int D, bool CAUSAL, int NW>
+hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
+  using T = DqPipeTile<D, NW>;
+  BwdArgs b = a;
+  b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW>), dim3((unsigned)blocks), dim3(T::NT), 0,
+                     stream, b);
+  return hipGetLastError();
+}
+
 template <int D, bool CAUSAL, int NW, int TILE>
 constexpr void* dkdv_entry() {
   if constexpr (dkdv_tiling_ok<D, NW, TILE>())
@@ -1102,6 +1433,14 @@ constexpr void* dkdv_pipe_entry() {
   static_assert(TILE == 32, "the pipelined dK/dV kernel streams 32-query units");
   if constexpr (dkdv_pipe_tiling_ok<D, NW>())
     return (void*)&dkdv_pipe_launch<D, CAUSAL, NW>;
+  else
+    return nullptr;
+}
+template <int D, bool CAUSAL, int NW, int TILE>
+constexpr void* dq_pipe_entry() {
+  static_assert(TILE == 32, "the pipelined dQ kernel streams 32-key units");
+  if constexpr (dq_pipe_tiling_ok<D, NW>())
+    return (void*)&dq_pipe_launch<D, CAUSAL, NW>;
   else
     return nullptr;
 }
@@ -1136,6 +1475,7 @@ static const Variant kDqVariants[] = {
     FA_BWD_VARIANT(dq_entry, 4, 32),
     FA_BWD_VARIANT(dq_entry, 2, 64),
     FA_BWD_VARIANT(dq_entry, 8, 64),
+    FA_BWD_VARIANT(dq_pipe_entry, 4, 32),
 };
 
 const Variant* dkdv_variants(int* count) {
