@@ -45,10 +45,14 @@ struct FwdTile {
   static_assert(NSTAGE * STAGE * 2 <= 160 * 1024, "LDS budget");
 };
 
-// The running max only moves when a tile's max exceeds it by more than this
-// (log2 units): p = exp2(s - m) then stays <= 2^8, exact in fp16 and fp32,
-// and the O / l rescale is skipped for most tiles.
-constexpr float kRescaleThreshold = 8.0f;
+// Lazy reference max. P = exp2(s c - m) is first computed against the
+// current reference max m; a lane's row sum of P over the tile is at least
+// each of its P, so while every lane's sum stays <= 2^8 every P is <= 2^8
+// (exact in fp16 and fp32) and nothing else is done. Otherwise (and on the
+// first tile, where m = -inf gives inf / NaN sums) a rare branch computes the
+// tile max, moves m to it, rescales O and l, and recomputes P. The max is
+// thus only reduced when it is needed.
+constexpr float kSumLimit = 256.0f;
 
 template <int V>
 using ic = std::integral_constant<int, V>;
@@ -210,39 +214,55 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
             if (!ok) sc[kb][j] = -INFINITY;
           }
       }
-      float mx4[4];
+      half8 pk[KB][2];
+      // P against the current reference max, and this lane's row sum.
+      auto probs = [&](const float16v* s) {
+        const float nm = -m;
+        float ls4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 4; ++u) mx4[u] = fmaxf(sc[0][4 * u], sc[0][4 * u + 1]);
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+          for (int j = 0; j < 16; ++j) {
+            const float p = exp2_fast(fmaf(s[kb][j], c, nm));
+            ls4[j & 3] += p;
+            pk[kb][j >> 3][j & 7] = (half_t)p;
+          }
+        return (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);
+      };
+      float lt = probs(sc);
+      if (__builtin_amdgcn_ballot_w64(!(lt <= kSumLimit)) != 0) {
+        // Rare: the scores are rebuilt from the K tile (still in this slot)
+        // rather than kept alive across the common path.
+        float16v s2[KB];
+        const half_t* Ks = lds + SLOT * T::STAGE;
 #pragma unroll
-        for (int j = (kb == 0 ? 2 : 0); j < 4; ++j)
+        for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) mx4[u] = fmaxf(mx4[u], sc[kb][4 * u + j]);
-      float mx = fmaxf(fmaxf(mx4[0], mx4[1]), fmaxf(mx4[2], mx4[3]));
-      mx = halves_max(mx) * c;
-      // Move the reference max only when it grew by more than the threshold
-      // for some lane of the wave (always on the first active tile).
-      if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleThreshold) != 0) {
+          for (int j = 0; j < 16; ++j) s2[kb][j] = 0.f;
+#pragma unroll
+          for (int kk = 0; kk < D / 16; ++kk)
+            s2[kb] = mfma32(*reinterpret_cast<const half8*>(Ks + 32 * kb * D + k_off[kk]), qf[kk],
+                            s2[kb]);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = kv0 + 32 * kb + result_row(j, g);
+            if (need_mask && (key >= N || (CAUSAL && key > qrow))) s2[kb][j] = -INFINITY;
+            mx = fmaxf(mx, s2[kb][j]);
+          }
+        mx = halves_max(mx) * c;
         const float m_new = fmaxf(m, mx);
         const float alpha = exp2_fast(m - m_new);
         l *= alpha;
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
         m = m_new;
+        lt = probs(s2);
       }
-      const float nm = -m;
-      half8 pk[KB][2];
-      float ls4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float p = exp2_fast(fmaf(sc[kb][j], c, nm));
-          ls4[j & 3] += p;
-          pk[kb][j >> 3][j & 7] = (half_t)p;
-        }
-      l += (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);
+      l += lt;
       // O^T += V^T P^T
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
@@ -284,6 +304,367 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
       buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u, v);
     }
   if (g == 0 && qrow < N) a.lse[(int64_t)head * N + qrow] = m + log2_fast(lt);
+}
+
+// ---------------------------------------------------------------------------
+// Software-pipelined forward over 32-key units.
+//
+// Work-group: NW waves x 32 queries (Q as MFMA B operand), 32-key units (K,
+// V rows) streamed through an 8-slot LDS DMA ring, two units per barrier
+// step. The body of unit u runs
+//   vector work of unit u      P^T = exp2(S^T c - m), its row sums, fp16 P^T
+//   matrix work of unit u + 1  S^T = K Q^T
+//   matrix work of unit u - 1  O^T += V^T P^T        (V^T via transposing reads)
+// P is computed against the current reference max m (see kSumLimit); only
+// when a row sum exceeds the limit (rare after the first unit) does a branch
+// after the body reduce the tile max, rescale O and l and recompute P of
+// unit u against the new max. Causal units whose keys all follow the
+// wave's queries use m = +inf (P = 0 exactly); the diagonal and the tail unit
+// set their masked S to -inf first. Each work-group rounds its unit count up
+// to the 8-unit unroll; padding units are masked the same way.
+// ---------------------------------------------------------------------------
+template <int D, int NW>
+struct FwdPipeTile {
+  static constexpr int BM = 32 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int KT = 32;
+  static constexpr int TILE = KT * D;  // halves of the K (or V) unit
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NSTAGE = 8;
+  static constexpr int AHEAD = 5;
+};
+
+template <int D, int NW>
+constexpr bool fwd_pipe_tiling_ok() {
+  using T = FwdPipeTile<D, NW>;
+  constexpr int instr = T::TILE * 2 / 1024;
+  return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
+         2 * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && D <= 64;
+}
+
+#ifndef FA_FWD_LEAD
+#define FA_FWD_LEAD 3
+#endif
+
+template <int V>
+using fic = std::integral_constant<int, V>;
+
+// f(integral_constant<int, I>) for I = B .. E-1, fully unrolled.
+template <int B, int E, typename F>
+__device__ __forceinline__ void fwd_static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    fwd_static_for<B + 1, E>(f);
+  }
+}
+
+template <int D, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+void fwd_pipe_kernel(FwdArgs a) {
+  using T = FwdPipeTile<D, NW>;
+  using Dma = DmaStager<D, T::KT, NW>;
+  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
+  constexpr int NS = T::NSTAGE;
+  constexpr int IPU = 2;  // this wave's DMA instructions per unit: K, V
+  __shared__ __attribute__((aligned(16))) half_t lds[NS * T::STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ql = lane & 31;
+  const int g = lane >> 5;
+
+  const TileHead th = decode_block(blockIdx.x, a.BH);
+  const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
+  const int head = th.head;
+  const int b = head / a.Hq;
+  const int hq = head - b * a.Hq;
+  const int kvh = b * a.Hkv + hq / a.group;
+  const int N = a.N;
+  const uint32_t slab = (uint32_t)N * D * 2u;
+  const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
+  const rsrc_t ro = make_rsrc(a.o + (int64_t)head * N * D, slab);
+  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
+  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
+
+  const int q0 = qtile * T::BM;
+  const int q0w = q0 + 32 * wave;
+  const int qrow = q0w + ql;
+
+  // Q^T operand fragments: lane (query ql, k-half g), d = 16*kk + 8*g .. +7.
+  half8 qf[D / 16];
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    qf[kk] = __builtin_bit_cast(half8, buf_load_b128(rq, (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u));
+  wait_all_vm();
+
+  const int kv_end = CAUSAL ? min(N, q0 + T::BM) : N;
+  const int nunits = (kv_end + T::KT - 1) / T::KT;
+  const int npad = (nunits + NS - 1) / NS * NS;
+
+  Dma dma;
+  dma.init(wave, lane);
+  const uint32_t lds0 = lds_addr(lds);
+  int i_row = 0;  // first key row of the next unit to fetch
+  auto issue = [&](int slot) {
+    const int row0 = i_row < kv_end ? i_row : N;  // past the end: zeros
+    const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
+    const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %4\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+        "s_mov_b32 m0, %5\n\t"
+        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
+        : "memory");
+    i_row += T::KT;
+  };
+#pragma unroll
+  for (int u = 0; u < T::AHEAD; ++u) issue(u);
+
+  // The V tile read as "unit -1" holds zeros (its P is zero too).
+  {
+    half_t* zs = lds + (NS - 1) * T::STAGE + T::TILE;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
+  }
+  // Units 0, 1, 2 landed (3, 4 in flight), zeros written.
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
+
+  int k_off[D / 16];  // row reads of K: row row_perm(ql), chunk 2*kk + g
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) k_off[kk] = swz_offset<D>(row_perm(ql), 2 * kk + g);
+  int v_off[D / 32][2];  // transposed reads of V (see read_tr)
+  {
+    const int grp = lane >> 4, i = lane & 15, r = i >> 2, qq = i & 3;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int col = 32 * db + 16 * (grp & 1) + 4 * qq;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int row = 8 * g + r + 4 * h2;
+        v_off[db][h2] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
+      }
+    }
+  }
+  auto tr8 = [&](const half_t* base, int db) {
+    const half4 lo = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + v_off[db][0])));
+    const half4 hi = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + v_off[db][1])));
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
+    return v;
+  };
+
+  float16v o[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[db][j] = 0.f;
+  float m = -INFINITY;  // reference max (scaled, log2 units); may lag the true max by <= 8
+  float l = 0.f;        // this lane's partial sum of exp2(s*c - m) (its half of each unit's keys)
+  const float c = a.c;
+  const float inf = __builtin_inff();
+
+  // Pipeline registers: S^T of the current unit, P^T of the previous one.
+  float16v s_cur;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s_cur[j] = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    s_cur = mfma32(*reinterpret_cast<const half8*>(lds + k_off[kk]), qf[kk], s_cur);
+  half8 pa_prev[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pa_prev[h][e] = (half_t)0.f;
+
+  auto pv = [&](const half_t* slot) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+        o[db] = mfma32(tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h], o[db]);
+  };
+
+  int c_key = 0;  // first key of the unit the body works on
+
+  auto body = [&](auto slot_c) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
+    const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
+    const int ka = c_key;
+    c_key += T::KT;
+
+    // Unit modes (wave-uniform): keys all past the queries (or past N), or
+    // a diagonal / tail unit whose masked scores become -inf.
+    const bool dead = (CAUSAL && ka > q0w) || ka >= N;
+    float m_eff = dead ? inf : m;
+    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > N)) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = ka + result_row(j, g);
+        if (key >= N || (CAUSAL && key > qrow)) s_cur[j] = -inf;
+      }
+    }
+
+    // Hand-ordered body: D/16 S tasks (unit u+1) and D/16 O tasks (unit
+    // u-1), alternating; group i issues the LDS reads of task i + kLead,
+    // runs task i and part of unit u's vector work; fences keep the order.
+    constexpr int NQ = D / 16;
+    constexpr int NTASK = 2 * NQ;
+    constexpr int kLead = FA_FWD_LEAD;
+    auto load_op = [&](auto t_c) -> half8 {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int q = t / 2;
+      constexpr int h = q / (D / 32), db = q % (D / 32);
+      if constexpr (t % 2 == 0) return *reinterpret_cast<const half8*>(nxt + k_off[q]);
+      else return tr8(prv + T::TILE + 16 * h * D, db);
+    };
+    float16v s_nx;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s_nx[j] = 0.f;
+    auto run_task = [&](auto t_c, const half8& op) {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int q = t / 2;
+      constexpr int h = q / (D / 32), db = q % (D / 32);
+      if constexpr (t % 2 == 0) s_nx = mfma32(op, qf[q], s_nx);
+      else o[db] = mfma32(op, pa_prev[h], o[db]);
+    };
+    half8 pa[2];
+    float pexp[16];
+    float lsum[2] = {0.f, 0.f};
+    // Vector work on value pairs in two stages placed in different groups:
+    //   A: p = exp2(s c - m)        B: row sums, fp16 P^T.
+    auto stage_a = [&](int pr) {
+      float p2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -m_eff));
+      asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
+      pexp[2 * pr] = p2[0];
+      pexp[2 * pr + 1] = p2[1];
+    };
+    auto stage_b = [&](int pr) {
+      half2v pp;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        lsum[e] += pexp[2 * pr + e];
+        pp[e] = (half_t)pexp[2 * pr + e];
+      }
+      asm volatile("" : "+v"(pp));
+      const int j = 2 * pr;
+      pa[j >> 3][j & 7] = pp[0];
+      pa[j >> 3][(j & 7) + 1] = pp[1];
+    };
+
+    half8 op[NTASK];
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(m_eff));
+    fwd_static_for<0, (kLead < NTASK ? kLead : NTASK)>(
+        [&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+    __builtin_amdgcn_sched_barrier(0);
+    fwd_static_for<0, NTASK>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(fic<i + kLead>{});
+      run_task(i_c, op[i]);
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr) {
+        const int ga = (2 * pr * NTASK) / 16;
+        const int gb = ga + 1 < NTASK ? ga + 1 : NTASK - 1;
+        if (ga == i) stage_a(pr);
+        if (gb == i) stage_b(pr);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+
+    // Row sum of unit u; a rare branch moves the reference max.
+    float l_u = lsum[0] + lsum[1];
+    if (!dead && __builtin_amdgcn_ballot_w64(!(l_u <= kSumLimit)) != 0) {
+      float mt = s_cur[0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) mt = __builtin_fmaxf(mt, s_cur[j]);
+      mt = halves_max(mt) * c;
+      const float m_new = __builtin_fmaxf(m, mt);
+      const float alpha = exp2_fast(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) o[db] *= alpha;
+      m = m_new;
+      l_u = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float p = exp2_fast(fmaf(s_cur[j], c, -m));
+        l_u += p;
+        pa[j >> 3][j & 7] = (half_t)p;
+      }
+    }
+    l += l_u;
+
+    s_cur = s_nx;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) pa_prev[h] = pa[h];
+  };
+
+  auto step = [&](auto p_c) {
+    constexpr int P = decltype(p_c)::value;
+    issue((2 * P + 5) % NS);
+    issue((2 * P + 6) % NS);
+    body(fic<2 * P>{});
+    body(fic<2 * P + 1>{});
+    wait_vm_and_barrier<2 * IPU>();
+  };
+
+  static_assert(NS == 8, "the loop below is unrolled for 8 slots");
+  for (int u = 0; u < npad; u += NS) {
+    step(fic<0>{});
+    step(fic<1>{});
+    step(fic<2>{});
+    step(fic<3>{});
+  }
+  pv(lds + (NS - 1) * T::STAGE);  // O of the last unit (slot 7)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Epilogue: lane (query qrow, half g) holds d = 32*db + 8*(j/4) + 4*g + j%4.
+  const float lt = halves_sum(l);
+  const float invl = 1.0f / lt;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const u32x2 v = pack4_half(o[db][4 * jq] * invl, o[db][4 * jq + 1] * invl,
+                                 o[db][4 * jq + 2] * invl, o[db][4 * jq + 3] * invl);
+      buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u, v);
+    }
+  if (g == 0 && qrow < N) a.lse[(int64_t)head * N + qrow] = m + log2_fast(lt);
+}
+
+template <int D, bool CAUSAL, int NW>
+hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
+  using T = FwdPipeTile<D, NW>;
+  FwdArgs b = a;
+  b.num_tiles = (a.N + T::BM - 1) / T::BM;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW>), dim3((unsigned)blocks), dim3(T::NT), 0,
+                     stream, b);
+  return hipGetLastError();
+}
+
+template <int D, bool CAUSAL, int NW>
+constexpr void* fwd_pipe_entry() {
+  if constexpr (fwd_pipe_tiling_ok<D, NW>())
+    return (void*)&fwd_pipe_launch<D, CAUSAL, NW>;
+  else
+    return nullptr;
 }
 
 template <int D, bool CAUSAL, int NW, int BN>
@@ -330,6 +711,10 @@ static const Variant kFwdVariants[] = {
     FA_FWD_VARIANT(4, 32),
     FA_FWD_VARIANT(2, 64),
     FA_FWD_VARIANT(4, 128),
+    {4, 128, 32,
+     {{fwd_pipe_entry<32, false, 4>(), fwd_pipe_entry<32, true, 4>()},
+      {fwd_pipe_entry<64, false, 4>(), fwd_pipe_entry<64, true, 4>()},
+      {fwd_pipe_entry<128, false, 4>(), fwd_pipe_entry<128, true, 4>()}}},
 };
 
 const Variant* fwd_variants(int* count) {
