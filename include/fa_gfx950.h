@@ -12,6 +12,7 @@
  *   fa_bwd_preprocess  replaces  _attn_bwd_preprocess[grid](...)  attention.py:736-744
  *   fa_bwd_dkdv        replaces  _attn_bwd[grid](...) phase 1     attention.py:754-770 (kernel 428-505)
  *   fa_bwd_dq          replaces  _attn_bwd[grid](...) phase 2     attention.py:754-770 (kernel 507-573)
+ *   fa_bwd_dq_delta    replaces  _attn_bwd_preprocess + phase 2   attention.py:736-744, 754-770
  *
  * Conventions shared by every entry point
  *   - Tensors are caller-owned device memory, contiguous, row-major:
@@ -110,6 +111,19 @@ int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
               fa_half_t* dq,
               int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
               float scale, int causal, void* stream);
+
+/* delta = rowsum(o * dO) (as fa_bwd_preprocess) and dq (as fa_bwd_dq with that
+ * delta) in one call: the reference's _attn_bwd_preprocess launch
+ * (attention.py:736-744) folded into phase 2 of its _attn_bwd launch
+ * (attention.py:754-770, kernel 507-573). When the selected dQ tiling computes
+ * delta itself this is a single launch; otherwise it is the two launches in
+ * order. delta is written before dq is; a dK/dV call that reads delta may
+ * follow on the same stream. */
+int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                    const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                    float* delta, fa_half_t* dq,
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                    float scale, int causal, void* stream);
 
 /* Thread-local description of the last failure on the calling thread
  * ("" if none). The pointer stays valid until the next call on the thread. */

@@ -98,6 +98,15 @@ def test_backward_entry_points_reject_bad_arguments(lib):
     assert rc == _lib.FA_ERR_HEAD_DIM
     rc = lib.fa_bwd_dq(P, P, P, P, P, P + 8, P, 1, 4, 2, 64, 64, 0.125, 1, None)
     assert rc == _lib.FA_ERR_MISALIGNED
+    rc = lib.fa_bwd_dq_delta(P, P, P, P, P, P, None, P, 1, 4, 2, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_NULL_POINTER
+    rc = lib.fa_bwd_dq_delta(P, P, P, P, P, P, P, P, 1, 4, 3, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE
+    rc = lib.fa_bwd_dq_delta(P, P, P, P + 8, P, P, P, P, 1, 4, 2, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_MISALIGNED
+    assert "fa_bwd_dq_delta" in _lib.last_error()
+    rc = lib.fa_bwd_dq_delta(P, P, P, P, P, P, P, P, 1, 4, 2, 64, 64, -1.0, 1, None)
+    assert rc == _lib.FA_ERR_BAD_SCALE
     rc = lib.fa_bwd_preprocess(P, P, None, 1, 1, 8, 64, None)
     assert rc == _lib.FA_ERR_NULL_POINTER
     rc = lib.fa_bwd_preprocess(P, P, P, 1, 1, 8, 40, None)

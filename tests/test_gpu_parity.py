@@ -270,6 +270,33 @@ def test_every_tiling_variant_matches_oracle(head_dim, causal):
                 _lib.set_tiling(kind, D, causal, -1)
 
 
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_fused_delta_matches_separate_launches(head_dim):
+    """fa_bwd_dq_delta (Delta inside the dQ launch where the tiling supports
+    it, else preprocess + dQ) agrees with fa_bwd_preprocess followed by
+    fa_bwd_dq, for the default tiling and for another compiled tiling."""
+    B, Hq, Hkv, N, D = 2, 4, 2, 333, head_dim
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=31, mult=0.5))
+    scale = D ** -0.5
+    for causal in (False, True):
+        o, lse = _ops.flash_fwd(q, k, v, causal, scale)
+        delta_ref = _ops.flash_bwd_preprocess(o, do)
+        dq_ref = _ops.flash_bwd_dq(q, k, v, do, lse, delta_ref, causal, scale)
+        default = _lib.get_tiling(_lib.KERNEL_DQ, D, causal)["variant"]
+        other = [t["variant"] for t in _lib.tiling_variants(_lib.KERNEL_DQ, D, causal)
+                 if t["variant"] != default][0]  # a classic tiling: preprocess + dQ
+        for variant in (-1, other):
+            _lib.set_tiling(_lib.KERNEL_DQ, D, causal, variant)
+            try:
+                delta, dq = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, causal, scale)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_DQ, D, causal, -1)
+            torch.cuda.synchronize()
+            tag = f"D={D} causal={causal} dq variant {variant}"
+            torch.testing.assert_close(delta, delta_ref, rtol=1e-5, atol=1e-5, msg=tag)
+            assert_close(f"{tag} dq", dq.float(), dq_ref.float(), max_abs=2e-3, rel_l2=1e-3)
+
+
 def test_deterministic_backward():
     q, k, v, do = make_inputs(2, 8, 2, 333, 64, seed=9)
     a = run_kernel(q, k, v, do, True)

@@ -1174,7 +1174,24 @@ void dq_pipe_kernel(BwdArgs a) {
     don[kk] = -__builtin_bit_cast(half8, buf_load_b128(rdo, off));
   }
   const float lse = buf_load_f32(rl, (uint32_t)qrow * 4u);
-  const float delta = buf_load_f32(rd, (uint32_t)qrow * 4u);
+  float delta;
+  if (a.o != nullptr) {
+    // Delta = rowsum(O * dO) of this lane's query (the halves g = 0, 1 hold
+    // the two 8-wide halves of every 16-wide chunk of the row).
+    const rsrc_t ro = make_rsrc(a.o + (int64_t)head * N * D, slab);
+    float part = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const half8 ov = __builtin_bit_cast(
+          half8, buf_load_b128(ro, (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf((float)ov[e], -(float)don[kk][e], part);
+    }
+    delta = halves_sum(part);
+    if (g == 0 && qrow < N) a.delta_out[(int64_t)head * N + qrow] = delta;
+  } else {
+    delta = buf_load_f32(rd, (uint32_t)qrow * 4u);
+  }
   wait_all_vm();
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(don[kk]));
@@ -1452,30 +1469,31 @@ constexpr void* dq_entry() {
     return nullptr;
 }
 
-#define FA_BWD_VARIANT(ENTRY, NW, TILE)                                         \
+#define FA_BWD_VARIANT(ENTRY, NW, TILE, FLAGS)                                  \
   {                                                                             \
     NW, 32 * NW, TILE,                                                          \
     {                                                                           \
       {ENTRY<32, false, NW, TILE>(), ENTRY<32, true, NW, TILE>()},              \
       {ENTRY<64, false, NW, TILE>(), ENTRY<64, true, NW, TILE>()},              \
       {ENTRY<128, false, NW, TILE>(), ENTRY<128, true, NW, TILE>()},            \
-    }                                                                           \
+    },                                                                          \
+    FLAGS                                                                       \
   }
 
 static const Variant kDkdvVariants[] = {
-    FA_BWD_VARIANT(dkdv_entry, 4, 64),
-    FA_BWD_VARIANT(dkdv_entry, 4, 32),
-    FA_BWD_VARIANT(dkdv_entry, 2, 64),
-    FA_BWD_VARIANT(dkdv_entry, 8, 64),
-    FA_BWD_VARIANT(dkdv_pipe_entry, 4, 32),
+    FA_BWD_VARIANT(dkdv_entry, 4, 64, 0),
+    FA_BWD_VARIANT(dkdv_entry, 4, 32, 0),
+    FA_BWD_VARIANT(dkdv_entry, 2, 64, 0),
+    FA_BWD_VARIANT(dkdv_entry, 8, 64, 0),
+    FA_BWD_VARIANT(dkdv_pipe_entry, 4, 32, 0),
 };
 
 static const Variant kDqVariants[] = {
-    FA_BWD_VARIANT(dq_entry, 4, 64),
-    FA_BWD_VARIANT(dq_entry, 4, 32),
-    FA_BWD_VARIANT(dq_entry, 2, 64),
-    FA_BWD_VARIANT(dq_entry, 8, 64),
-    FA_BWD_VARIANT(dq_pipe_entry, 4, 32),
+    FA_BWD_VARIANT(dq_entry, 4, 64, 0),
+    FA_BWD_VARIANT(dq_entry, 4, 32, 0),
+    FA_BWD_VARIANT(dq_entry, 2, 64, 0),
+    FA_BWD_VARIANT(dq_entry, 8, 64, 0),
+    FA_BWD_VARIANT(dq_pipe_entry, 4, 32, kFusesDelta),
 };
 
 const Variant* dkdv_variants(int* count) {

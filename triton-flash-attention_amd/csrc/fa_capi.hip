@@ -142,6 +142,8 @@ fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
   a.scale = scale;
   a.nsplit = 1;
   a.part = nullptr;
+  a.o = nullptr;
+  a.delta_out = nullptr;
   return a;
 }
 
@@ -290,6 +292,34 @@ int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const 
   a.dq = reinterpret_cast<fa::half_t*>(dq);
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
   return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_bwd_dq launch");
+}
+
+int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                    const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
+                    fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                    float scale, int causal, void* stream) {
+  if (!q || !k || !v || !o || !dO || !lse || !delta || !dq)
+    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dq_delta: null pointer");
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  if ((rc = check_aligned("fa_bwd_dq_delta", {q, k, v, o, dO, lse, delta, dq}))) return rc;
+  if ((rc = check_scale(scale))) return rc;
+  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq_delta: no kernel for the selected tiling");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  a.dq = reinterpret_cast<fa::half_t*>(dq);
+  if (var->flags & fa::kFusesDelta) {
+    a.o = reinterpret_cast<const fa::half_t*>(o);
+    a.delta_out = delta;
+  } else {
+    hipError_t e = fa::launch_preprocess(reinterpret_cast<const fa::half_t*>(o),
+                                         reinterpret_cast<const fa::half_t*>(dO), delta,
+                                         B * Hq * N, (int)D, s);
+    if (e != hipSuccess) return hip_result(e, "fa_bwd_dq_delta preprocess launch");
+  }
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
+  return hip_result(fn(a, s), "fa_bwd_dq_delta launch");
 }
 
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4) {

@@ -702,7 +702,8 @@ constexpr void* fwd_entry() {
       {fwd_entry<32, false, NW, BN>(), fwd_entry<32, true, NW, BN>()},          \
       {fwd_entry<64, false, NW, BN>(), fwd_entry<64, true, NW, BN>()},          \
       {fwd_entry<128, false, NW, BN>(), fwd_entry<128, true, NW, BN>()},        \
-    }                                                                           \
+    },                                                                          \
+    0                                                                           \
   }
 
 static const Variant kFwdVariants[] = {
@@ -714,7 +715,8 @@ static const Variant kFwdVariants[] = {
     {4, 128, 32,
      {{fwd_pipe_entry<32, false, 4>(), fwd_pipe_entry<32, true, 4>()},
       {fwd_pipe_entry<64, false, 4>(), fwd_pipe_entry<64, true, 4>()},
-      {fwd_pipe_entry<128, false, 4>(), fwd_pipe_entry<128, true, 4>()}}},
+      {fwd_pipe_entry<128, false, 4>(), fwd_pipe_entry<128, true, 4>()}},
+     0},
 };
 
 const Variant* fwd_variants(int* count) {

@@ -51,6 +51,11 @@ struct BwdArgs {
   // writes fp32 partials part[split][B*Hkv][N][D] (dK then dV planes).
   int nsplit;
   float* part;
+  // Fused Delta (dQ kernels whose variant has kFusesDelta): when o is set the
+  // kernel computes Delta = rowsum(O * dO) itself and writes it to delta_out
+  // instead of reading delta.
+  const half_t* o;
+  float* delta_out;
 };
 
 enum KernelKind { kFwd = 0, kDkdv = 1, kDq = 2, kNumKinds = 3 };
@@ -66,7 +71,11 @@ struct Variant {
   int rows;
   int tile;
   void* fn[3][2];  // [D index: 32, 64, 128][causal]
+  int flags;       // kFusesDelta
 };
+
+// The dQ variant can compute Delta itself (BwdArgs::o / delta_out).
+constexpr int kFusesDelta = 1;
 
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);

@@ -52,6 +52,10 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _INT,
         (_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P),
     ),
+    "fa_bwd_dq_delta": (
+        _INT,
+        (_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P),
+    ),
     "fa_last_error": (ctypes.c_char_p, ()),
     "fa_abi_version": (_INT, ()),
     "fa_get_tiling": (_INT, (_INT, _I64, _INT, _INT_P)),

@@ -11,6 +11,7 @@ Reference launches replaced (triton_flash_attention/attention.py):
     flash_bwd_preprocess -> _attn_bwd_preprocess[grid]   736-744
     flash_bwd_dkdv       -> _attn_bwd[grid], phase 1     754-770 (428-505)
     flash_bwd_dq         -> _attn_bwd[grid], phase 2     754-770 (507-573)
+    flash_bwd_dq_delta   -> preprocess + phase 2         736-744, 754-770
 """
 
 from __future__ import annotations
@@ -207,11 +208,34 @@ def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.T
     return dq
 
 
+def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
+    """Delta [B,H,N] fp32 = rowsum(O * dO) and dQ [B,Hq,N,D] fp16 in one call
+    (one launch when the dQ tiling computes Delta itself)."""
+    B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
+    _require(o, "o", torch.float16, q.device)
+    if o.shape != q.shape:
+        raise ValueError("o must have the shape of q")
+    delta = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
+    _check_bwd_inputs(q, k, v, do, lse, delta)
+    q, k, v, o, do, lse = _aligned_all(q, k, v, o, do, lse)
+    lib = _lib.load()
+    dq = torch.empty_like(q)
+    with torch.cuda.device(q.device):
+        rc = _launch(
+            "dq", lib.fa_bwd_dq_delta,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+            lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+        )
+    _lib.check(rc)
+    return delta, dq
+
+
 def flash_bwd(
     q, k, v, o, lse, do, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """dQ, dK, dV: preprocess, then the dK/dV and dQ kernels."""
-    delta = flash_bwd_preprocess(o, do)
+    """dQ, dK, dV: dQ together with Delta (the reference's preprocess), then
+    dK/dV, which reads that Delta."""
+    delta, dq = flash_bwd_dq_delta(q, k, v, o, do, lse, causal, scale)
     dk, dv = flash_bwd_dkdv(q, k, v, do, lse, delta, causal, scale)
-    dq = flash_bwd_dq(q, k, v, do, lse, delta, causal, scale)
     return dq, dk, dv
