@@ -323,23 +323,27 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 // set their masked S to -inf first. Each work-group rounds its unit count up
 // to the 8-unit unroll; padding units are masked the same way.
 // ---------------------------------------------------------------------------
-template <int D, int NW>
+// UPS = units per barrier step: 2 (8-slot ring, 64 KiB at D = 64, two
+// work-groups per CU) or 1 (6-slot ring, 48 KiB, three work-groups per CU).
+template <int D, int NW, int UPS>
 struct FwdPipeTile {
   static constexpr int BM = 32 * NW;
   static constexpr int NT = 64 * NW;
   static constexpr int KT = 32;
   static constexpr int TILE = KT * D;  // halves of the K (or V) unit
   static constexpr int STAGE = 2 * TILE;
-  static constexpr int NSTAGE = 8;
-  static constexpr int AHEAD = 5;
+  static constexpr int NSTAGE = UPS == 2 ? 8 : 6;
+  static constexpr int AHEAD = UPS == 2 ? 5 : 4;  // units issued before step 0
+  static constexpr int WGS_PER_CU = UPS == 2 ? 2 : 3;
+  static_assert(UPS == 1 || UPS == 2, "units per step");
 };
 
-template <int D, int NW>
+template <int D, int NW, int UPS>
 constexpr bool fwd_pipe_tiling_ok() {
-  using T = FwdPipeTile<D, NW>;
+  using T = FwdPipeTile<D, NW, UPS>;
   constexpr int instr = T::TILE * 2 / 1024;
   return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
-         2 * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && D <= 64;
+         T::WGS_PER_CU * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && D <= 64;
 }
 
 #ifndef FA_FWD_LEAD
@@ -358,10 +362,16 @@ __device__ __forceinline__ void fwd_static_for(F&& f) {
   }
 }
 
-template <int D, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+template <int N, typename F>
+__device__ __forceinline__ void static_for_fwd_issue(F&& f) {
+  fwd_static_for<0, N>(f);
+}
+
+template <int D, bool CAUSAL, int NW, int UPS>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS>::WGS_PER_CU)))
 void fwd_pipe_kernel(FwdArgs a) {
-  using T = FwdPipeTile<D, NW>;
+  using T = FwdPipeTile<D, NW, UPS>;
   using Dma = DmaStager<D, T::KT, NW>;
   static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
   constexpr int NS = T::NSTAGE;
@@ -432,7 +442,7 @@ void fwd_pipe_kernel(FwdArgs a) {
     const u32x4 z = {0u, 0u, 0u, 0u};
     for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
   }
-  // Units 0, 1, 2 landed (3, 4 in flight), zeros written.
+  // Units 0 .. AHEAD-3 landed (the last two in flight), zeros written.
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
 
   int k_off[D / 16];  // row reads of K: row row_perm(ql), chunk 2*kk + g
@@ -614,23 +624,23 @@ void fwd_pipe_kernel(FwdArgs a) {
     for (int h = 0; h < 2; ++h) pa_prev[h] = pa[h];
   };
 
+  // One barrier step: UPS units; issues the units AHEAD.. ahead into the
+  // slots of units finished before the last barrier, then waits for all but
+  // the two most recent units (the next step reads up to 2 units ahead).
   auto step = [&](auto p_c) {
     constexpr int P = decltype(p_c)::value;
-    issue((2 * P + 5) % NS);
-    issue((2 * P + 6) % NS);
-    body(fic<2 * P>{});
-    body(fic<2 * P + 1>{});
+    static_for_fwd_issue<UPS>([&](auto e_c) {
+      issue((UPS * P + T::AHEAD + decltype(e_c)::value) % NS);
+    });
+    static_for_fwd_issue<UPS>([&](auto e_c) { body(fic<UPS * P + decltype(e_c)::value>{}); });
     wait_vm_and_barrier<2 * IPU>();
   };
 
-  static_assert(NS == 8, "the loop below is unrolled for 8 slots");
+  static_assert(NS % UPS == 0, "whole steps per ring turn");
   for (int u = 0; u < npad; u += NS) {
-    step(fic<0>{});
-    step(fic<1>{});
-    step(fic<2>{});
-    step(fic<3>{});
+    fwd_static_for<0, NS / UPS>([&](auto p_c) { step(p_c); });
   }
-  pv(lds + (NS - 1) * T::STAGE);  // O of the last unit (slot 7)
+  pv(lds + (NS - 1) * T::STAGE);  // O of the last unit (the ring's last slot)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // Epilogue: lane (query qrow, half g) holds d = 32*db + 8*(j/4) + 4*g + j%4.
@@ -647,22 +657,22 @@ void fwd_pipe_kernel(FwdArgs a) {
   if (g == 0 && qrow < N) a.lse[(int64_t)head * N + qrow] = m + log2_fast(lt);
 }
 
-template <int D, bool CAUSAL, int NW>
+template <int D, bool CAUSAL, int NW, int UPS>
 hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
-  using T = FwdPipeTile<D, NW>;
+  using T = FwdPipeTile<D, NW, UPS>;
   FwdArgs b = a;
   b.num_tiles = (a.N + T::BM - 1) / T::BM;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW>), dim3((unsigned)blocks), dim3(T::NT), 0,
-                     stream, b);
+  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS>), dim3((unsigned)blocks), dim3(T::NT),
+                     0, stream, b);
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, int NW>
+template <int D, bool CAUSAL, int NW, int UPS>
 constexpr void* fwd_pipe_entry() {
-  if constexpr (fwd_pipe_tiling_ok<D, NW>())
-    return (void*)&fwd_pipe_launch<D, CAUSAL, NW>;
+  if constexpr (fwd_pipe_tiling_ok<D, NW, UPS>())
+    return (void*)&fwd_pipe_launch<D, CAUSAL, NW, UPS>;
   else
     return nullptr;
 }
@@ -713,9 +723,14 @@ static const Variant kFwdVariants[] = {
     FA_FWD_VARIANT(2, 64),
     FA_FWD_VARIANT(4, 128),
     {4, 128, 32,
-     {{fwd_pipe_entry<32, false, 4>(), fwd_pipe_entry<32, true, 4>()},
-      {fwd_pipe_entry<64, false, 4>(), fwd_pipe_entry<64, true, 4>()},
-      {fwd_pipe_entry<128, false, 4>(), fwd_pipe_entry<128, true, 4>()}},
+     {{fwd_pipe_entry<32, false, 4, 2>(), fwd_pipe_entry<32, true, 4, 2>()},
+      {fwd_pipe_entry<64, false, 4, 2>(), fwd_pipe_entry<64, true, 4, 2>()},
+      {fwd_pipe_entry<128, false, 4, 2>(), fwd_pipe_entry<128, true, 4, 2>()}},
+     0},
+    {4, 128, 32,
+     {{fwd_pipe_entry<32, false, 4, 1>(), fwd_pipe_entry<32, true, 4, 1>()},
+      {fwd_pipe_entry<64, false, 4, 1>(), fwd_pipe_entry<64, true, 4, 1>()},
+      {fwd_pipe_entry<128, false, 4, 1>(), fwd_pipe_entry<128, true, 4, 1>()}},
      0},
 };
 
