@@ -454,15 +454,20 @@ struct DkdvPipeTile {
   static constexpr int NSTAGE = 8;
   static constexpr int AHEAD = 5;                   // units issued before step 0
   static constexpr int LDS_HALVES = NSTAGE * STAGE + 2 * 64;  // + 64 x +inf
+  // D <= 64: two work-groups (two waves per SIMD, <= 256 registers each);
+  // D = 128: one (one wave per SIMD, up to 512 registers).
+  static constexpr int WGS_PER_CU = D <= 64 ? 2 : 1;
 };
 
 template <int D, int NW>
 constexpr bool dkdv_pipe_tiling_ok() {
   using T = DkdvPipeTile<D, NW>;
   constexpr int instr = T::TILE * 2 / 1024;
-  // one 1 KiB piece per wave (duplicates allowed), and two work-groups per CU
-  return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
-         2 * T::LDS_HALVES * 2 <= 160 * 1024 && D <= 64;
+  // one or two 1 KiB pieces per wave (duplicates allowed when the tile has
+  // fewer pieces than waves), and the ring of every resident work-group in LDS
+  return (T::TILE * 2) % 1024 == 0 &&
+         ((instr <= NW && NW % instr == 0) || instr == 2 * NW) &&
+         T::WGS_PER_CU * T::LDS_HALVES * 2 <= 160 * 1024;
 }
 
 // LDS reads of the pipelined dK/dV body are issued this many MFMA tasks
@@ -472,13 +477,15 @@ constexpr bool dkdv_pipe_tiling_ok() {
 #endif
 
 template <int D, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(DkdvPipeTile<D, NW>::WGS_PER_CU)))
 void dkdv_pipe_kernel(BwdArgs a) {
   using T = DkdvPipeTile<D, NW>;
   using Dma = DmaStager<D, T::QT, NW>;
-  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
+  static_assert(Dma::PER_WAVE == 1 || Dma::PER_WAVE == 2, "one or two tile pieces per wave");
   constexpr int NS = T::NSTAGE;
-  constexpr int IPU = 3;  // this wave's DMA instructions per unit: Q, dO, LSE or Delta
+  // this wave's DMA instructions per unit: its Q and dO pieces, LSE or Delta
+  constexpr int IPU = 2 * Dma::PER_WAVE + 1;
   __shared__ __attribute__((aligned(16))) half_t lds[T::LDS_HALVES];
   constexpr int kInfOff = NS * T::STAGE / 2;  // float offset of the +inf table
 
@@ -552,19 +559,41 @@ void dkdv_pipe_kernel(BwdArgs a) {
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u);
     const uint32_t piece = (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %5\n\t"
-        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %6\n\t"
-        "buffer_load_dwordx4 %1, %4, 0 offen lds\n\t"
-        "s_mov_b32 m0, %8\n\t"
-        "buffer_load_dword %2, %7, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(vt), "v"(va), "s"(r_q), "s"(r_do), "s"(base + piece),
-          "s"(base + T::TILE * 2u + piece), "s"(r_aux), "s"(base + aux_lds)
-        : "memory");
+    if constexpr (Dma::PER_WAVE == 1) {
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %5\n\t"
+          "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %6\n\t"
+          "buffer_load_dwordx4 %1, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %8\n\t"
+          "buffer_load_dword %2, %7, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(vt), "v"(va), "s"(r_q), "s"(r_do), "s"(base + piece),
+            "s"(base + T::TILE * 2u + piece), "s"(r_aux), "s"(base + aux_lds)
+          : "memory");
+    } else {
+      const uint32_t vt1 = (uint32_t)row0 * (D * 2u) + dma.voff[1];
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %6\n\t"
+          "buffer_load_dwordx4 %1, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %7\n\t"
+          "buffer_load_dwordx4 %2, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %8\n\t"
+          "buffer_load_dwordx4 %1, %5, 0 offen lds\n\t"
+          "s_mov_b32 m0, %9\n\t"
+          "buffer_load_dwordx4 %2, %5, 0 offen lds\n\t"
+          "s_mov_b32 m0, %11\n\t"
+          "buffer_load_dword %3, %10, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(vt), "v"(vt1), "v"(va), "s"(r_q), "s"(r_do), "s"(base + piece),
+            "s"(base + piece + 1024u), "s"(base + T::TILE * 2u + piece),
+            "s"(base + T::TILE * 2u + piece + 1024u), "s"(r_aux), "s"(base + aux_lds)
+          : "memory");
+    }
     --i_left;
     i_row += T::QT;
     if (i_row >= N && i_left > 0) {
@@ -666,13 +695,19 @@ void dkdv_pipe_kernel(BwdArgs a) {
       sa_prev[h][e] = (half_t)0.f;
     }
 
+  // D = 128 holds dK and dV (128 registers) in AGPRs, beside ~250 VGPRs.
+  constexpr bool kAgprAcc = D > 64;
+  auto acc_mfma = [&](float16v& acc, const half8& a, const half8& b) {
+    if constexpr (kAgprAcc) mfma32_agpr(acc, a, b);
+    else acc = mfma32(a, b, acc);
+  };
   auto dvdk = [&](const half_t* slot) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
-        dv[db] = mfma32(tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h], dv[db]);
-        dk[db] = mfma32(tr8(slot + 16 * h * D, db), sa_prev[h], dk[db]);
+        acc_mfma(dv[db], tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h]);
+        acc_mfma(dk[db], tr8(slot + 16 * h * D, db), sa_prev[h]);
       }
   };
 
@@ -729,8 +764,8 @@ void dkdv_pipe_kernel(BwdArgs a) {
       constexpr int t = decltype(t_c)::value;
       constexpr int kind = t % 4, q = t / 4;
       constexpr int h = q / (D / 32), db = q % (D / 32);
-      if constexpr (kind == 0) dv[db] = mfma32(op, pa_prev[h], dv[db]);
-      else if constexpr (kind == 1) dk[db] = mfma32(op, sa_prev[h], dk[db]);
+      if constexpr (kind == 0) acc_mfma(dv[db], op, pa_prev[h]);
+      else if constexpr (kind == 1) acc_mfma(dk[db], op, sa_prev[h]);
       else if constexpr (kind == 2) s_nx = mfma32(op, kf[q], s_nx);
       else dp_nx = mfma32(op, vn[q], dp_nx);
     };
@@ -822,6 +857,7 @@ void dkdv_pipe_kernel(BwdArgs a) {
   }
   // dV/dK of the last unit (slot 7; zeros if it was a padding unit).
   dvdk(lds + (NS - 1) * T::STAGE);
+  if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const float nscale = -a.scale;  // dK accumulated -dS

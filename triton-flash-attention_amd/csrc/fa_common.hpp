@@ -55,6 +55,20 @@ __device__ __forceinline__ float16v mfma32(half8 a, half8 b, float16v c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// The same MFMA accumulating in place into AGPRs, for accumulators that only
+// MFMAs touch until the epilogue (the compiler's MFMA selection keeps every
+// accumulator in VGPRs, which a kernel needing more than 256 registers would
+// otherwise spill). The leading s_nop 1 gives the two wait states a VALU
+// write of an operand needs before an MFMA reads it (the hazard checks do
+// not look inside asm); after the last call and before the accumulator is
+// read, agpr_acc_drain() waits out the MFMA's passes.
+__device__ __forceinline__ void mfma32_agpr(float16v& acc, half8 a, half8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void agpr_acc_drain() {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
 // Row permutation applied when a 32-row A operand is read from LDS so that
 // the MFMA result rows held by lane half g, values j = 0..7 / 8..15, are the
 // CONTIGUOUS operand rows 8g..8g+7 / 16+8g..16+8g+7. That makes a lane's
