@@ -1151,14 +1151,17 @@ struct DqPipeTile {
   static constexpr int STAGE = 2 * TILE;
   static constexpr int NSTAGE = 8;
   static constexpr int AHEAD = 5;
+  // D <= 64: two work-groups per CU; D = 128: one (dQ accumulated in AGPRs).
+  static constexpr int WGS_PER_CU = D <= 64 ? 2 : 1;
 };
 
 template <int D, int NW>
 constexpr bool dq_pipe_tiling_ok() {
   using T = DqPipeTile<D, NW>;
   constexpr int instr = T::TILE * 2 / 1024;
-  return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
-         2 * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && D <= 64;
+  return (T::TILE * 2) % 1024 == 0 &&
+         ((instr <= NW && NW % instr == 0) || instr == 2 * NW) &&
+         T::WGS_PER_CU * T::NSTAGE * T::STAGE * 2 <= 160 * 1024;
 }
 
 #ifndef FA_DQ_LEAD
@@ -1166,13 +1169,14 @@ constexpr bool dq_pipe_tiling_ok() {
 #endif
 
 template <int D, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(DqPipeTile<D, NW>::WGS_PER_CU)))
 void dq_pipe_kernel(BwdArgs a) {
   using T = DqPipeTile<D, NW>;
   using Dma = DmaStager<D, T::KT, NW>;
-  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
+  static_assert(Dma::PER_WAVE == 1 || Dma::PER_WAVE == 2, "one or two tile pieces per wave");
   constexpr int NS = T::NSTAGE;
-  constexpr int IPU = 2;  // this wave's DMA instructions per unit: K, V
+  constexpr int IPU = 2 * Dma::PER_WAVE;  // this wave's DMA instructions per unit: K, V pieces
   __shared__ __attribute__((aligned(16))) half_t lds[NS * T::STAGE];
 
   const int tid = threadIdx.x;
@@ -1245,16 +1249,35 @@ void dq_pipe_kernel(BwdArgs a) {
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %4\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-        "s_mov_b32 m0, %5\n\t"
-        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
-        : "memory");
+    if constexpr (Dma::PER_WAVE == 1) {
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %4\n\t"
+          "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+          "s_mov_b32 m0, %5\n\t"
+          "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
+          : "memory");
+    } else {
+      const uint32_t vt1 = (uint32_t)row0 * (D * 2u) + dma.voff[1];
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %5\n\t"
+          "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %6\n\t"
+          "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %7\n\t"
+          "buffer_load_dwordx4 %1, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %8\n\t"
+          "buffer_load_dwordx4 %2, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(vt), "v"(vt1), "s"(r_k), "s"(r_v), "s"(base), "s"(base + 1024u),
+            "s"(base + T::TILE * 2u), "s"(base + T::TILE * 2u + 1024u)
+          : "memory");
+    }
     i_row += T::KT;
   };
 #pragma unroll
@@ -1325,12 +1348,17 @@ void dq_pipe_kernel(BwdArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) sa_prev[h][e] = (half_t)0.f;
 
+  // D = 128 holds dQ (64 registers) in AGPRs.
+  constexpr bool kAgprAcc = D > 64;
+  auto acc_mfma = [&](float16v& acc, const half8& a, const half8& b) {
+    if constexpr (kAgprAcc) mfma32_agpr(acc, a, b);
+    else acc = mfma32(a, b, acc);
+  };
   auto dq_mm = [&](const half_t* slot) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-        dq[db] = mfma32(tr8(slot + 16 * h * D, db), sa_prev[h], dq[db]);
+      for (int db = 0; db < D / 32; ++db) acc_mfma(dq[db], tr8(slot + 16 * h * D, db), sa_prev[h]);
   };
 
   int c_key = 0;  // first key of the unit the body works on
@@ -1377,7 +1405,7 @@ void dq_pipe_kernel(BwdArgs a) {
       constexpr int t = decltype(t_c)::value;
       constexpr int kind = t % 3, q = t / 3;
       constexpr int h = q / (D / 32), db = q % (D / 32);
-      if constexpr (kind == 0) dq[db] = mfma32(op, sa_prev[h], dq[db]);
+      if constexpr (kind == 0) acc_mfma(dq[db], op, sa_prev[h]);
       else if constexpr (kind == 1) s_nx = mfma32(op, qf[q], s_nx);
       else dp_nx = mfma32(op, don[q], dp_nx);
     };
@@ -1447,6 +1475,7 @@ void dq_pipe_kernel(BwdArgs a) {
     step(ic<3>{});
   }
   dq_mm(lds + (NS - 1) * T::STAGE);  // dQ of the last unit (slot 7)
+  if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const float nscale = -a.scale;  // accumulated -dS

@@ -50,7 +50,8 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;
 //         D = 128 runs one work-group per CU with dK, dV in AGPRs)
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
-//         3 = 8 waves, 64; 4 = 4 waves, 32-key units, software-pipelined (D <= 64)
+//         3 = 8 waves, 64; 4 = 4 waves, 32-key units, software-pipelined (all D;
+//         at D = 128 the classic 4 waves x 32 stays faster)
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
     {{6, 6}, {6, 6}, {2, 2}},  // fwd
