@@ -1,0 +1,184 @@
+"""Driver-free compile check of the gfx950 kernel library.
+
+The MI355X counterpart of the reference's ``scripts/aot_compile_check.py``
+(which AOT-compiles its forward, preprocess and backward kernels for an NVIDIA
+target without a GPU, lines 81-156): this compiles every HIP source of the
+library for ``--offload-arch=gfx950`` with the production flags into a
+temporary file, no GPU or driver needed, and reads the compiler's per-kernel
+resource report (VGPRs, AGPRs, scratch, occupancy, LDS). With ``--strict`` it
+also fails when a kernel the default tiling table selects spills registers to
+scratch memory: a spill reload inside a pipelined loop is a vector-memory load,
+and waiting for it drains the kernel's DMA ring.
+
+    python -m triton_flash_attention.compile_check [--arch gfx950] [--report] [--strict]
+"""
+
+from __future__ import annotations
+
+import argparse
+import re
+import shutil
+import subprocess
+import sys
+import tempfile
+from dataclasses import dataclass
+from pathlib import Path
+
+from . import _build
+
+SUPPORTED_ARCHS = ("gfx950",)
+
+# Kernel instances the default tiling table (kDefault in csrc/fa_capi.hip)
+# selects, as demangled name prefixes, for D = 32, 64, 128, both mask modes.
+DEFAULT_KERNELS = (
+    "fa::fwd_pipe_kernel<32, false, 4, 1>", "fa::fwd_pipe_kernel<32, true, 4, 1>",
+    "fa::fwd_pipe_kernel<64, false, 4, 1>", "fa::fwd_pipe_kernel<64, true, 4, 1>",
+    "fa::fwd_kernel<128, false, 4, 32>", "fa::fwd_kernel<128, true, 4, 32>",
+    "fa::dkdv_pipe_kernel<32, false, 4>", "fa::dkdv_pipe_kernel<32, true, 4>",
+    "fa::dkdv_pipe_kernel<64, false, 4>", "fa::dkdv_pipe_kernel<64, true, 4>",
+    "fa::dkdv_pipe_kernel<128, false, 4>", "fa::dkdv_pipe_kernel<128, true, 4>",
+    "fa::dq_pipe_kernel<32, false, 4>", "fa::dq_pipe_kernel<32, true, 4>",
+    "fa::dq_pipe_kernel<64, false, 4>", "fa::dq_pipe_kernel<64, true, 4>",
+    "fa::dq_kernel<128, false, 4, 32>", "fa::dq_kernel<128, true, 4, 32>",
+    "fa::preprocess_kernel<32>", "fa::preprocess_kernel<64>", "fa::preprocess_kernel<128>",
+    "fa::split_reduce_kernel",
+)
+# The same table as (kernel kind, head_dim) -> default variant index, for the
+# test that keeps this list in step with kDefault (kinds: 0 fwd, 1 dK/dV, 2 dQ).
+DEFAULT_VARIANTS = {
+    (0, 32): 6, (0, 64): 6, (0, 128): 2,
+    (1, 32): 4, (1, 64): 4, (1, 128): 4,
+    (2, 32): 4, (2, 64): 4, (2, 128): 1,
+}
+
+
+@dataclass
+class KernelUsage:
+    name: str
+    vgprs: int = -1
+    agprs: int = -1
+    scratch: int = -1
+    occupancy: int = -1
+    lds: int = -1
+
+
+_FIELDS = (
+    ("vgprs", re.compile(r"remark:\s+VGPRs: (\d+)")),
+    ("agprs", re.compile(r"remark:\s+AGPRs: (\d+)")),
+    ("scratch", re.compile(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)")),
+    ("occupancy", re.compile(r"remark:\s+Occupancy \[waves/SIMD\]: (\d+)")),
+    ("lds", re.compile(r"remark:\s+LDS Size \[bytes/block\]: (\d+)")),
+)
+_NAME = re.compile(r"remark: Function Name: (\S+)")
+
+
+_MANGLED = re.compile(r"^_ZN2fa(\d+)")
+_TARG = re.compile(r"L([ib])(\d+)E")
+
+
+def _short_name(mangled: str) -> str:
+    """``fa::name<args>`` of this library's kernels (integer / bool template
+    arguments only), for names a demangler leaves as they are."""
+    m = _MANGLED.match(mangled)
+    if m is None:
+        return mangled
+    n = int(m.group(1))
+    start = m.end()
+    name = mangled[start:start + n]
+    rest = mangled[start + n:]
+    args = []
+    if rest.startswith("I"):
+        body = rest[1:rest.index("EE") + 1] if "EE" in rest else ""
+        for kind, val in _TARG.findall(body):
+            args.append(("true" if val == "1" else "false") if kind == "b" else val)
+    return f"fa::{name}<{', '.join(args)}>(...)" if args else f"fa::{name}(...)"
+
+
+def _demangle(names: list[str]) -> list[str]:
+    tool = shutil.which("c++filt") or shutil.which("llvm-cxxfilt")
+    out_names = names
+    if tool is not None and names:
+        out = subprocess.run([tool], input="\n".join(names), capture_output=True, text=True)
+        lines = out.stdout.splitlines()
+        if out.returncode == 0 and len(lines) == len(names):
+            out_names = lines
+    return [_short_name(n) if n.startswith("_Z") else n for n in out_names]
+
+
+def parse_resource_usage(text: str) -> list[KernelUsage]:
+    """Kernel records from hipcc's ``-Rpass-analysis=kernel-resource-usage`` remarks."""
+    kernels: list[KernelUsage] = []
+    for line in text.splitlines():
+        m = _NAME.search(line)
+        if m:
+            kernels.append(KernelUsage(m.group(1)))
+            continue
+        if not kernels:
+            continue
+        for field, pattern in _FIELDS:
+            m = pattern.search(line)
+            if m:
+                setattr(kernels[-1], field, int(m.group(1)))
+                break
+    for k, name in zip(kernels, _demangle([k.name for k in kernels])):
+        k.name = name.removeprefix("void ")
+    return kernels
+
+
+def compile_library(arch: str = "gfx950") -> tuple[list[KernelUsage], str]:
+    """Compile the library into a temporary file; returns (kernels, diagnostics)."""
+    if arch not in SUPPORTED_ARCHS:
+        raise ValueError(f"unsupported arch {arch!r}: the kernels are written for {SUPPORTED_ARCHS}")
+    with tempfile.TemporaryDirectory() as tmp:
+        cmd = _build.build_command(Path(tmp) / "libfa_check.so",
+                                   extra=("-Rpass-analysis=kernel-resource-usage",))
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+    diag = "\n".join(ln for ln in (proc.stderr or "").splitlines()
+                     if "packed-fp32-ops" not in ln and "remark:" not in ln)
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + diag[-6000:])
+    return parse_resource_usage(proc.stderr or ""), diag
+
+
+def spilling_defaults(kernels: list[KernelUsage]) -> tuple[list[KernelUsage], list[str]]:
+    """(default kernels that use scratch, default kernels missing from the report)."""
+    spills, missing = [], []
+    for prefix in DEFAULT_KERNELS:
+        found = [k for k in kernels if k.name.startswith(prefix + "(")]
+        if not found:
+            missing.append(prefix)
+        spills += [k for k in found if k.scratch != 0]
+    return spills, missing
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description="Driver-free gfx950 compile check")
+    parser.add_argument("--arch", default="gfx950", help="offload target (only gfx950)")
+    parser.add_argument("--report", action="store_true", help="print every kernel's resource usage")
+    parser.add_argument("--strict", action="store_true",
+                        help="fail if a default-tiling kernel spills to scratch")
+    args = parser.parse_args(argv)
+    try:
+        kernels, _ = compile_library(args.arch)
+    except (ValueError, RuntimeError) as e:
+        print(f"compile check FAILED: {e}", file=sys.stderr)
+        return 1
+    if args.report:
+        print(f"{'kernel':58s} {'VGPR':>5s} {'AGPR':>5s} {'scratch':>7s} {'waves/SIMD':>10s} {'LDS':>7s}")
+        for k in kernels:
+            print(f"{k.name[:58]:58s} {k.vgprs:5d} {k.agprs:5d} {k.scratch:7d} {k.occupancy:10d} {k.lds:7d}")
+    spills, missing = spilling_defaults(kernels)
+    if args.strict and (spills or missing):
+        for k in spills:
+            print(f"default kernel spills {k.scratch} bytes/lane to scratch: {k.name}", file=sys.stderr)
+        for name in missing:
+            print(f"default kernel not in the compiler report: {name}", file=sys.stderr)
+        return 1
+    print(f"compile check passed for {args.arch}: {len(kernels)} kernels (forward, preprocess, "
+          f"dK/dV, dQ, split reduce; causal/bidirectional; D 32/64/128; MHA/GQA)"
+          + ("; no scratch in the default tilings" if args.strict else ""))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
