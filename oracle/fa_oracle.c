@@ -25,6 +25,12 @@
  *   oracle_bwd             torch fp64 autograd through SDPA; golden fixtures;
  *                          closed forms (constant V -> dQ = dK = 0, N=1);
  *                          GQA group sum == MHA with repeated K/V
+ *   oracle_bwd, fold = 1   equal to fold = 0 when c32 is a power of two (the
+ *                          fp16 rounding of c32 x is then exact); a numpy
+ *                          restatement with np.float16 casts of the scaled
+ *                          operands on tiny inputs; differs from fold = 0 by
+ *                          no more than a 2^-11 relative operand perturbation
+ *                          allows, and does differ at a generic scale
  */
 #include <math.h>
 #include <stdint.h>
@@ -195,9 +201,20 @@ void oracle_bwd_preprocess(const double* o, const double* dO, int64_t rows, int6
   for (int64_t r = 0; r < rows; ++r) delta[r] = dot(o + r * D, dO + r * D, D);
 }
 
+/* fp16(fp32(c32 * x)) for every element: the reference backward's scaled
+ * score operands, k_scaled = (k * (sm_scale * _INV_LN2)).to(tl.float16) and
+ * q_scaled likewise (attention.py:435, 515): an fp32 product, rounded to fp16. */
+static void scaled_half(const double* x, int64_t n, float c32, double* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_round_half((double)(c32 * (float)x[i]));
+}
+
 /* Backward from the saved base-2 LSE (attention.py:258-350, 403-573;
  * docs/architecture.md:75-90), closed form per (query row i, key j):
  *   P_ij  = exp2(s_ij - lse2_i) on visible pairs, 0 elsewhere (296-300, 339-343)
+ *           with s_ij = c q_i.k_j (fold = 0, exact), or, as the reference
+ *           computes it (fold = 1), s_ij = q_i.fp16(c32 k_j) for dK, dV
+ *           (297, 435) and s_ij = fp16(c32 q_i).k_j for dQ (340, 515),
+ *           c32 = fp32(fp32(scale) * fp32(1/ln 2))
  *   dV_j += P_ij dO_i                                          (302)
  *   dP_ij = dO_i . V_j                                         (303, 345)
  *   dS_ij = P_ij (dP_ij - Delta_i)                             (304, 346; the ln2
@@ -208,9 +225,10 @@ void oracle_bwd_preprocess(const double* o, const double* dO, int64_t rows, int6
  * head so each output row has one writer. */
 void oracle_bwd(const double* q, const double* k, const double* v, const double* dO,
                 const double* lse2, const double* delta, int64_t B, int64_t Hq, int64_t Hkv,
-                int64_t N, int64_t D, double scale, int causal, double* dq, double* dk,
-                double* dv) {
+                int64_t N, int64_t D, double scale, int causal, int fold, double* dq,
+                double* dk, double* dv) {
   const double c = scale * INV_LN2;
+  const float c32 = (float)scale * (float)INV_LN2;
   const int64_t group = Hq / Hkv;
 #pragma omp parallel for schedule(dynamic)
   for (int64_t bkv = 0; bkv < B * Hkv; ++bkv) {
@@ -221,11 +239,15 @@ void oracle_bwd(const double* q, const double* k, const double* v, const double*
     double* dV = dv + bkv * N * D;
     memset(dK, 0, sizeof(double) * (size_t)(N * D));
     memset(dV, 0, sizeof(double) * (size_t)(N * D));
+    double* ks = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
+    double* qs = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
+    if (fold) scaled_half(K, N * D, c32, ks);
     for (int64_t gi = 0; gi < group; ++gi) {
       const int64_t bh = b * Hq + hkv * group + gi;
       const double* Q = q + bh * N * D;
       const double* G = dO + bh * N * D;
       double* dQ = dq + bh * N * D;
+      if (fold) scaled_half(Q, N * D, c32, qs);
       for (int64_t i = 0; i < N; ++i) {
         const double* qi = Q + i * D;
         const double* gi_row = G + i * D;
@@ -235,19 +257,25 @@ void oracle_bwd(const double* q, const double* k, const double* v, const double*
         const double dlt = delta[bh * N + i];
         const int64_t last = causal ? i : N - 1;
         for (int64_t j = 0; j <= last; ++j) {
-          const double p = exp2(dot(qi, K + j * D, D) * c - lse);
+          /* p_k feeds dK and dV, p_q feeds dQ; equal unless fold */
+          const double p_k = fold ? exp2(dot(qi, ks + j * D, D) - lse)
+                                  : exp2(dot(qi, K + j * D, D) * c - lse);
+          const double p_q = fold ? exp2(dot(qs + i * D, K + j * D, D) - lse) : p_k;
           const double dp = dot(gi_row, V + j * D, D);
-          const double ds = p * (dp - dlt);
+          const double ds_k = p_k * (dp - dlt);
+          const double ds_q = p_q * (dp - dlt);
           double* dvj = dV + j * D;
           double* dkj = dK + j * D;
           const double* kj = K + j * D;
           for (int64_t d = 0; d < D; ++d) {
-            dvj[d] += p * gi_row[d];
-            dkj[d] += scale * ds * qi[d];
-            dqi[d] += scale * ds * kj[d];
+            dvj[d] += p_k * gi_row[d];
+            dkj[d] += scale * ds_k * qi[d];
+            dqi[d] += scale * ds_q * kj[d];
           }
         }
       }
     }
+    free(ks);
+    free(qs);
   }
 }

@@ -9,7 +9,10 @@ Functions and the reference lines they restate
     fwd(..., online=False)  closed-form softmax attention, LSE base 2 (61-79, 230-231)
     fwd(..., online=True)   the tiled online-softmax recurrence with fp16 P (25-79, 170-234)
     bwd_preprocess          Delta = rowsum(O * dO) (237-255)
-    bwd                     dQ, dK, dV from LSE (258-350, 403-573), GQA group sums (503-505)
+    bwd(..., fold=False)    dQ, dK, dV from LSE (258-350, 403-573), GQA group sums (503-505),
+                            scores c q.k in exact arithmetic
+    bwd(..., fold=True)     the same with the reference's fp16-rounded score operands,
+                            fp16(c k) for dK/dV and fp16(c q) for dQ (435, 515)
     round_half              fp16 round-to-nearest-even (the .to(tl.float16) casts)
 """
 
@@ -56,7 +59,7 @@ def _load():
     lib.oracle_bwd_preprocess.restype = None
     lib.oracle_bwd_preprocess.argtypes = [P, P, I64, I64, P]
     lib.oracle_bwd.restype = None
-    lib.oracle_bwd.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, F64, INT, P, P, P]
+    lib.oracle_bwd.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, F64, INT, INT, P, P, P]
     _lib = lib
     return lib
 
@@ -117,8 +120,10 @@ def bwd_preprocess(o, do) -> np.ndarray:
     return delta
 
 
-def bwd(q, k, v, do, lse2, delta, causal: bool, scale: float | None = None):
-    """(dQ, dK, dV) float64 from the saved base-2 LSE and Delta."""
+def bwd(q, k, v, do, lse2, delta, causal: bool, scale: float | None = None, *,
+        fold: bool = False):
+    """(dQ, dK, dV) float64 from the saved base-2 LSE and Delta. ``fold``: score
+    operands rounded as the reference backward rounds them (attention.py:435, 515)."""
     q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
     lse2, delta = _f64(lse2), _f64(delta)
     B, Hq, Hkv, N, D = _dims(q, k, v)
@@ -127,11 +132,13 @@ def bwd(q, k, v, do, lse2, delta, causal: bool, scale: float | None = None):
     dk = np.empty_like(k)
     dv = np.empty_like(v)
     _load().oracle_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(lse2), _ptr(delta),
-                       B, Hq, Hkv, N, D, scale, int(causal), _ptr(dq), _ptr(dk), _ptr(dv))
+                       B, Hq, Hkv, N, D, scale, int(causal), int(fold), _ptr(dq), _ptr(dk),
+                       _ptr(dv))
     return dq, dk, dv
 
 
-def attention(q, k, v, do, causal: bool, scale: float | None = None, *, o16=None):
+def attention(q, k, v, do, causal: bool, scale: float | None = None, *, o16=None,
+              fold_bwd: bool = False):
     """Full reference computation: O, LSE2, Delta, dQ, dK, dV (float64).
 
     Delta uses the fp16-rounded O the kernel stores, like the reference
@@ -141,5 +148,5 @@ def attention(q, k, v, do, causal: bool, scale: float | None = None, *, o16=None
     o, lse = fwd(q, k, v, causal, scale)
     o_stored = round_half(o) if o16 is None else _f64(o16)
     delta = bwd_preprocess(o_stored, do)
-    dq, dk, dv = bwd(q, k, v, do, lse, delta, causal, scale)
+    dq, dk, dv = bwd(q, k, v, do, lse, delta, causal, scale, fold=fold_bwd)
     return {"o": o, "lse": lse, "delta": delta, "dq": dq, "dk": dk, "dv": dv}

@@ -76,8 +76,10 @@ def run_kernel(q, k, v, do, causal, scale=None):
 
 
 def check_against_oracle(got, q, k, v, do, causal, scale=None, tag=""):
+    # The backward is checked against the reference's own algorithm: scores
+    # from its fp16-rounded scaled operands (attention.py:435, 515).
     ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
-                           o16=got["o16"].numpy())
+                           o16=got["o16"].numpy(), fold_bwd=True)
     report = {}
     for name in ("o", "dq", "dk", "dv"):
         report[name] = assert_close(f"{tag} {name}", got[name], ref[name])
@@ -231,7 +233,7 @@ def test_every_tiling_variant_matches_oracle(head_dim, causal):
     delta = _ops.flash_bwd_preprocess(o, dod)
     torch.cuda.synchronize()
     ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
-                           o16=o.cpu().numpy())
+                           o16=o.cpu().numpy(), fold_bwd=True)
 
     def close(tag, got, name):
         assert_close(tag, torch.as_tensor(got).double().cpu().numpy(), ref[name])

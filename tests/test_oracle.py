@@ -239,6 +239,94 @@ def test_golden_config1_cpu_fallback_is_close_to_fp64():
 
 
 # ---------------------------------------------------------------------------
+# Backward with the reference's fp16-rounded score operands (fold=True):
+# k_scaled = fp16(k * (sm_scale * log2 e)) for dK/dV, q_scaled likewise for dQ
+# (attention.py:435, 515), the product taken in fp32.
+# ---------------------------------------------------------------------------
+INV_LN2 = 1.4426950408889634
+
+
+def _scale_with_c32(target: float) -> float:
+    """A scale whose fp32 product with fp32(1/ln 2) is exactly ``target``."""
+    s = np.float32(target / INV_LN2)
+    for _ in range(64):
+        c = np.float32(s) * np.float32(INV_LN2)
+        if c == np.float32(target):
+            return float(s)
+        s = np.nextafter(s, np.float32(np.inf) if c < target else np.float32(-np.inf))
+    raise AssertionError("no fp32 scale found")
+
+
+def _numpy_folded_bwd(q, k, v, do, lse2, delta, causal, scale):
+    """Tiny-input restatement in numpy (float16 casts via numpy, not the oracle)."""
+    B, Hq, N, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    c32 = np.float32(scale) * np.float32(INV_LN2)
+    f16 = lambda x: (c32 * x.astype(np.float32)).astype(np.float16).astype(np.float64)
+    dq = np.zeros(q.shape)
+    dk = np.zeros(k.shape)
+    dv = np.zeros(v.shape)
+    vis = np.tril(np.ones((N, N), bool)) if causal else np.ones((N, N), bool)
+    for b in range(B):
+        for h in range(Hq):
+            hk = h // G
+            Q, K, V, dO = q[b, h], k[b, hk], v[b, hk], do[b, h]
+            lse = lse2[b, h][:, None]
+            p_k = np.where(vis, np.exp2(Q @ f16(K).T - lse), 0.0)
+            p_q = np.where(vis, np.exp2(f16(Q) @ K.T - lse), 0.0)
+            dp = dO @ V.T
+            dv[b, hk] += p_k.T @ dO
+            dk[b, hk] += scale * (p_k * (dp - delta[b, h][:, None])).T @ Q
+            dq[b, h] = scale * (p_q * (dp - delta[b, h][:, None])) @ K
+    return dq, dk, dv
+
+
+def test_folded_backward_is_exact_when_c_is_a_power_of_two():
+    # operands n/8 and c32 = 2^-3: fp16(c32 x) = x/8 exactly
+    rng = np.random.default_rng(12)
+    q, k, v, do = (rng.integers(-12, 13, size=s).astype(np.float64) / 8.0
+                   for s in ((1, 4, 24, 32), (1, 2, 24, 32), (1, 2, 24, 32), (1, 4, 24, 32)))
+    scale = _scale_with_c32(0.125)
+    for causal in (False, True):
+        _, lse = oracle.fwd(q, k, v, causal, scale)
+        delta = oracle.bwd_preprocess(oracle.round_half(oracle.fwd(q, k, v, causal, scale)[0]), do)
+        exact = oracle.bwd(q, k, v, do, lse, delta, causal, scale)
+        folded = oracle.bwd(q, k, v, do, lse, delta, causal, scale, fold=True)
+        for a, b in zip(folded, exact):
+            # only the double vs fp32 value of c separates them (~1e-8 relative)
+            assert _maxdiff(a, b) <= 1e-6 * max(1.0, float(np.abs(b).max()))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_folded_backward_matches_numpy_restatement(causal):
+    q, k, v, do = _inputs(1, 4, 2, 9, 16, seed=31)
+    qn, kn, vn, don = (t.numpy().astype(np.float64) for t in (q, k, v, do))
+    scale = 0.37
+    o, lse = oracle.fwd(qn, kn, vn, causal, scale)
+    delta = oracle.bwd_preprocess(oracle.round_half(o), don)
+    got = oracle.bwd(qn, kn, vn, don, lse, delta, causal, scale, fold=True)
+    want = _numpy_folded_bwd(qn, kn, vn, don, lse, delta, causal, scale)
+    for a, b in zip(got, want):
+        assert _maxdiff(a, b) < 1e-12
+
+
+def test_folded_backward_differs_within_the_operand_rounding():
+    q, k, v, do = _inputs(1, 2, 2, 40, 64, seed=32)
+    qn, kn, vn, don = (t.numpy().astype(np.float64) for t in (q, k, v, do))
+    o, lse = oracle.fwd(qn, kn, vn, True)
+    delta = oracle.bwd_preprocess(oracle.round_half(o), don)
+    exact = oracle.bwd(qn, kn, vn, don, lse, delta, True)
+    folded = oracle.bwd(qn, kn, vn, don, lse, delta, True, fold=True)
+    for a, b in zip(folded, exact):
+        rel = float(np.linalg.norm(a - b) / np.linalg.norm(b))
+        # the rounding is applied (dV too: its P uses the rounded K) ...
+        assert rel > 1e-7
+        # ... and is no larger than a half-ulp (2^-11) operand perturbation
+        assert rel < 2e-3
+
+
+# ---------------------------------------------------------------------------
 # Planted mistakes: each variant of the oracle must fail the checks above.
 # ---------------------------------------------------------------------------
 def test_planted_mistakes_are_caught():

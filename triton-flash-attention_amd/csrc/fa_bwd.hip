@@ -3,7 +3,10 @@
 //
 // Semantics follow the reference backward (triton_flash_attention/attention.py):
 //   Delta_i = sum_d O_id dO_id in fp32 from the stored fp16 O      (237-255)
-//   P = exp2(s * scale * log2(e) - LSE), masked keys/queries -> 0 (296-300, 339-343)
+//   P = exp2(s - LSE) with the scores s taken in log2 units from the
+//   reference's scaled fp16 operands: s = q . fp16(c k) for dK / dV and
+//   s = fp16(c q) . k for dQ, c = fp32(scale * log2(e))       (297, 340, 435, 515)
+//   masked keys/queries -> 0                                      (296-300, 339-343)
 //   dV = P^T dO, dP = dO V^T, dS = P (dP - Delta)                  (302-304, 345-346)
 //   dK = scale dS^T Q, dQ = scale dS K                             (305, 347, 499, 572)
 //   causal: dK/dV visit query tiles at or below the key tile, dQ visits
@@ -128,8 +131,8 @@ hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_
 // Streams (query head of the GQA group, 64-query tile) steps through a
 // 3-slot LDS ring filled by DMA: Q tile, dO tile (row-major, swizzled) and
 // the tile's LSE / Delta values. Per 32-query block:
-//   S = Q K^T, dP = dO V^T                  (row reads, result: lane = key)
-//   P = exp2(S c - LSE), dS = P (dP - Delta)
+//   S = Q fp16(c K)^T, dP = dO V^T          (row reads, result: lane = key)
+//   P = exp2(S - LSE), dS = P (dP - Delta)
 //   dV^T += dO^T P, dK^T += Q^T dS          (dO^T / Q^T via transposing reads)
 // S and dP of every block of the tile are issued before the first block's
 // vector work, so matrix and vector work overlap.
@@ -186,8 +189,9 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const int k0w = k0 + 32 * wave;
   const int krow = k0w + ql;
 
-  // K and V as B-operands (column = key ql, d = 16*kk + 8*g .. +7), completed
-  // before the first DMA.
+  // fp16(c K) and V as B-operands (column = key ql, d = 16*kk + 8*g .. +7),
+  // completed before the first DMA; fp16(c K) is the reference's k_scaled
+  // (attention.py:435), so S comes out in log2 units.
   half8 kf[D / 16], vf[D / 16];
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
@@ -196,6 +200,12 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
     vf[kk] = __builtin_bit_cast(half8, buf_load_b128(rv, off));
   }
   wait_all_vm();
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kf[kk][e] = (half_t)(a.c * (float)kf[kk][e]);
+    asm volatile("" : "+v"(kf[kk]));
+  }
 
   const int q_begin = CAUSAL ? (k0 / QT) * QT : 0;
   const int ntq = (N - q_begin + QT - 1) / QT;
@@ -269,7 +279,6 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
       dv[db][j] = 0.f;
     }
 
-  const float c = a.c;
   const bool wave_live = k0w < N;
 
   auto step = [&](auto slot_c, int u) {
@@ -337,7 +346,7 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
       half8 pa[2], sa[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float pj = exp2_fast(fmaf(s[qb][j], c, -lse_v[j]));
+        float pj = exp2_fast(s[qb][j] - lse_v[j]);
         if (need_mask) {
           const int q = qa + result_row(j, g);
           if (q >= N || (CAUSAL && q < krow)) pj = 0.f;
@@ -428,15 +437,19 @@ hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
 // DMA ring), but the three stages of a unit are spread over consecutive
 // units so that each unit's body has matrix and vector work that do not
 // depend on each other:
-//   body of unit u:  vector work of unit u      P = exp2(S c - LSE'), dS' = P dPd
-//                    matrix work of unit u + 1  S = Q K^T, dPd = Delta - dO V^T
+//   body of unit u:  vector work of unit u      P = exp2(-Sl), dS' = P dPd
+//                    matrix work of unit u + 1  Sl = LSE' - Q fp16(c K)^T,
+//                                               dPd = Delta - dO V^T
 //                    matrix work of unit u - 1  dV^T += dO^T P, dK^T += Q^T dS'
-// dPd starts from Delta in the accumulator and uses -V, so dS' = -dS and the
-// subtraction of Delta costs nothing; dK is negated once at the end.
-// Causal mask: units a wave sees entirely before its keys read LSE' = +inf
-// (P = 0 exactly) from a small table; the diagonal unit sets its masked S
-// values to -inf. Rows past N need no mask: their Q and dO rows load as
-// zeros, so their P (finite) multiplies zero in both updates.
+// The scores use the reference's scaled key operand fp16(c K) (k_scaled,
+// attention.py:435). Both accumulators start from a per-query table (LSE' in
+// log2 units, Delta) and multiply -fp16(c K) and -V, so neither the LSE'
+// subtraction nor the Delta subtraction costs vector work; dS' = -dS and dK
+// is negated once at the end. Causal mask: units a wave sees entirely before
+// its keys read LSE' = +inf (P = 0 exactly) from a small table; the diagonal
+// unit sets its masked Sl values to +inf. Rows past N need no mask: their Q
+// and dO rows load as zeros, so their P (finite) multiplies zero in both
+// updates.
 // A step is two units and ends with one work-group barrier. The ring has 8
 // unit slots: units 2s-1 .. 2s+2 are read in step s, 2s+3 and 2s+4 are in
 // flight and 2s+5, 2s+6 are issued. Every work-group runs its unit count
@@ -511,7 +524,11 @@ void dkdv_pipe_kernel(BwdArgs a) {
   const int k0w = k0 + 32 * wave;
   const int krow = k0w + ql;
 
-  // K and -V as B operands (column = key ql, d = 16*kk + 8*g .. +7).
+  // -fp16(c K) and -V as B operands (column = key ql, d = 16*kk + 8*g .. +7).
+  // The scaled key operand is the reference's k_scaled (attention.py:435):
+  // c K in fp32 rounded to fp16. With the S accumulator started from LSE',
+  // the MFMA yields LSE' - s and P = exp2(-acc) needs no multiply-add.
+  const float c = a.c;
   half8 kf[D / 16], vn[D / 16];
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
@@ -520,9 +537,13 @@ void dkdv_pipe_kernel(BwdArgs a) {
     vn[kk] = -__builtin_bit_cast(half8, buf_load_b128(rv, off));
   }
   wait_all_vm();
-  // Opaque from here on, so that -V is not recomputed from V inside the loop.
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(vn[kk]));
+  for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kf[kk][e] = (half_t)(-c * (float)kf[kk][e]);
+  // Opaque from here on, so that the operands are not recomputed inside the loop.
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(kf[kk]), "+v"(vn[kk]));
 
   const int q_begin = CAUSAL ? k0 : 0;  // k0 is a multiple of 32
   const int ntq = (N - q_begin + T::QT - 1) / T::QT;
@@ -672,14 +693,20 @@ void dkdv_pipe_kernel(BwdArgs a) {
       dv[db][j] = 0.f;
     }
 
-  const float c = a.c;
   const float* const fl = reinterpret_cast<const float*>(lds);
-  // Pipeline registers: S, dPd of the current unit; P, dS' of the previous one.
+  int c_row = q_begin + (u_lo - min(u_lo / ntq, G - 1) * ntq) * T::QT;  // compute cursor
+  // Float offset (from lds) of the lane's LSE' values for the unit of row qa
+  // in ring slot slot: units a wave sees entirely before its keys read +inf.
+  auto lse_table = [&](int slot, int qa) {
+    if (CAUSAL && qa < k0w) return kInfOff + 8 * g;
+    return (slot * T::STAGE + 2 * T::TILE) / 2 + 8 * g;
+  };
+  // Pipeline registers: LSE' - s, dPd of the current unit; P, dS' of the
+  // previous one.
   float16v s_cur, dp_cur;
   {
     dp_cur = table16(reinterpret_cast<const float*>(lds + 2 * T::TILE) + 64 + 8 * g);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s_cur[j] = 0.f;
+    s_cur = table16(fl + lse_table(0, c_row));
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
       s_cur = mfma32(*reinterpret_cast<const half8*>(lds + r_off[kk]), kf[kk], s_cur);
@@ -711,8 +738,6 @@ void dkdv_pipe_kernel(BwdArgs a) {
       }
   };
 
-  int c_row = q_begin + (u_lo - min(u_lo / ntq, G - 1) * ntq) * T::QT;  // compute cursor
-
   // Body of one unit in ring slot SLOT (see the header comment).
   auto body = [&](auto slot_c) {
     constexpr int SLOT = decltype(slot_c)::value;
@@ -723,16 +748,14 @@ void dkdv_pipe_kernel(BwdArgs a) {
     c_row += T::QT;
     if (c_row >= N) c_row = q_begin;  // next query head of the group
 
-    // Float offset (from lds) of the lane's LSE' values of this unit.
-    int ltab = (SLOT * T::STAGE + 2 * T::TILE) / 2 + 8 * g;
+    // LSE' offset of the next unit, whose S accumulator starts from it.
+    int ltab = lse_table((SLOT + 1) % NS, c_row);
     if constexpr (CAUSAL) {
-      if (qa < k0w) {
-        ltab = kInfOff + 8 * g;
-      } else if (qa == k0w) {
+      if (qa == k0w) {
         // diagonal unit: query 16h + 8g + e is kept iff it is >= key ql
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          if (16 * (j >> 3) + 8 * g + (j & 7) < ql) s_cur[j] = -__builtin_inff();
+          if (16 * (j >> 3) + 8 * g + (j & 7) < ql) s_cur[j] = __builtin_inff();
       }
     }
 
@@ -758,8 +781,6 @@ void dkdv_pipe_kernel(BwdArgs a) {
       else return *reinterpret_cast<const half8*>(do_nxt + r_off[q]);
     };
     float16v s_nx, dp_nx;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s_nx[j] = 0.f;
     auto run_task = [&](auto t_c, const half8& op) {
       constexpr int t = decltype(t_c)::value;
       constexpr int kind = t % 4, q = t / 4;
@@ -770,17 +791,16 @@ void dkdv_pipe_kernel(BwdArgs a) {
       else dp_nx = mfma32(op, vn[q], dp_nx);
     };
     half8 pa[2], sa[2];
-    float16v lse;
     // Vector work on value pairs (2pr, 2pr+1) in two stages placed in
     // different groups, so that an MFMA separates each exp from its users:
-    //   A: p = exp2(s c - lse)      B: dS' = p dPd, both packed to fp16.
+    //   A: p = exp2(-(LSE' - s))      B: dS' = p dPd, both packed to fp16.
     // The empty asm statements pin each stage to its fenced group (plain
     // arithmetic would otherwise float).
     float pexp[16];
     auto stage_a = [&](int pr) {
       float p2[2];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -lse[2 * pr + e]));
+      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(-s_cur[2 * pr + e]);
       asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
       pexp[2 * pr] = p2[0];
       pexp[2 * pr + 1] = p2[1];
@@ -807,7 +827,7 @@ void dkdv_pipe_kernel(BwdArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(ltab));
     static_for<0, kLead>([&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
-    lse = table16(fl + ltab);
+    s_nx = table16(fl + ltab);
     dp_nx = table16(reinterpret_cast<const float*>(nxt + 2 * T::TILE) + 64 + 8 * g);
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NTASK>([&](auto i_c) {
@@ -918,8 +938,8 @@ hipError_t dkdv_pipe_launch(const BwdArgs& a, hipStream_t stream) {
 // Work-group: NW waves x 32 queries (Q, dO resident in VGPRs as B operands,
 // LSE / Delta one per lane). Streams 64-key tiles (K, V row-major, swizzled)
 // through a 3-slot DMA ring. Per 32-key block:
-//   S^T = K Q^T, dP^T = V dO^T               (row reads, result: lane = query)
-//   P^T = exp2(S^T c - LSE), dS^T = P^T (dP^T - Delta)
+//   S^T = K fp16(c Q)^T, dP^T = V dO^T       (row reads, result: lane = query)
+//   P^T = exp2(S^T - LSE), dS^T = P^T (dP^T - Delta)
 //   dQ^T += K^T dS^T                          (K^T via transposing reads)
 // --------------------------------------------------------------------------
 template <int D, int NW, int KT>
@@ -973,6 +993,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   const int q0w = q0 + 32 * wave;
   const int qrow = q0w + ql;
 
+  // fp16(c Q) (the reference's q_scaled, attention.py:515) and dO as B operands.
   half8 qf[D / 16], dof[D / 16];
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
@@ -983,6 +1004,12 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   const float lse = buf_load_f32(rl, (uint32_t)qrow * 4u);
   const float delta = buf_load_f32(rd, (uint32_t)qrow * 4u);
   wait_all_vm();
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[kk][e] = (half_t)(a.c * (float)qf[kk][e]);
+    asm volatile("" : "+v"(qf[kk]));
+  }
 
   const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
   const int ntiles = (kv_end + KT - 1) / KT;
@@ -1034,7 +1061,6 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) dq[db][j] = 0.f;
 
-  const float c = a.c;
   const float nl = -lse;
 
   auto step = [&](auto slot_c, int t) {
@@ -1076,7 +1102,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
       half8 sa[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        float pj = exp2_fast(fmaf(s[kb][j], c, nl));
+        float pj = exp2_fast(s[kb][j] + nl);
         if (need_mask) {
           const int key = ka + result_row(j, g);
           if (key >= N || (CAUSAL && key > qrow)) pj = 0.f;
@@ -1132,15 +1158,17 @@ hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
 // Work-group: NW waves x 32 queries (Q, dO as MFMA B operands, LSE and Delta
 // one per lane), 32-key units (K, V rows) streamed through an 8-slot LDS DMA
 // ring, two units per barrier step. The body of unit u runs
-//   vector work of unit u      P^T = exp2(S^T c - LSE), dS'^T = P^T dPd^T
-//   matrix work of unit u + 1  S^T = K Q^T, dPd^T = Delta - V dO^T
+//   vector work of unit u      P^T = exp2(-Sl^T), dS'^T = P^T dPd^T
+//   matrix work of unit u + 1  Sl^T = LSE - K fp16(c Q)^T, dPd^T = Delta - V dO^T
 //   matrix work of unit u - 1  dQ^T += K^T dS'^T      (K^T via transposing reads)
-// with dPd^T started from Delta in the accumulator (operand -dO), so
-// dS' = -dS and dQ is negated once at the end. Keys past N need no mask:
-// their K and V rows load as zeros, so their P (finite) multiplies zero.
-// Causal: units of keys after all of a wave's queries use LSE = +inf (P = 0
-// exactly); the diagonal unit sets its masked S to -inf. Each work-group
-// rounds its unit count up to the 8-unit unroll (padding units are zeros).
+// The scores use the reference's scaled query operand fp16(c Q) (q_scaled,
+// attention.py:515); both accumulators start from per-query values (operands
+// -fp16(c Q) and -dO), so dS' = -dS and dQ is negated once at the end. Keys
+// past N need no mask: their K and V rows load as zeros, so their P (finite)
+// multiplies zero. Causal: units of keys after all of a wave's queries, and
+// the masked values of the diagonal unit, get Sl = +inf (P = 0 exactly).
+// Each work-group rounds its unit count up to the 8-unit unroll (padding
+// units are zeros).
 // --------------------------------------------------------------------------
 template <int D, int NW>
 struct DqPipeTile {
@@ -1205,7 +1233,8 @@ void dq_pipe_kernel(BwdArgs a) {
   const int q0w = q0 + 32 * wave;
   const int qrow = q0w + ql;
 
-  // Q and -dO as B operands (column = query ql, d = 16*kk + 8*g .. +7).
+  // -fp16(c Q) and -dO as B operands (column = query ql, d = 16*kk + 8*g .. +7).
+  const float c = a.c;
   half8 qf[D / 16], don[D / 16];
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
@@ -1234,7 +1263,11 @@ void dq_pipe_kernel(BwdArgs a) {
   }
   wait_all_vm();
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(don[kk]));
+  for (int kk = 0; kk < D / 16; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[kk][e] = (half_t)(-c * (float)qf[kk][e]);
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[kk]), "+v"(don[kk]));
 
   const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
   const int nunits = (kv_end + T::KT - 1) / T::KT;
@@ -1328,15 +1361,16 @@ void dq_pipe_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) dq[db][j] = 0.f;
 
-  const float c = a.c;
   const float inf = __builtin_inff();
-  // Pipeline registers: S^T, dPd^T of the current unit; dS'^T of the previous one.
-  float16v s_cur, dp_cur;
+  // Accumulator starts: LSE and Delta of the lane's query in every value.
+  float16v lse16, delta16;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    s_cur[j] = 0.f;
-    dp_cur[j] = delta;
+    lse16[j] = lse;
+    delta16[j] = delta;
   }
+  // Pipeline registers: Sl^T, dPd^T of the current unit; dS'^T of the previous one.
+  float16v s_cur = lse16, dp_cur = delta16;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
     s_cur = mfma32(*reinterpret_cast<const half8*>(lds + r_off[kk]), qf[kk], s_cur);
@@ -1370,15 +1404,16 @@ void dq_pipe_kernel(BwdArgs a) {
     const int ka = c_key;
     c_key += T::KT;
 
-    float lse_u = lse;
     if constexpr (CAUSAL) {
       if (ka > q0w) {
-        lse_u = inf;  // every key of the unit follows every query of the wave
+        // every key of the unit follows every query of the wave
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s_cur[j] = inf;
       } else if (ka == q0w) {
         // diagonal unit: key 16h + 8g + e (value j = 8h + e) is kept iff <= query ql
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          if (16 * (j >> 3) + 8 * g + (j & 7) > ql) s_cur[j] = -inf;
+          if (16 * (j >> 3) + 8 * g + (j & 7) > ql) s_cur[j] = inf;
       }
     }
 
@@ -1398,9 +1433,7 @@ void dq_pipe_kernel(BwdArgs a) {
       else if constexpr (kind == 1) return *reinterpret_cast<const half8*>(k_nxt + r_off[q]);
       else return *reinterpret_cast<const half8*>(v_nxt + r_off[q]);
     };
-    float16v s_nx, dp_nx;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) s_nx[j] = 0.f;
+    float16v s_nx = lse16, dp_nx = delta16;
     auto run_task = [&](auto t_c, const half8& op) {
       constexpr int t = decltype(t_c)::value;
       constexpr int kind = t % 3, q = t / 3;
@@ -1412,11 +1445,11 @@ void dq_pipe_kernel(BwdArgs a) {
     half8 sa[2];
     float pexp[16];
     // Vector work on value pairs in two stages placed in different groups:
-    //   A: p = exp2(s c - lse)      B: dS' = p dPd, packed to fp16.
+    //   A: p = exp2(-Sl)      B: dS' = p dPd, packed to fp16.
     auto stage_a = [&](int pr) {
       float p2[2];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -lse_u));
+      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(-s_cur[2 * pr + e]);
       asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
       pexp[2 * pr] = p2[0];
       pexp[2 * pr + 1] = p2[1];
@@ -1433,10 +1466,7 @@ void dq_pipe_kernel(BwdArgs a) {
 
     half8 op[NTASK];
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" : "+v"(lse_u));
     static_for<0, kLead>([&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
-#pragma unroll
-    for (int j = 0; j < 16; ++j) dp_nx[j] = delta;
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NTASK>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
