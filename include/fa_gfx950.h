@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 /* Error codes returned before any HIP call is made. */
 #define FA_OK 0
@@ -60,7 +60,8 @@ extern "C" {
 #define FA_ERR_BAD_TILING (-6)         /* no compiled kernel for this tiling     */
 #define FA_ERR_MISALIGNED (-7)         /* a tensor pointer is not 16-byte aligned */
 
-/* 16-bit storage type of IEEE binary16 elements. */
+/* 16-bit storage type of the tensor elements: IEEE binary16 for the entry
+ * points without a suffix, bfloat16 for the _bf16 ones. */
 typedef uint16_t fa_half_t;
 
 /* Forward: o = softmax(scale * q k^T [+ causal mask]) v, and lse (base 2).
@@ -124,6 +125,42 @@ int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                     float* delta, fa_half_t* dq,
                     int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                     float scale, int causal, void* stream);
+
+/* bfloat16 twins of the launches above: same arguments, same semantics and
+ * checks, q/k/v/o/dO/dq/dk/dv holding bfloat16 (lse and delta stay float32;
+ * arithmetic in fp32, P and dS rounded to bfloat16 for the MFMAs, the
+ * backward's scaled score operands rounded to bfloat16). No counterpart in
+ * the reference, which sends every non-fp16 input to torch SDPA
+ * (attention.py:653-655); they widen the dtypes the GPU path serves. Compiled
+ * for the default tilings; a bf16 call whose kernel has an overridden tiling
+ * without a bf16 build uses the default tiling. */
+int fa_fwd_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                fa_half_t* o, float* lse,
+                int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                float scale, int causal, void* stream);
+int fa_bwd_preprocess_bf16(const fa_half_t* o, const fa_half_t* dO, float* delta,
+                           int64_t B, int64_t Hq, int64_t N, int64_t D, void* stream);
+int fa_bwd_dkdv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                     const fa_half_t* dO, const float* lse, const float* delta,
+                     fa_half_t* dk, fa_half_t* dv,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                     float scale, int causal, void* stream);
+int fa_bwd_dkdv_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                        const fa_half_t* dO, const float* lse, const float* delta,
+                        fa_half_t* dk, fa_half_t* dv,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                        float scale, int causal, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+int fa_bwd_dq_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   const fa_half_t* dO, const float* lse, const float* delta,
+                   fa_half_t* dq,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                   float scale, int causal, void* stream);
+int fa_bwd_dq_delta_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                         const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                         float* delta, fa_half_t* dq,
+                         int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                         float scale, int causal, void* stream);
 
 /* Thread-local description of the last failure on the calling thread
  * ("" if none). The pointer stays valid until the next call on the thread. */

@@ -25,12 +25,13 @@
  *   oracle_bwd             torch fp64 autograd through SDPA; golden fixtures;
  *                          closed forms (constant V -> dQ = dK = 0, N=1);
  *                          GQA group sum == MHA with repeated K/V
- *   oracle_bwd, fold = 1   equal to fold = 0 when c32 is a power of two (the
- *                          fp16 rounding of c32 x is then exact); a numpy
- *                          restatement with np.float16 casts of the scaled
- *                          operands on tiny inputs; differs from fold = 0 by
- *                          no more than a 2^-11 relative operand perturbation
- *                          allows, and does differ at a generic scale
+ *   oracle_bwd, fold = 1/2 equal to fold = 0 when c32 is a power of two (the
+ *                          rounding of c32 x is then exact); a numpy / torch
+ *                          restatement with np.float16 / torch.bfloat16 casts
+ *                          of the scaled operands on tiny inputs; differs from
+ *                          fold = 0 by no more than a half-ulp relative operand
+ *                          perturbation allows, and does differ at a generic
+ *                          scale
  */
 #include <math.h>
 #include <stdint.h>
@@ -201,11 +202,27 @@ void oracle_bwd_preprocess(const double* o, const double* dO, int64_t rows, int6
   for (int64_t r = 0; r < rows; ++r) delta[r] = dot(o + r * D, dO + r * D, D);
 }
 
-/* fp16(fp32(c32 * x)) for every element: the reference backward's scaled
- * score operands, k_scaled = (k * (sm_scale * _INV_LN2)).to(tl.float16) and
- * q_scaled likewise (attention.py:435, 515): an fp32 product, rounded to fp16. */
-static void scaled_half(const double* x, int64_t n, float c32, double* out) {
-  for (int64_t i = 0; i < n; ++i) out[i] = oracle_round_half((double)(c32 * (float)x[i]));
+/* Round a float to the nearest bfloat16 value (ties to even), widened back. */
+static double round_bf16(float f) {
+  uint32_t b;
+  memcpy(&b, &f, sizeof b);
+  b += 0x7fffu + ((b >> 16) & 1u);
+  b &= 0xffff0000u;
+  float r;
+  memcpy(&r, &b, sizeof r);
+  return (double)r;
+}
+
+/* rnd(fp32(c32 * x)) for every element, rnd = fp16 (fold = 1) or bf16
+ * (fold = 2): the reference backward's scaled score operands,
+ * k_scaled = (k * (sm_scale * _INV_LN2)).to(tl.float16) and q_scaled
+ * likewise (attention.py:435, 515), an fp32 product rounded to the element
+ * type (bf16 is this build's added element type). */
+static void scaled_operand(const double* x, int64_t n, float c32, int fold, double* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float p = c32 * (float)x[i];
+    out[i] = fold == 2 ? round_bf16(p) : oracle_round_half((double)p);
+  }
 }
 
 /* Backward from the saved base-2 LSE (attention.py:258-350, 403-573;
@@ -214,7 +231,7 @@ static void scaled_half(const double* x, int64_t n, float c32, double* out) {
  *           with s_ij = c q_i.k_j (fold = 0, exact), or, as the reference
  *           computes it (fold = 1), s_ij = q_i.fp16(c32 k_j) for dK, dV
  *           (297, 435) and s_ij = fp16(c32 q_i).k_j for dQ (340, 515),
- *           c32 = fp32(fp32(scale) * fp32(1/ln 2))
+ *           c32 = fp32(fp32(scale) * fp32(1/ln 2)); fold = 2 rounds to bf16
  *   dV_j += P_ij dO_i                                          (302)
  *   dP_ij = dO_i . V_j                                         (303, 345)
  *   dS_ij = P_ij (dP_ij - Delta_i)                             (304, 346; the ln2
@@ -241,13 +258,13 @@ void oracle_bwd(const double* q, const double* k, const double* v, const double*
     memset(dV, 0, sizeof(double) * (size_t)(N * D));
     double* ks = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
     double* qs = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
-    if (fold) scaled_half(K, N * D, c32, ks);
+    if (fold) scaled_operand(K, N * D, c32, fold, ks);
     for (int64_t gi = 0; gi < group; ++gi) {
       const int64_t bh = b * Hq + hkv * group + gi;
       const double* Q = q + bh * N * D;
       const double* G = dO + bh * N * D;
       double* dQ = dq + bh * N * D;
-      if (fold) scaled_half(Q, N * D, c32, qs);
+      if (fold) scaled_operand(Q, N * D, c32, fold, qs);
       for (int64_t i = 0; i < N; ++i) {
         const double* qi = Q + i * D;
         const double* gi_row = G + i * D;

@@ -12,7 +12,8 @@ Functions and the reference lines they restate
     bwd(..., fold=False)    dQ, dK, dV from LSE (258-350, 403-573), GQA group sums (503-505),
                             scores c q.k in exact arithmetic
     bwd(..., fold=True)     the same with the reference's fp16-rounded score operands,
-                            fp16(c k) for dK/dV and fp16(c q) for dQ (435, 515)
+                            fp16(c k) for dK/dV and fp16(c q) for dQ (435, 515);
+                            fold="bfloat16" rounds them to bf16 (the added bf16 path)
     round_half              fp16 round-to-nearest-even (the .to(tl.float16) casts)
 """
 
@@ -120,10 +121,16 @@ def bwd_preprocess(o, do) -> np.ndarray:
     return delta
 
 
+_FOLD_MODES = {False: 0, True: 1, "float16": 1, "bfloat16": 2}
+
+
 def bwd(q, k, v, do, lse2, delta, causal: bool, scale: float | None = None, *,
-        fold: bool = False):
+        fold: bool | str = False):
     """(dQ, dK, dV) float64 from the saved base-2 LSE and Delta. ``fold``: score
-    operands rounded as the reference backward rounds them (attention.py:435, 515)."""
+    operands rounded as the reference backward rounds them (attention.py:435,
+    515), to fp16 (True or "float16") or to bf16 ("bfloat16")."""
+    if fold not in _FOLD_MODES:
+        raise ValueError(f"fold must be one of {list(_FOLD_MODES)}")
     q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
     lse2, delta = _f64(lse2), _f64(delta)
     B, Hq, Hkv, N, D = _dims(q, k, v)
@@ -132,13 +139,13 @@ def bwd(q, k, v, do, lse2, delta, causal: bool, scale: float | None = None, *,
     dk = np.empty_like(k)
     dv = np.empty_like(v)
     _load().oracle_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(lse2), _ptr(delta),
-                       B, Hq, Hkv, N, D, scale, int(causal), int(fold), _ptr(dq), _ptr(dk),
+                       B, Hq, Hkv, N, D, scale, int(causal), _FOLD_MODES[fold], _ptr(dq), _ptr(dk),
                        _ptr(dv))
     return dq, dk, dv
 
 
 def attention(q, k, v, do, causal: bool, scale: float | None = None, *, o16=None,
-              fold_bwd: bool = False):
+              fold_bwd: bool | str = False):
     """Full reference computation: O, LSE2, Delta, dQ, dK, dV (float64).
 
     Delta uses the fp16-rounded O the kernel stores, like the reference

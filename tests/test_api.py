@@ -152,6 +152,9 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
     assert d.backend == "triton"
     for D in (32, 64, 128):
         assert attn._decide(_facts(head_dim=D, value_head_dim=D)).backend == "triton"
+    # bfloat16 is served too (the reference sends it to SDPA, attention.py:653-656)
+    d = attn._decide(_facts(dtype=torch.bfloat16))
+    assert d.backend == "triton" and "bfloat16" in d.reason
 
 
 @pytest.mark.parametrize(
@@ -160,8 +163,8 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
         (dict(kv_len=64), "self-attention"),
         (dict(value_head_dim=32), "equal query/key and value head sizes"),
         (dict(device_type="cpu"), "requires a CUDA tensor"),
-        (dict(dtype=torch.bfloat16), "supports float16"),
-        (dict(dtype=torch.float32), "supports float16"),
+        (dict(dtype=torch.float32), "supports float16 and bfloat16"),
+        (dict(dtype=torch.float64), "supports float16 and bfloat16"),
         (dict(head_dim=96, value_head_dim=96), "head_dim must be one of (32, 64, 128)"),
         (dict(q_len=1 << 24, kv_len=1 << 24), "too long"),
         (dict(arch="gfx942:sramecc+:xnack-"), "gfx950"),

@@ -10,14 +10,14 @@ import pytest
 from triton_flash_attention import _lib, compile_check
 
 REMARKS = """\
-fa_fwd.hip:61:1: remark: Function Name: _ZN2fa15fwd_pipe_kernelILi64ELb1ELi4ELi1EEEvNS_7FwdArgsE [-Rpass-analysis=kernel-resource-usage]
+fa_fwd.hip:61:1: remark: Function Name: _ZN2fa15fwd_pipe_kernelILi64ELb1ELi4ELi1ENS_3F16EEEvNS_7FwdArgsE [-Rpass-analysis=kernel-resource-usage]
 fa_fwd.hip:61:1: remark:     TotalSGPRs: 64 [-Rpass-analysis=kernel-resource-usage]
 fa_fwd.hip:61:1: remark:     VGPRs: 168 [-Rpass-analysis=kernel-resource-usage]
 fa_fwd.hip:61:1: remark:     AGPRs: 0 [-Rpass-analysis=kernel-resource-usage]
 fa_fwd.hip:61:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]
 fa_fwd.hip:61:1: remark:     Occupancy [waves/SIMD]: 3 [-Rpass-analysis=kernel-resource-usage]
 fa_fwd.hip:61:1: remark:     LDS Size [bytes/block]: 49152 [-Rpass-analysis=kernel-resource-usage]
-fa_bwd.hip:37:1: remark: Function Name: _ZN2fa17preprocess_kernelILi32EEEvPKDF16_S2_Pfl [-Rpass-analysis=kernel-resource-usage]
+fa_bwd.hip:37:1: remark: Function Name: _ZN2fa17preprocess_kernelILi32ENS_3F16EEEvPKDF16_S3_Pfl [-Rpass-analysis=kernel-resource-usage]
 fa_bwd.hip:37:1: remark:     VGPRs: 16 [-Rpass-analysis=kernel-resource-usage]
 fa_bwd.hip:37:1: remark:     AGPRs: 0 [-Rpass-analysis=kernel-resource-usage]
 fa_bwd.hip:37:1: remark:     ScratchSize [bytes/lane]: 12 [-Rpass-analysis=kernel-resource-usage]
@@ -30,19 +30,19 @@ def test_resource_report_parsing():
     ks = compile_check.parse_resource_usage(REMARKS)
     # c++filt demangles the first; the second (fp16 pointer arguments) may stay
     # mangled there and is named by the fallback decoder instead.
-    assert [k.name.split("(")[0] for k in ks] == ["fa::fwd_pipe_kernel<64, true, 4, 1>",
-                                                  "fa::preprocess_kernel<32>"]
+    assert [k.name.split("(")[0] for k in ks] == ["fa::fwd_pipe_kernel<64, true, 4, 1, fa::F16>",
+                                                  "fa::preprocess_kernel<32, fa::F16>"]
     fwd, pre = ks
     assert (fwd.vgprs, fwd.agprs, fwd.scratch, fwd.occupancy, fwd.lds) == (168, 0, 0, 3, 49152)
     assert (pre.vgprs, pre.scratch, pre.occupancy) == (16, 12, 8)
     spills, missing = compile_check.spilling_defaults(ks)
-    assert [k.name.split("(")[0] for k in spills] == ["fa::preprocess_kernel<32>"]
-    assert "fa::dkdv_pipe_kernel<64, true, 4>" in missing
+    assert [k.name.split("(")[0] for k in spills] == ["fa::preprocess_kernel<32, fa::F16>"]
+    assert "fa::dkdv_pipe_kernel<64, true, 4, fa::BF16>" in missing
 
 
 def test_fallback_names_for_undemangled_kernels():
-    assert compile_check._short_name("_ZN2fa17preprocess_kernelILi128EEEvPKDF16_S2_Pfl") == \
-        "fa::preprocess_kernel<128>(...)"
+    assert compile_check._short_name("_ZN2fa17preprocess_kernelILi128ENS_4BF16EEEvPKDF16_S3_Pfl") == \
+        "fa::preprocess_kernel<128, fa::BF16>(...)"
     assert compile_check._short_name("_ZN2fa14dq_pipe_kernelILi32ELb0ELi4EEEvNS_7BwdArgsE") == \
         "fa::dq_pipe_kernel<32, false, 4>(...)"
     assert compile_check._short_name("_ZN2fa19split_reduce_kernelEPKfPDF16_S2_li") == \

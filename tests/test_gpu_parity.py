@@ -23,6 +23,8 @@ import torch
 from fa_testutil import (
     CONFIGS,
     LSE_TOL,
+    MAX_ABS_TOL,
+    REL_L2_TOL,
     assert_close,
     errors,
     make_inputs,
@@ -376,3 +378,75 @@ def test_full_config_matches_fp32_reference(name, causal):
     }
     if N * N * D * G <= 2 ** 32:
         check_against_oracle(got, qs, ks, vs, dos, causal, tag=f"{name} oracle slice")
+
+
+# ---------------------------------------------------------------------------
+# bfloat16, an element type this build adds (the reference sends bf16 to torch
+# SDPA, attention.py:653-656). bf16's unit roundoff (2^-9) is 4x fp16's
+# (2^-11), so O, dQ, dK, dV get 4x the fp16 tolerances; LSE is an fp32
+# quantity of inputs that are exact in the oracle and keeps its tolerance.
+# The backward is compared with the oracle's bf16-rounded score operands.
+# ---------------------------------------------------------------------------
+BF16_MAX_ABS_TOL = 4 * MAX_ABS_TOL
+BF16_REL_L2_TOL = 4 * REL_L2_TOL
+
+
+def check_bf16_against_oracle(got, q, k, v, do, causal, scale=None, tag=""):
+    f = lambda t: t.float().numpy()
+    ref = oracle.attention(f(q), f(k), f(v), f(do), causal, scale,
+                           o16=got["o16"].float().numpy(), fold_bwd="bfloat16")
+    report = {}
+    for name in ("o", "dq", "dk", "dv"):
+        report[name] = assert_close(f"{tag} {name}", got[name], ref[name],
+                                    max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL)
+    lse_err = float(np.max(np.abs(got["lse"] - ref["lse"])))
+    assert lse_err <= LSE_TOL, f"{tag} lse: max-abs {lse_err:.3e} (tol {LSE_TOL:.0e})"
+    _note(f"{tag}: " + ", ".join(f"{k}={v[0]:.2e}/{v[1]:.2e}" for k, v in report.items())
+          + f", lse={lse_err:.2e}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sequence", [17, 129])
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_bf16_reference_shapes_match_oracle(sequence, head_dim, causal):
+    q, k, v, do = make_inputs(1, 2, 2, sequence, head_dim, seed=123, mult=0.5, do_mult=0.1,
+                              dtype=torch.bfloat16)
+    got = run_kernel(q, k, v, do, causal)
+    assert got["o16"].dtype == torch.bfloat16
+    check_bf16_against_oracle(got, q, k, v, do, causal,
+                              tag=f"bf16 N={sequence} D={head_dim} causal={causal}")
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_bf16_gqa_tail_matches_oracle(head_dim):
+    q, k, v, do = make_inputs(2, 6, 3, 300, head_dim, seed=55, dtype=torch.bfloat16)
+    for causal in (False, True):
+        got = run_kernel(q, k, v, do, causal)
+        check_bf16_against_oracle(got, q, k, v, do, causal,
+                                  tag=f"bf16 GQA 6->3 N=300 D={head_dim} causal={causal}")
+
+
+def test_bf16_dispatch_selects_the_custom_kernel():
+    q = torch.randn(1, 2, 64, 64, device=DEV, dtype=torch.bfloat16)
+    d = explain_dispatch(q, q, q)
+    assert d.backend == "triton" and "bfloat16" in d.reason
+
+
+def test_bf16_full_c2_matches_fp32_reference():
+    cfg = CONFIGS["c2"]
+    B, Hq, Hkv, N, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["N"], cfg["D"]
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, cfg["seed"], cfg["mult"], dtype=torch.bfloat16)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    qa, ka, va = (t.clone().requires_grad_() for t in (qd, kd, vd))
+    out = scaled_dot_product_attention(qa, ka, va, is_causal=True, backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qa, ka, va), dod)
+    _, lse = _ops.flash_fwd(qd, kd, vd, True, D ** -0.5)
+    torch.cuda.synchronize()
+    ref = torch_reference_fp32(qd, kd, vd, dod, True, o16=out.detach())
+    torch.cuda.synchronize()
+    for tname, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert t.dtype == torch.bfloat16 and torch.isfinite(t).all()
+        ma, rl = assert_close(f"bf16 c2 {tname}", t.float(), ref[tname],
+                              max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL)
+        _note(f"  bf16 c2 {tname}: max-abs {ma:.3e} rel-L2 {rl:.3e}")
+    assert float((lse - ref["lse"]).abs().max()) <= LSE_TOL

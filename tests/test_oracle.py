@@ -257,13 +257,18 @@ def _scale_with_c32(target: float) -> float:
     raise AssertionError("no fp32 scale found")
 
 
-def _numpy_folded_bwd(q, k, v, do, lse2, delta, causal, scale):
-    """Tiny-input restatement in numpy (float16 casts via numpy, not the oracle)."""
+def _numpy_folded_bwd(q, k, v, do, lse2, delta, causal, scale, fold=True):
+    """Tiny-input restatement in numpy (float16 casts via numpy, bfloat16 casts
+    via torch; not the oracle's rounding code)."""
     B, Hq, N, D = q.shape
     Hkv = k.shape[1]
     G = Hq // Hkv
     c32 = np.float32(scale) * np.float32(INV_LN2)
-    f16 = lambda x: (c32 * x.astype(np.float32)).astype(np.float16).astype(np.float64)
+    if fold == "bfloat16":
+        f16 = lambda x: torch.from_numpy(c32 * x.astype(np.float32)).to(torch.bfloat16) \
+            .double().numpy()
+    else:
+        f16 = lambda x: (c32 * x.astype(np.float32)).astype(np.float16).astype(np.float64)
     dq = np.zeros(q.shape)
     dk = np.zeros(k.shape)
     dv = np.zeros(v.shape)
@@ -292,38 +297,42 @@ def test_folded_backward_is_exact_when_c_is_a_power_of_two():
         _, lse = oracle.fwd(q, k, v, causal, scale)
         delta = oracle.bwd_preprocess(oracle.round_half(oracle.fwd(q, k, v, causal, scale)[0]), do)
         exact = oracle.bwd(q, k, v, do, lse, delta, causal, scale)
-        folded = oracle.bwd(q, k, v, do, lse, delta, causal, scale, fold=True)
-        for a, b in zip(folded, exact):
-            # only the double vs fp32 value of c separates them (~1e-8 relative)
-            assert _maxdiff(a, b) <= 1e-6 * max(1.0, float(np.abs(b).max()))
+        for fold in (True, "bfloat16"):  # x/8 has <= 4 significant bits: exact in both
+            folded = oracle.bwd(q, k, v, do, lse, delta, causal, scale, fold=fold)
+            for a, b in zip(folded, exact):
+                # only the double vs fp32 value of c separates them (~1e-8 relative)
+                assert _maxdiff(a, b) <= 1e-6 * max(1.0, float(np.abs(b).max()))
 
 
+@pytest.mark.parametrize("fold", [True, "bfloat16"])
 @pytest.mark.parametrize("causal", [False, True])
-def test_folded_backward_matches_numpy_restatement(causal):
+def test_folded_backward_matches_numpy_restatement(causal, fold):
     q, k, v, do = _inputs(1, 4, 2, 9, 16, seed=31)
     qn, kn, vn, don = (t.numpy().astype(np.float64) for t in (q, k, v, do))
     scale = 0.37
     o, lse = oracle.fwd(qn, kn, vn, causal, scale)
     delta = oracle.bwd_preprocess(oracle.round_half(o), don)
-    got = oracle.bwd(qn, kn, vn, don, lse, delta, causal, scale, fold=True)
-    want = _numpy_folded_bwd(qn, kn, vn, don, lse, delta, causal, scale)
+    got = oracle.bwd(qn, kn, vn, don, lse, delta, causal, scale, fold=fold)
+    want = _numpy_folded_bwd(qn, kn, vn, don, lse, delta, causal, scale, fold)
     for a, b in zip(got, want):
         assert _maxdiff(a, b) < 1e-12
 
 
-def test_folded_backward_differs_within_the_operand_rounding():
+@pytest.mark.parametrize("fold,bound", [(True, 2e-3), ("bfloat16", 8e-3)])
+def test_folded_backward_differs_within_the_operand_rounding(fold, bound):
     q, k, v, do = _inputs(1, 2, 2, 40, 64, seed=32)
     qn, kn, vn, don = (t.numpy().astype(np.float64) for t in (q, k, v, do))
     o, lse = oracle.fwd(qn, kn, vn, True)
     delta = oracle.bwd_preprocess(oracle.round_half(o), don)
     exact = oracle.bwd(qn, kn, vn, don, lse, delta, True)
-    folded = oracle.bwd(qn, kn, vn, don, lse, delta, True, fold=True)
+    folded = oracle.bwd(qn, kn, vn, don, lse, delta, True, fold=fold)
     for a, b in zip(folded, exact):
         rel = float(np.linalg.norm(a - b) / np.linalg.norm(b))
         # the rounding is applied (dV too: its P uses the rounded K) ...
         assert rel > 1e-7
-        # ... and is no larger than a half-ulp (2^-11) operand perturbation
-        assert rel < 2e-3
+        # ... and is no larger than a half-ulp operand perturbation (2^-11 for
+        # fp16, 2^-8 for bf16) allows
+        assert rel < bound
 
 
 # ---------------------------------------------------------------------------

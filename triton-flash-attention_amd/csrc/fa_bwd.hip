@@ -36,7 +36,7 @@ namespace fa {
 // --------------------------------------------------------------------------
 // Delta = rowsum(O * dO)
 // --------------------------------------------------------------------------
-template <int D>
+template <int D, class E = F16>
 __global__ __launch_bounds__(256) void preprocess_kernel(const half_t* __restrict__ o,
                                                          const half_t* __restrict__ dO,
                                                          float* __restrict__ delta,
@@ -51,35 +51,42 @@ __global__ __launch_bounds__(256) void preprocess_kernel(const half_t* __restric
     const half8 ov = *reinterpret_cast<const half8*>(o + off);
     const half8 dv = *reinterpret_cast<const half8*>(dO + off);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc = fmaf((float)ov[i], (float)dv[i], acc);
+    for (int i = 0; i < 8; ++i) acc = fmaf(elem_to_f32<E>(ov[i]), elem_to_f32<E>(dv[i]), acc);
   }
 #pragma unroll
   for (int off = TPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
   if (cc == 0 && row < rows) delta[row] = acc;
 }
 
-hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
-                             int D, hipStream_t stream) {
+template <class E>
+hipError_t launch_preprocess_e(const half_t* o, const half_t* dO, float* delta, int64_t rows,
+                               int D, hipStream_t stream) {
   const int64_t threads = rows * (D / 8);
   const int64_t blocks = (threads + 255) / 256;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   switch (D) {
     case 32:
-      hipLaunchKernelGGL(preprocess_kernel<32>, dim3((unsigned)blocks), dim3(256), 0, stream, o,
-                         dO, delta, rows);
+      hipLaunchKernelGGL((preprocess_kernel<32, E>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                         o, dO, delta, rows);
       break;
     case 64:
-      hipLaunchKernelGGL(preprocess_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, o,
-                         dO, delta, rows);
+      hipLaunchKernelGGL((preprocess_kernel<64, E>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                         o, dO, delta, rows);
       break;
     case 128:
-      hipLaunchKernelGGL(preprocess_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, stream,
+      hipLaunchKernelGGL((preprocess_kernel<128, E>), dim3((unsigned)blocks), dim3(256), 0, stream,
                          o, dO, delta, rows);
       break;
     default:
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
+                             int D, int dtype, hipStream_t stream) {
+  return dtype == kBF16 ? launch_preprocess_e<BF16>(o, dO, delta, rows, D, stream)
+                        : launch_preprocess_e<F16>(o, dO, delta, rows, D, stream);
 }
 
 template <int V>
@@ -95,8 +102,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // --------------------------------------------------------------------------
-// dK/dV split reduction: out[i] = fp16(sum_s part[s][i]) in split order.
+// dK/dV split reduction: out[i] = E(sum_s part[s][i]) in split order.
 // --------------------------------------------------------------------------
+template <class E = F16>
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
                                                            half_t* __restrict__ dk,
                                                            half_t* __restrict__ dv,
@@ -110,17 +118,21 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   for (int sp = 1; sp < nsplit; ++sp) acc += src[(int64_t)sp * 2 * plane4];
   half4 h;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) h[e] = (half_t)acc[e];
+  for (int e = 0; e < 4; ++e) h[e] = to_elem<E>(acc[e]);
   *reinterpret_cast<half4*>((is_v ? dv : dk) + 4 * j) = h;
 }
 
 hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_t plane_elems,
-                               int nsplit, hipStream_t stream) {
+                               int nsplit, int dtype, hipStream_t stream) {
   const int64_t plane4 = plane_elems / 4;
   const int64_t blocks = (2 * plane4 + 255) / 256;
   if (plane_elems % 4 != 0 || blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, part, dk,
-                     dv, plane4, nsplit);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(split_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       part, dk, dv, plane4, nsplit);
+  else
+    hipLaunchKernelGGL(split_reduce_kernel<F16>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       part, dk, dv, plane4, nsplit);
   return hipGetLastError();
 }
 
@@ -155,7 +167,7 @@ constexpr bool dkdv_tiling_ok() {
          3 * (2 * QT * D + 256) * 2 <= 160 * 1024;
 }
 
-template <int D, bool CAUSAL, int NW, int QT>
+template <int D, bool CAUSAL, int NW, int QT, class E = F16>
 __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   using T = DkdvTile<D, NW, QT>;
   using Dma = DmaStager<D, QT, NW>;
@@ -203,7 +215,7 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kf[kk][e] = (half_t)(a.c * (float)kf[kk][e]);
+    for (int e = 0; e < 8; ++e) kf[kk][e] = to_elem<E>(a.c * elem_to_f32<E>(kf[kk][e]));
     asm volatile("" : "+v"(kf[kk]));
   }
 
@@ -307,8 +319,8 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
           const int off = 32 * qb * D + r_off[kk];
-          s[qb] = mfma32(*reinterpret_cast<const half8*>(Qs + off), kf[kk], s[qb]);
-          dp[qb] = mfma32(*reinterpret_cast<const half8*>(dOs + off), vf[kk], dp[qb]);
+          s[qb] = mma<E>(*reinterpret_cast<const half8*>(Qs + off), kf[kk], s[qb]);
+          dp[qb] = mma<E>(*reinterpret_cast<const half8*>(dOs + off), vf[kk], dp[qb]);
         }
       }
     }
@@ -351,15 +363,15 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
           const int q = qa + result_row(j, g);
           if (q >= N || (CAUSAL && q < krow)) pj = 0.f;
         }
-        pa[j >> 3][j & 7] = (half_t)pj;
-        sa[j >> 3][j & 7] = (half_t)(pj * (dp[qb][j] - del_v[j]));
+        pa[j >> 3][j & 7] = to_elem<E>(pj);
+        sa[j >> 3][j & 7] = to_elem<E>(pj * (dp[qb][j] - del_v[j]));
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
-          dv[db] = mfma32(dot_f[h][db], pa[h], dv[db]);
-          dk[db] = mfma32(qt_f[h][db], sa[h], dk[db]);
+          dv[db] = mma<E>(dot_f[h][db], pa[h], dv[db]);
+          dk[db] = mma<E>(qt_f[h][db], sa[h], dk[db]);
         }
     }
     // Step st+1's tile complete for this wave, then published; slot st is free.
@@ -408,15 +420,15 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
     for (int jq = 0; jq < 4; ++jq) {
       const uint32_t off = (uint32_t)(krow * D + 32 * db + 8 * jq + 4 * g) * 2u;
       buf_store_b64(rdk, off,
-                    pack4_half(dk[db][4 * jq] * scale, dk[db][4 * jq + 1] * scale,
+                    pack4<E>(dk[db][4 * jq] * scale, dk[db][4 * jq + 1] * scale,
                                dk[db][4 * jq + 2] * scale, dk[db][4 * jq + 3] * scale));
       buf_store_b64(rdv, off,
-                    pack4_half(dv[db][4 * jq], dv[db][4 * jq + 1], dv[db][4 * jq + 2],
+                    pack4<E>(dv[db][4 * jq], dv[db][4 * jq + 1], dv[db][4 * jq + 2],
                                dv[db][4 * jq + 3]));
     }
 }
 
-template <int D, bool CAUSAL, int NW, int QT>
+template <int D, bool CAUSAL, int NW, int QT, class E = F16>
 hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DkdvTile<D, NW, QT>;
   BwdArgs b = a;
@@ -424,7 +436,7 @@ hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((dkdv_kernel<D, CAUSAL, NW, QT>), dim3((unsigned)blocks), dim3(T::NT), 0,
+  hipLaunchKernelGGL((dkdv_kernel<D, CAUSAL, NW, QT, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
   return hipGetLastError();
 }
@@ -489,7 +501,7 @@ constexpr bool dkdv_pipe_tiling_ok() {
 #define FA_DKDV_LEAD 3
 #endif
 
-template <int D, bool CAUSAL, int NW>
+template <int D, bool CAUSAL, int NW, class E = F16>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(DkdvPipeTile<D, NW>::WGS_PER_CU)))
 void dkdv_pipe_kernel(BwdArgs a) {
@@ -534,13 +546,13 @@ void dkdv_pipe_kernel(BwdArgs a) {
   for (int kk = 0; kk < D / 16; ++kk) {
     const uint32_t off = (uint32_t)(krow * D + 16 * kk + 8 * g) * 2u;
     kf[kk] = __builtin_bit_cast(half8, buf_load_b128(rk, off));
-    vn[kk] = -__builtin_bit_cast(half8, buf_load_b128(rv, off));
+    vn[kk] = neg8(__builtin_bit_cast(half8, buf_load_b128(rv, off)));
   }
   wait_all_vm();
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kf[kk][e] = (half_t)(-c * (float)kf[kk][e]);
+    for (int e = 0; e < 8; ++e) kf[kk][e] = to_elem<E>(-c * elem_to_f32<E>(kf[kk][e]));
   // Opaque from here on, so that the operands are not recomputed inside the loop.
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(kf[kk]), "+v"(vn[kk]));
@@ -709,8 +721,8 @@ void dkdv_pipe_kernel(BwdArgs a) {
     s_cur = table16(fl + lse_table(0, c_row));
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      s_cur = mfma32(*reinterpret_cast<const half8*>(lds + r_off[kk]), kf[kk], s_cur);
-      dp_cur = mfma32(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), vn[kk], dp_cur);
+      s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + r_off[kk]), kf[kk], s_cur);
+      dp_cur = mma<E>(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), vn[kk], dp_cur);
     }
   }
   half8 pa_prev[2], sa_prev[2];
@@ -725,8 +737,8 @@ void dkdv_pipe_kernel(BwdArgs a) {
   // D = 128 holds dK and dV (128 registers) in AGPRs, beside ~250 VGPRs.
   constexpr bool kAgprAcc = D > 64;
   auto acc_mfma = [&](float16v& acc, const half8& a, const half8& b) {
-    if constexpr (kAgprAcc) mfma32_agpr(acc, a, b);
-    else acc = mfma32(a, b, acc);
+    if constexpr (kAgprAcc) mma_agpr<E>(acc, a, b);
+    else acc = mma<E>(a, b, acc);
   };
   auto dvdk = [&](const half_t* slot) {
 #pragma unroll
@@ -787,8 +799,8 @@ void dkdv_pipe_kernel(BwdArgs a) {
       constexpr int h = q / (D / 32), db = q % (D / 32);
       if constexpr (kind == 0) acc_mfma(dv[db], op, pa_prev[h]);
       else if constexpr (kind == 1) acc_mfma(dk[db], op, sa_prev[h]);
-      else if constexpr (kind == 2) s_nx = mfma32(op, kf[q], s_nx);
-      else dp_nx = mfma32(op, vn[q], dp_nx);
+      else if constexpr (kind == 2) s_nx = mma<E>(op, kf[q], s_nx);
+      else dp_nx = mma<E>(op, vn[q], dp_nx);
     };
     half8 pa[2], sa[2];
     // Vector work on value pairs (2pr, 2pr+1) in two stages placed in
@@ -810,8 +822,8 @@ void dkdv_pipe_kernel(BwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int j = 2 * pr + e;
-        pp[e] = (half_t)pexp[j];
-        ss[e] = (half_t)(pexp[j] * dp_cur[j]);
+        pp[e] = to_elem<E>(pexp[j]);
+        ss[e] = to_elem<E>(pexp[j] * dp_cur[j]);
       }
       asm volatile("" : "+v"(pp), "+v"(ss));
       const int j = 2 * pr;
@@ -911,15 +923,15 @@ void dkdv_pipe_kernel(BwdArgs a) {
     for (int jq = 0; jq < 4; ++jq) {
       const uint32_t off = (uint32_t)(krow * D + 32 * db + 8 * jq + 4 * g) * 2u;
       buf_store_b64(rdk, off,
-                    pack4_half(dk[db][4 * jq] * nscale, dk[db][4 * jq + 1] * nscale,
+                    pack4<E>(dk[db][4 * jq] * nscale, dk[db][4 * jq + 1] * nscale,
                                dk[db][4 * jq + 2] * nscale, dk[db][4 * jq + 3] * nscale));
       buf_store_b64(rdv, off,
-                    pack4_half(dv[db][4 * jq], dv[db][4 * jq + 1], dv[db][4 * jq + 2],
+                    pack4<E>(dv[db][4 * jq], dv[db][4 * jq + 1], dv[db][4 * jq + 2],
                                dv[db][4 * jq + 3]));
     }
 }
 
-template <int D, bool CAUSAL, int NW>
+template <int D, bool CAUSAL, int NW, class E = F16>
 hipError_t dkdv_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DkdvPipeTile<D, NW>;
   BwdArgs b = a;
@@ -927,7 +939,7 @@ hipError_t dkdv_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((dkdv_pipe_kernel<D, CAUSAL, NW>), dim3((unsigned)blocks), dim3(T::NT), 0,
+  hipLaunchKernelGGL((dkdv_pipe_kernel<D, CAUSAL, NW, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
   return hipGetLastError();
 }
@@ -959,7 +971,7 @@ constexpr bool dq_tiling_ok() {
          3 * (2 * KT * D) * 2 <= 160 * 1024;
 }
 
-template <int D, bool CAUSAL, int NW, int KT>
+template <int D, bool CAUSAL, int NW, int KT, class E = F16>
 __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   using T = DqTile<D, NW, KT>;
   using Dma = DmaStager<D, KT, NW>;
@@ -1007,7 +1019,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[kk][e] = (half_t)(a.c * (float)qf[kk][e]);
+    for (int e = 0; e < 8; ++e) qf[kk][e] = to_elem<E>(a.c * elem_to_f32<E>(qf[kk][e]));
     asm volatile("" : "+v"(qf[kk]));
   }
 
@@ -1084,8 +1096,8 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
           const int off = 32 * kb * D + r_off[kk];
-          s[kb] = mfma32(*reinterpret_cast<const half8*>(Ks + off), qf[kk], s[kb]);
-          dp[kb] = mfma32(*reinterpret_cast<const half8*>(Vs + off), dof[kk], dp[kb]);
+          s[kb] = mma<E>(*reinterpret_cast<const half8*>(Ks + off), qf[kk], s[kb]);
+          dp[kb] = mma<E>(*reinterpret_cast<const half8*>(Vs + off), dof[kk], dp[kb]);
         }
       }
     }
@@ -1107,12 +1119,12 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
           const int key = ka + result_row(j, g);
           if (key >= N || (CAUSAL && key > qrow)) pj = 0.f;
         }
-        sa[j >> 3][j & 7] = (half_t)(pj * (dp[kb][j] - delta));
+        sa[j >> 3][j & 7] = to_elem<E>(pj * (dp[kb][j] - delta));
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) dq[db] = mfma32(kt_f[h][db], sa[h], dq[db]);
+        for (int db = 0; db < D / 32; ++db) dq[db] = mma<E>(kt_f[h][db], sa[h], dq[db]);
     }
     wait_vm_and_barrier<(T::AHEAD - 1) * IPT>();
   };
@@ -1135,19 +1147,19 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
     for (int jq = 0; jq < 4; ++jq) {
       const uint32_t off = (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u;
       buf_store_b64(rdq, off,
-                    pack4_half(dq[db][4 * jq] * scale, dq[db][4 * jq + 1] * scale,
+                    pack4<E>(dq[db][4 * jq] * scale, dq[db][4 * jq + 1] * scale,
                                dq[db][4 * jq + 2] * scale, dq[db][4 * jq + 3] * scale));
     }
 }
 
-template <int D, bool CAUSAL, int NW, int KT>
+template <int D, bool CAUSAL, int NW, int KT, class E = F16>
 hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DqTile<D, NW, KT>;
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((dq_kernel<D, CAUSAL, NW, KT>), dim3((unsigned)blocks), dim3(T::NT), 0,
+  hipLaunchKernelGGL((dq_kernel<D, CAUSAL, NW, KT, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
   return hipGetLastError();
 }
@@ -1196,7 +1208,7 @@ constexpr bool dq_pipe_tiling_ok() {
 #define FA_DQ_LEAD 3
 #endif
 
-template <int D, bool CAUSAL, int NW>
+template <int D, bool CAUSAL, int NW, class E = F16>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(DqPipeTile<D, NW>::WGS_PER_CU)))
 void dq_pipe_kernel(BwdArgs a) {
@@ -1240,7 +1252,7 @@ void dq_pipe_kernel(BwdArgs a) {
   for (int kk = 0; kk < D / 16; ++kk) {
     const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u;
     qf[kk] = __builtin_bit_cast(half8, buf_load_b128(rq, off));
-    don[kk] = -__builtin_bit_cast(half8, buf_load_b128(rdo, off));
+    don[kk] = neg8(__builtin_bit_cast(half8, buf_load_b128(rdo, off)));
   }
   const float lse = buf_load_f32(rl, (uint32_t)qrow * 4u);
   float delta;
@@ -1254,7 +1266,7 @@ void dq_pipe_kernel(BwdArgs a) {
       const half8 ov = __builtin_bit_cast(
           half8, buf_load_b128(ro, (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part = fmaf((float)ov[e], -(float)don[kk][e], part);
+      for (int e = 0; e < 8; ++e) part = fmaf(elem_to_f32<E>(ov[e]), -elem_to_f32<E>(don[kk][e]), part);
     }
     delta = halves_sum(part);
     if (g == 0 && qrow < N) a.delta_out[(int64_t)head * N + qrow] = delta;
@@ -1265,7 +1277,7 @@ void dq_pipe_kernel(BwdArgs a) {
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[kk][e] = (half_t)(-c * (float)qf[kk][e]);
+    for (int e = 0; e < 8; ++e) qf[kk][e] = to_elem<E>(-c * elem_to_f32<E>(qf[kk][e]));
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[kk]), "+v"(don[kk]));
 
@@ -1373,8 +1385,8 @@ void dq_pipe_kernel(BwdArgs a) {
   float16v s_cur = lse16, dp_cur = delta16;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
-    s_cur = mfma32(*reinterpret_cast<const half8*>(lds + r_off[kk]), qf[kk], s_cur);
-    dp_cur = mfma32(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), don[kk], dp_cur);
+    s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + r_off[kk]), qf[kk], s_cur);
+    dp_cur = mma<E>(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), don[kk], dp_cur);
   }
   half8 sa_prev[2];
 #pragma unroll
@@ -1385,8 +1397,8 @@ void dq_pipe_kernel(BwdArgs a) {
   // D = 128 holds dQ (64 registers) in AGPRs.
   constexpr bool kAgprAcc = D > 64;
   auto acc_mfma = [&](float16v& acc, const half8& a, const half8& b) {
-    if constexpr (kAgprAcc) mfma32_agpr(acc, a, b);
-    else acc = mfma32(a, b, acc);
+    if constexpr (kAgprAcc) mma_agpr<E>(acc, a, b);
+    else acc = mma<E>(a, b, acc);
   };
   auto dq_mm = [&](const half_t* slot) {
 #pragma unroll
@@ -1439,8 +1451,8 @@ void dq_pipe_kernel(BwdArgs a) {
       constexpr int kind = t % 3, q = t / 3;
       constexpr int h = q / (D / 32), db = q % (D / 32);
       if constexpr (kind == 0) acc_mfma(dq[db], op, sa_prev[h]);
-      else if constexpr (kind == 1) s_nx = mfma32(op, qf[q], s_nx);
-      else dp_nx = mfma32(op, don[q], dp_nx);
+      else if constexpr (kind == 1) s_nx = mma<E>(op, qf[q], s_nx);
+      else dp_nx = mma<E>(op, don[q], dp_nx);
     };
     half8 sa[2];
     float pexp[16];
@@ -1457,7 +1469,7 @@ void dq_pipe_kernel(BwdArgs a) {
     auto stage_b = [&](int pr) {
       half2v ss;
 #pragma unroll
-      for (int e = 0; e < 2; ++e) ss[e] = (half_t)(pexp[2 * pr + e] * dp_cur[2 * pr + e]);
+      for (int e = 0; e < 2; ++e) ss[e] = to_elem<E>(pexp[2 * pr + e] * dp_cur[2 * pr + e]);
       asm volatile("" : "+v"(ss));
       const int j = 2 * pr;
       sa[j >> 3][j & 7] = ss[0];
@@ -1516,79 +1528,75 @@ void dq_pipe_kernel(BwdArgs a) {
     for (int jq = 0; jq < 4; ++jq) {
       const uint32_t off = (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u;
       buf_store_b64(rdq, off,
-                    pack4_half(dq[db][4 * jq] * nscale, dq[db][4 * jq + 1] * nscale,
+                    pack4<E>(dq[db][4 * jq] * nscale, dq[db][4 * jq + 1] * nscale,
                                dq[db][4 * jq + 2] * nscale, dq[db][4 * jq + 3] * nscale));
     }
 }
 
-template <int D, bool CAUSAL, int NW>
+template <int D, bool CAUSAL, int NW, class E = F16>
 hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DqPipeTile<D, NW>;
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW>), dim3((unsigned)blocks), dim3(T::NT), 0,
+  hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, int NW, int TILE>
+template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
 constexpr void* dkdv_entry() {
   if constexpr (dkdv_tiling_ok<D, NW, TILE>())
-    return (void*)&dkdv_launch<D, CAUSAL, NW, TILE>;
+    return (void*)&dkdv_launch<D, CAUSAL, NW, TILE, E>;
   else
     return nullptr;
 }
-template <int D, bool CAUSAL, int NW, int TILE>
+template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
 constexpr void* dkdv_pipe_entry() {
   static_assert(TILE == 32, "the pipelined dK/dV kernel streams 32-query units");
   if constexpr (dkdv_pipe_tiling_ok<D, NW>())
-    return (void*)&dkdv_pipe_launch<D, CAUSAL, NW>;
+    return (void*)&dkdv_pipe_launch<D, CAUSAL, NW, E>;
   else
     return nullptr;
 }
-template <int D, bool CAUSAL, int NW, int TILE>
+template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
 constexpr void* dq_pipe_entry() {
   static_assert(TILE == 32, "the pipelined dQ kernel streams 32-key units");
   if constexpr (dq_pipe_tiling_ok<D, NW>())
-    return (void*)&dq_pipe_launch<D, CAUSAL, NW>;
+    return (void*)&dq_pipe_launch<D, CAUSAL, NW, E>;
   else
     return nullptr;
 }
-template <int D, bool CAUSAL, int NW, int TILE>
+template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
 constexpr void* dq_entry() {
   if constexpr (dq_tiling_ok<D, NW, TILE>())
-    return (void*)&dq_launch<D, CAUSAL, NW, TILE>;
+    return (void*)&dq_launch<D, CAUSAL, NW, TILE, E>;
   else
     return nullptr;
 }
 
-#define FA_BWD_VARIANT(ENTRY, NW, TILE, FLAGS)                                  \
-  {                                                                             \
-    NW, 32 * NW, TILE,                                                          \
-    {                                                                           \
-      {ENTRY<32, false, NW, TILE>(), ENTRY<32, true, NW, TILE>()},              \
-      {ENTRY<64, false, NW, TILE>(), ENTRY<64, true, NW, TILE>()},              \
-      {ENTRY<128, false, NW, TILE>(), ENTRY<128, true, NW, TILE>()},            \
-    },                                                                          \
-    FLAGS                                                                       \
-  }
+// FA_BWD_VARIANT_BF also compiles the tiling for bf16; bf16 is compiled only
+// for the tilings the default table uses, to bound the build.
+#define FA_BWD_VARIANT(ENTRY, NW, TILE, FLAGS) \
+  {NW, 32 * NW, TILE, {FA_ENTRIES(ENTRY, F16, NW, TILE), FA_NO_ENTRIES}, FLAGS}
+#define FA_BWD_VARIANT_BF(ENTRY, NW, TILE, FLAGS) \
+  {NW, 32 * NW, TILE, {FA_ENTRIES(ENTRY, F16, NW, TILE), FA_ENTRIES(ENTRY, BF16, NW, TILE)}, FLAGS}
 
 static const Variant kDkdvVariants[] = {
     FA_BWD_VARIANT(dkdv_entry, 4, 64, 0),
     FA_BWD_VARIANT(dkdv_entry, 4, 32, 0),
     FA_BWD_VARIANT(dkdv_entry, 2, 64, 0),
     FA_BWD_VARIANT(dkdv_entry, 8, 64, 0),
-    FA_BWD_VARIANT(dkdv_pipe_entry, 4, 32, 0),
+    FA_BWD_VARIANT_BF(dkdv_pipe_entry, 4, 32, 0),
 };
 
 static const Variant kDqVariants[] = {
     FA_BWD_VARIANT(dq_entry, 4, 64, 0),
-    FA_BWD_VARIANT(dq_entry, 4, 32, 0),
+    FA_BWD_VARIANT_BF(dq_entry, 4, 32, 0),
     FA_BWD_VARIANT(dq_entry, 2, 64, 0),
     FA_BWD_VARIANT(dq_entry, 8, 64, 0),
-    FA_BWD_VARIANT(dq_pipe_entry, 4, 32, kFusesDelta),
+    FA_BWD_VARIANT_BF(dq_pipe_entry, 4, 32, kFusesDelta),
 };
 
 const Variant* dkdv_variants(int* count) {

@@ -32,6 +32,12 @@ int hip_result(hipError_t e, const char* what) {
   return fail((int)e, "%s: %s (hipError %d)", what, hipGetErrorString(e), (int)e);
 }
 
+// hip_result for a launch of the entry point `name` ("<name> launch: ...").
+int launch_result(hipError_t e, const char* name) {
+  if (e == hipSuccess) return hip_result(e, name);
+  return fail((int)e, "%s launch: %s (hipError %d)", name, hipGetErrorString(e), (int)e);
+}
+
 // Process-wide tiling choice per (kernel, D index, causal); -1 = table default.
 int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
                                        {{-1, -1}, {-1, -1}, {-1, -1}},
@@ -74,15 +80,21 @@ const fa::Variant* registry(int kind, int* count) {
 }
 
 // A variant is usable for (D, causal) when it was compiled for that head_dim.
-bool usable(const fa::Variant& v, int di, int causal) { return v.fn[di][causal ? 1 : 0] != nullptr; }
+// (bf16 is compiled for the default tilings only.)
+bool usable(const fa::Variant& v, int di, int causal, int dt = fa::kF16) {
+  return v.fn[dt][di][causal ? 1 : 0] != nullptr;
+}
 
-const fa::Variant* select(int kind, int di, int causal, int* index) {
+// The tiling used for (kind, D, causal, element type): the override if set,
+// else the default; a bf16 call whose overridden tiling has no bf16 build
+// uses the default tiling.
+const fa::Variant* select(int kind, int di, int causal, int* index, int dt = fa::kF16) {
   int count = 0;
   const fa::Variant* vs = registry(kind, &count);
   if (!vs) return nullptr;
   int v = g_override[kind][di][causal ? 1 : 0];
-  if (v < 0) v = kDefault[kind][di][causal ? 1 : 0];
-  if (v >= count || !usable(vs[v], di, causal)) return nullptr;
+  if (v < 0 || (v < count && !usable(vs[v], di, causal, dt))) v = kDefault[kind][di][causal ? 1 : 0];
+  if (v >= count || !usable(vs[v], di, causal, dt)) return nullptr;
   if (index) *index = v;
   return &vs[v];
 }
@@ -178,16 +190,16 @@ int fa_abi_version(void) { return FA_ABI_VERSION; }
 
 const char* fa_last_error(void) { return g_last_error; }
 
-int fa_fwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o, float* lse,
-           int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
-           void* stream) {
-  if (!q || !k || !v || !o || !lse) return fail(FA_ERR_NULL_POINTER, "fa_fwd: null pointer");
+static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                    const fa_half_t* v, fa_half_t* o, float* lse, int64_t B, int64_t Hq,
+                    int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
+  if (!q || !k || !v || !o || !lse) return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
-  if ((rc = check_aligned("fa_fwd", {q, k, v, o, lse}))) return rc;
+  if ((rc = check_aligned(name, {q, k, v, o, lse}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd: no kernel for the selected tiling");
+  const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
+  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::FwdArgs a;
   a.q = reinterpret_cast<const fa::half_t*>(q);
   a.k = reinterpret_cast<const fa::half_t*>(k);
@@ -201,39 +213,40 @@ int fa_fwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t
   a.BH = (int)(B * Hq);
   a.num_tiles = 0;
   a.c = scale * fa::kLog2e;
-  auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
-  return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_fwd launch");
+  auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
+  return launch_result(fn(a, static_cast<hipStream_t>(stream)), name);
 }
 
-int fa_bwd_preprocess(const fa_half_t* o, const fa_half_t* dO, float* delta, int64_t B,
-                      int64_t Hq, int64_t N, int64_t D, void* stream) {
-  if (!o || !dO || !delta) return fail(FA_ERR_NULL_POINTER, "fa_bwd_preprocess: null pointer");
+static int preprocess_impl(int dt, const char* name, const fa_half_t* o, const fa_half_t* dO,
+                           float* delta, int64_t B, int64_t Hq, int64_t N, int64_t D,
+                           void* stream) {
+  if (!o || !dO || !delta) return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, 1, N, D);
   if (rc) return rc;
-  if ((rc = check_aligned("fa_bwd_preprocess", {o, dO, delta}))) return rc;
-  return hip_result(fa::launch_preprocess(reinterpret_cast<const fa::half_t*>(o),
+  if ((rc = check_aligned(name, {o, dO, delta}))) return rc;
+  return launch_result(fa::launch_preprocess(reinterpret_cast<const fa::half_t*>(o),
                                           reinterpret_cast<const fa::half_t*>(dO), delta,
-                                          B * Hq * N, (int)D, static_cast<hipStream_t>(stream)),
-                    "fa_bwd_preprocess launch");
+                                          B * Hq * N, (int)D, dt, static_cast<hipStream_t>(stream)),
+                    name);
 }
 
-int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
-                const float* lse, const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B,
-                int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
-                void* stream) {
+static int dkdv_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                     const fa_half_t* v, const fa_half_t* dO, const float* lse,
+                     const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq,
+                     int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
   if (!q || !k || !v || !dO || !lse || !delta || !dk || !dv)
-    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dkdv: null pointer");
+    return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
-  if ((rc = check_aligned("fa_bwd_dkdv", {q, k, v, dO, lse, delta, dk, dv}))) return rc;
+  if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dkdv: no kernel for the selected tiling");
+  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
   a.dv = reinterpret_cast<fa::half_t*>(dv);
-  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
-  return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_bwd_dkdv launch");
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
+  return launch_result(fn(a, static_cast<hipStream_t>(stream)), name);
 }
 
 int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
@@ -245,71 +258,73 @@ int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   return split_workspace_bytes(dkdv_split(*var, B, Hkv, N), B, Hkv, N, D);
 }
 
-int fa_bwd_dkdv_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
-                   const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dk,
-                   fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
-                   float scale, int causal, void* workspace, int64_t workspace_bytes,
-                   void* stream) {
+static int dkdv_ws_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                        const fa_half_t* v, const fa_half_t* dO, const float* lse,
+                        const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq,
+                        int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+                        void* workspace, int64_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !dO || !lse || !delta || !dk || !dv)
-    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dkdv_ws: null pointer");
+    return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
-  if ((rc = check_aligned("fa_bwd_dkdv_ws", {q, k, v, dO, lse, delta, dk, dv}))) return rc;
+  if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dkdv_ws: no kernel for the selected tiling");
+  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
   a.dv = reinterpret_cast<fa::half_t*>(dv);
   const int nsplit = dkdv_split(*var, B, Hkv, N);
   const int64_t need = split_workspace_bytes(nsplit, B, Hkv, N, D);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   if (need == 0 || workspace == nullptr || workspace_bytes < need) {
     if (need > 0 && workspace != nullptr)
-      return fail(FA_ERR_BAD_SHAPE, "fa_bwd_dkdv_ws: workspace of %lld bytes is smaller than the "
-                  "%lld bytes fa_bwd_dkdv_workspace_bytes reports", (long long)workspace_bytes,
+      return fail(FA_ERR_BAD_SHAPE, "%s: workspace of %lld bytes is smaller than the "
+                  "%lld bytes fa_bwd_dkdv_workspace_bytes reports", name, (long long)workspace_bytes,
                   (long long)need);
-    return hip_result(fn(a, s), "fa_bwd_dkdv_ws launch");
+    return launch_result(fn(a, s), name);
   }
-  if ((rc = check_aligned("fa_bwd_dkdv_ws", {workspace}))) return rc;
+  if ((rc = check_aligned(name, {workspace}))) return rc;
   a.nsplit = nsplit;
   a.part = static_cast<float*>(workspace);
   hipError_t e = fn(a, s);
-  if (e != hipSuccess) return hip_result(e, "fa_bwd_dkdv_ws launch");
-  return hip_result(fa::launch_split_reduce(a.part, a.dk, a.dv, B * Hkv * N * D, nsplit, s),
-                    "fa_bwd_dkdv_ws reduce launch");
+  if (e != hipSuccess) return launch_result(e, name);
+  return launch_result(fa::launch_split_reduce(a.part, a.dk, a.dv, B * Hkv * N * D, nsplit, dt, s),
+                    name);
 }
 
-int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
-              const float* lse, const float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
-              int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
+static int dq_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                   const fa_half_t* v, const fa_half_t* dO, const float* lse, const float* delta,
+                   fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                   float scale, int causal, void* stream) {
   if (!q || !k || !v || !dO || !lse || !delta || !dq)
-    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dq: null pointer");
+    return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
-  if ((rc = check_aligned("fa_bwd_dq", {q, k, v, dO, lse, delta, dq}))) return rc;
+  if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq: no kernel for the selected tiling");
+  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
+  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
-  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
-  return hip_result(fn(a, static_cast<hipStream_t>(stream)), "fa_bwd_dq launch");
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
+  return launch_result(fn(a, static_cast<hipStream_t>(stream)), name);
 }
 
-int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
-                    const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
-                    fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
-                    float scale, int causal, void* stream) {
+static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                         const fa_half_t* v, const fa_half_t* o, const fa_half_t* dO,
+                         const float* lse, float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
+                         int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+                         void* stream) {
   if (!q || !k || !v || !o || !dO || !lse || !delta || !dq)
-    return fail(FA_ERR_NULL_POINTER, "fa_bwd_dq_delta: null pointer");
+    return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
-  if ((rc = check_aligned("fa_bwd_dq_delta", {q, k, v, o, dO, lse, delta, dq}))) return rc;
+  if ((rc = check_aligned(name, {q, k, v, o, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq_delta: no kernel for the selected tiling");
+  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
+  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   hipStream_t s = static_cast<hipStream_t>(stream);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
@@ -319,11 +334,89 @@ int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
   } else {
     hipError_t e = fa::launch_preprocess(reinterpret_cast<const fa::half_t*>(o),
                                          reinterpret_cast<const fa::half_t*>(dO), delta,
-                                         B * Hq * N, (int)D, s);
-    if (e != hipSuccess) return hip_result(e, "fa_bwd_dq_delta preprocess launch");
+                                         B * Hq * N, (int)D, dt, s);
+    if (e != hipSuccess) return launch_result(e, name);
   }
-  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[fa::head_dim_index(D)][causal ? 1 : 0]);
-  return hip_result(fn(a, s), "fa_bwd_dq_delta launch");
+  auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
+  return launch_result(fn(a, s), name);
+}
+
+// ---- exported launches: fp16 (the reference's dtype) and bf16 twins ------
+int fa_fwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o, float* lse,
+           int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+           void* stream) {
+  return fwd_impl(fa::kF16, "fa_fwd", q, k, v, o, lse, B, Hq, Hkv, N, D, scale, causal, stream);
+}
+int fa_fwd_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
+                float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale,
+                int causal, void* stream) {
+  return fwd_impl(fa::kBF16, "fa_fwd_bf16", q, k, v, o, lse, B, Hq, Hkv, N, D, scale, causal,
+                  stream);
+}
+int fa_bwd_preprocess(const fa_half_t* o, const fa_half_t* dO, float* delta, int64_t B,
+                      int64_t Hq, int64_t N, int64_t D, void* stream) {
+  return preprocess_impl(fa::kF16, "fa_bwd_preprocess", o, dO, delta, B, Hq, N, D, stream);
+}
+int fa_bwd_preprocess_bf16(const fa_half_t* o, const fa_half_t* dO, float* delta, int64_t B,
+                           int64_t Hq, int64_t N, int64_t D, void* stream) {
+  return preprocess_impl(fa::kBF16, "fa_bwd_preprocess_bf16", o, dO, delta, B, Hq, N, D, stream);
+}
+int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
+                const float* lse, const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B,
+                int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+                void* stream) {
+  return dkdv_impl(fa::kF16, "fa_bwd_dkdv", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv, N, D,
+                   scale, causal, stream);
+}
+int fa_bwd_dkdv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                     const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dk,
+                     fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                     float scale, int causal, void* stream) {
+  return dkdv_impl(fa::kBF16, "fa_bwd_dkdv_bf16", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv,
+                   N, D, scale, causal, stream);
+}
+int fa_bwd_dkdv_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dk,
+                   fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                   float scale, int causal, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
+  return dkdv_ws_impl(fa::kF16, "fa_bwd_dkdv_ws", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv,
+                      N, D, scale, causal, workspace, workspace_bytes, stream);
+}
+int fa_bwd_dkdv_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                        const fa_half_t* dO, const float* lse, const float* delta,
+                        fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv,
+                        int64_t N, int64_t D, float scale, int causal, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
+  return dkdv_ws_impl(fa::kBF16, "fa_bwd_dkdv_ws_bf16", q, k, v, dO, lse, delta, dk, dv, B, Hq,
+                      Hkv, N, D, scale, causal, workspace, workspace_bytes, stream);
+}
+int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
+              const float* lse, const float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
+              int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
+  return dq_impl(fa::kF16, "fa_bwd_dq", q, k, v, dO, lse, delta, dq, B, Hq, Hkv, N, D, scale,
+                 causal, stream);
+}
+int fa_bwd_dq_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dq,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale,
+                   int causal, void* stream) {
+  return dq_impl(fa::kBF16, "fa_bwd_dq_bf16", q, k, v, dO, lse, delta, dq, B, Hq, Hkv, N, D,
+                 scale, causal, stream);
+}
+int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                    const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
+                    fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                    float scale, int causal, void* stream) {
+  return dq_delta_impl(fa::kF16, "fa_bwd_dq_delta", q, k, v, o, dO, lse, delta, dq, B, Hq, Hkv,
+                       N, D, scale, causal, stream);
+}
+int fa_bwd_dq_delta_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                         const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
+                         fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                         float scale, int causal, void* stream) {
+  return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_bf16", q, k, v, o, dO, lse, delta, dq, B, Hq,
+                       Hkv, N, D, scale, causal, stream);
 }
 
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4) {

@@ -69,6 +69,51 @@ __device__ __forceinline__ void agpr_acc_drain() {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+// ---------------------------------------------------------------------------
+// Element types. Tensors are fp16 (F16) or bf16 (BF16); the kernels move and
+// stage both as 16-bit containers (half_t, half8) and only the conversions
+// and the MFMA opcode depend on the type. Round-to-nearest-even both ways.
+// ---------------------------------------------------------------------------
+struct F16 {};
+struct BF16 {};
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+template <class E> __device__ __forceinline__ half_t to_elem(float x);
+template <> __device__ __forceinline__ half_t to_elem<F16>(float x) { return (half_t)x; }
+template <> __device__ __forceinline__ half_t to_elem<BF16>(float x) {
+  return __builtin_bit_cast(half_t, (__bf16)x);
+}
+template <class E> __device__ __forceinline__ float elem_to_f32(half_t h);
+template <> __device__ __forceinline__ float elem_to_f32<F16>(half_t h) { return (float)h; }
+template <> __device__ __forceinline__ float elem_to_f32<BF16>(half_t h) {
+  return (float)__builtin_bit_cast(__bf16, h);
+}
+
+// D(32x32, fp32) += A(32x16) * B(16x32) in the element type.
+template <class E> __device__ __forceinline__ float16v mma(half8 a, half8 b, float16v c);
+template <> __device__ __forceinline__ float16v mma<F16>(half8 a, half8 b, float16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ float16v mma<BF16>(half8 a, half8 b, float16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+// mfma32_agpr in the element type.
+template <class E> __device__ __forceinline__ void mma_agpr(float16v& acc, half8 a, half8 b);
+template <> __device__ __forceinline__ void mma_agpr<F16>(float16v& acc, half8 a, half8 b) {
+  mfma32_agpr(acc, a, b);
+}
+template <> __device__ __forceinline__ void mma_agpr<BF16>(float16v& acc, half8 a, half8 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// Sign flip of 8 packed 16-bit values (the same bits for fp16 and bf16).
+__device__ __forceinline__ half8 neg8(half8 v) {
+  const u32x4 m = {0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+  return __builtin_bit_cast(half8, __builtin_bit_cast(u32x4, v) ^ m);
+}
+
 // Row permutation applied when a 32-row A operand is read from LDS so that
 // the MFMA result rows held by lane half g, values j = 0..7 / 8..15, are the
 // CONTIGUOUS operand rows 8g..8g+7 / 16+8g..16+8g+7. That makes a lane's
@@ -151,6 +196,19 @@ __device__ __forceinline__ u32x2 pack4_half(float a, float b, float c, float d) 
   h[1] = (half_t)b;
   h[2] = (half_t)c;
   h[3] = (half_t)d;
+  return __builtin_bit_cast(u32x2, h);
+}
+// The same for the element type E.
+template <class E> __device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d);
+template <> __device__ __forceinline__ u32x2 pack4<F16>(float a, float b, float c, float d) {
+  return pack4_half(a, b, c, d);
+}
+template <> __device__ __forceinline__ u32x2 pack4<BF16>(float a, float b, float c, float d) {
+  bf16x4 h;
+  h[0] = (__bf16)a;
+  h[1] = (__bf16)b;
+  h[2] = (__bf16)c;
+  h[3] = (__bf16)d;
   return __builtin_bit_cast(u32x2, h);
 }
 

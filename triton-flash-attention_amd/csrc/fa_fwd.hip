@@ -57,7 +57,7 @@ constexpr float kSumLimit = 256.0f;
 template <int V>
 using ic = std::integral_constant<int, V>;
 
-template <int D, bool CAUSAL, int NW, int BN>
+template <int D, bool CAUSAL, int NW, int BN, class E = F16>
 __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, NW, BN>;
   using Dma = DmaStager<D, BN, NW>;
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) sbuf[SB][kb][j] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) sbuf[SB][kb] = mfma32(ka[kb][kk], qf[kk], sbuf[SB][kb]);
+      for (int kk = 0; kk < D / 16; ++kk) sbuf[SB][kb] = mma<E>(ka[kb][kk], qf[kk], sbuf[SB][kb]);
     }
   };
 
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
           for (int j = 0; j < 16; ++j) {
             const float p = exp2_fast(fmaf(s[kb][j], c, nm));
             ls4[j & 3] += p;
-            pk[kb][j >> 3][j & 7] = (half_t)p;
+            pk[kb][j >> 3][j & 7] = to_elem<E>(p);
           }
         return (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);
       };
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
           for (int j = 0; j < 16; ++j) s2[kb][j] = 0.f;
 #pragma unroll
           for (int kk = 0; kk < D / 16; ++kk)
-            s2[kb] = mfma32(*reinterpret_cast<const half8*>(Ks + 32 * kb * D + k_off[kk]), qf[kk],
+            s2[kb] = mma<E>(*reinterpret_cast<const half8*>(Ks + 32 * kb * D + k_off[kk]), qf[kk],
                             s2[kb]);
         }
         float mx = -INFINITY;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int db = 0; db < D / 32; ++db) o[db] = mfma32(va[kb][h][db], pk[kb][h], o[db]);
+          for (int db = 0; db < D / 32; ++db) o[db] = mma<E>(va[kb][h][db], pk[kb][h], o[db]);
     }
     // (4) tile t+2 complete for this wave (AHEAD-2 newer tiles may still be
     //     in flight), then publish it and release slot t to the next DMA.
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   for (int db = 0; db < D / 32; ++db)
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq) {
-      const u32x2 v = pack4_half(o[db][4 * jq] * inv, o[db][4 * jq + 1] * inv,
+      const u32x2 v = pack4<E>(o[db][4 * jq] * inv, o[db][4 * jq + 1] * inv,
                                  o[db][4 * jq + 2] * inv, o[db][4 * jq + 3] * inv);
       buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u, v);
     }
@@ -367,7 +367,7 @@ __device__ __forceinline__ void static_for_fwd_issue(F&& f) {
   fwd_static_for<0, N>(f);
 }
 
-template <int D, bool CAUSAL, int NW, int UPS>
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS>::WGS_PER_CU)))
 void fwd_pipe_kernel(FwdArgs a) {
@@ -491,7 +491,7 @@ void fwd_pipe_kernel(FwdArgs a) {
   for (int j = 0; j < 16; ++j) s_cur[j] = 0.f;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
-    s_cur = mfma32(*reinterpret_cast<const half8*>(lds + k_off[kk]), qf[kk], s_cur);
+    s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + k_off[kk]), qf[kk], s_cur);
   half8 pa_prev[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -503,7 +503,7 @@ void fwd_pipe_kernel(FwdArgs a) {
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
-        o[db] = mfma32(tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h], o[db]);
+        o[db] = mma<E>(tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h], o[db]);
   };
 
   int c_key = 0;  // first key of the unit the body works on
@@ -547,8 +547,8 @@ void fwd_pipe_kernel(FwdArgs a) {
       constexpr int t = decltype(t_c)::value;
       constexpr int q = t / 2;
       constexpr int h = q / (D / 32), db = q % (D / 32);
-      if constexpr (t % 2 == 0) s_nx = mfma32(op, qf[q], s_nx);
-      else o[db] = mfma32(op, pa_prev[h], o[db]);
+      if constexpr (t % 2 == 0) s_nx = mma<E>(op, qf[q], s_nx);
+      else o[db] = mma<E>(op, pa_prev[h], o[db]);
     };
     half8 pa[2];
     float pexp[16];
@@ -568,7 +568,7 @@ void fwd_pipe_kernel(FwdArgs a) {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         lsum[e] += pexp[2 * pr + e];
-        pp[e] = (half_t)pexp[2 * pr + e];
+        pp[e] = to_elem<E>(pexp[2 * pr + e]);
       }
       asm volatile("" : "+v"(pp));
       const int j = 2 * pr;
@@ -614,7 +614,7 @@ void fwd_pipe_kernel(FwdArgs a) {
       for (int j = 0; j < 16; ++j) {
         const float p = exp2_fast(fmaf(s_cur[j], c, -m));
         l_u += p;
-        pa[j >> 3][j & 7] = (half_t)p;
+        pa[j >> 3][j & 7] = to_elem<E>(p);
       }
     }
     l += l_u;
@@ -650,41 +650,41 @@ void fwd_pipe_kernel(FwdArgs a) {
   for (int db = 0; db < D / 32; ++db)
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq) {
-      const u32x2 v = pack4_half(o[db][4 * jq] * invl, o[db][4 * jq + 1] * invl,
+      const u32x2 v = pack4<E>(o[db][4 * jq] * invl, o[db][4 * jq + 1] * invl,
                                  o[db][4 * jq + 2] * invl, o[db][4 * jq + 3] * invl);
       buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u, v);
     }
   if (g == 0 && qrow < N) a.lse[(int64_t)head * N + qrow] = m + log2_fast(lt);
 }
 
-template <int D, bool CAUSAL, int NW, int UPS>
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdPipeTile<D, NW, UPS>;
   FwdArgs b = a;
   b.num_tiles = (a.N + T::BM - 1) / T::BM;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS>), dim3((unsigned)blocks), dim3(T::NT),
+  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS, E>), dim3((unsigned)blocks), dim3(T::NT),
                      0, stream, b);
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, int NW, int UPS>
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 constexpr void* fwd_pipe_entry() {
   if constexpr (fwd_pipe_tiling_ok<D, NW, UPS>())
-    return (void*)&fwd_pipe_launch<D, CAUSAL, NW, UPS>;
+    return (void*)&fwd_pipe_launch<D, CAUSAL, NW, UPS, E>;
   else
     return nullptr;
 }
 
-template <int D, bool CAUSAL, int NW, int BN>
+template <int D, bool CAUSAL, int NW, int BN, class E = F16>
 hipError_t fwd_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdTile<D, NW, BN>;
   FwdArgs b = a;
   b.num_tiles = (a.N + T::BM - 1) / T::BM;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, NW, BN>), dim3((unsigned)blocks), dim3(T::NT), 0,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, NW, BN, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
   return hipGetLastError();
 }
@@ -697,41 +697,29 @@ constexpr bool fwd_tiling_ok() {
          4 * (2 * BN * D) * 2 <= 160 * 1024;  // NSTAGE slots of K + V tiles
 }
 
-template <int D, bool CAUSAL, int NW, int BN>
+template <int D, bool CAUSAL, int NW, int BN, class E = F16>
 constexpr void* fwd_entry() {
   if constexpr (fwd_tiling_ok<D, NW, BN>())
-    return (void*)&fwd_launch<D, CAUSAL, NW, BN>;
+    return (void*)&fwd_launch<D, CAUSAL, NW, BN, E>;
   else
     return nullptr;
 }
 
-#define FA_FWD_VARIANT(NW, BN)                                                  \
-  {                                                                             \
-    NW, 32 * NW, BN,                                                            \
-    {                                                                           \
-      {fwd_entry<32, false, NW, BN>(), fwd_entry<32, true, NW, BN>()},          \
-      {fwd_entry<64, false, NW, BN>(), fwd_entry<64, true, NW, BN>()},          \
-      {fwd_entry<128, false, NW, BN>(), fwd_entry<128, true, NW, BN>()},        \
-    },                                                                          \
-    0                                                                           \
-  }
+// FA_FWD_VARIANT_BF also compiles the tiling for bf16; bf16 is compiled only
+// for the tilings the default table uses, to bound the build.
+#define FA_FWD_VARIANT(NW, BN) \
+  {NW, 32 * NW, BN, {FA_ENTRIES(fwd_entry, F16, NW, BN), FA_NO_ENTRIES}, 0}
+#define FA_FWD_VARIANT_BF(NW, BN) \
+  {NW, 32 * NW, BN, {FA_ENTRIES(fwd_entry, F16, NW, BN), FA_ENTRIES(fwd_entry, BF16, NW, BN)}, 0}
 
 static const Variant kFwdVariants[] = {
     FA_FWD_VARIANT(4, 64),
     FA_FWD_VARIANT(8, 64),
-    FA_FWD_VARIANT(4, 32),
+    FA_FWD_VARIANT_BF(4, 32),
     FA_FWD_VARIANT(2, 64),
     FA_FWD_VARIANT(4, 128),
-    {4, 128, 32,
-     {{fwd_pipe_entry<32, false, 4, 2>(), fwd_pipe_entry<32, true, 4, 2>()},
-      {fwd_pipe_entry<64, false, 4, 2>(), fwd_pipe_entry<64, true, 4, 2>()},
-      {fwd_pipe_entry<128, false, 4, 2>(), fwd_pipe_entry<128, true, 4, 2>()}},
-     0},
-    {4, 128, 32,
-     {{fwd_pipe_entry<32, false, 4, 1>(), fwd_pipe_entry<32, true, 4, 1>()},
-      {fwd_pipe_entry<64, false, 4, 1>(), fwd_pipe_entry<64, true, 4, 1>()},
-      {fwd_pipe_entry<128, false, 4, 1>(), fwd_pipe_entry<128, true, 4, 1>()}},
-     0},
+    {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 2), FA_NO_ENTRIES}, 0},
+    {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe_entry, BF16, 4, 1)}, 0},
 };
 
 const Variant* fwd_variants(int* count) {

@@ -70,9 +70,20 @@ struct Variant {
   int waves;
   int rows;
   int tile;
-  void* fn[3][2];  // [D index: 32, 64, 128][causal]
-  int flags;       // kFusesDelta
+  void* fn[2][3][2];  // [element type: fp16, bf16][D index: 32, 64, 128][causal]; null = not compiled
+  int flags;          // kFusesDelta
 };
+
+// Element type index of Variant::fn.
+enum DType { kF16 = 0, kBF16 = 1 };
+
+// The six launchers (D = 32, 64, 128; bidirectional, causal) of one tiling
+// ENTRY<D, causal, args..., E>(), and an empty table.
+#define FA_ENTRIES(ENTRY, E, ...)                                              \
+  {{ENTRY<32, false, __VA_ARGS__, E>(), ENTRY<32, true, __VA_ARGS__, E>()},    \
+   {ENTRY<64, false, __VA_ARGS__, E>(), ENTRY<64, true, __VA_ARGS__, E>()},    \
+   {ENTRY<128, false, __VA_ARGS__, E>(), ENTRY<128, true, __VA_ARGS__, E>()}}
+#define FA_NO_ENTRIES {{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}}
 
 // The dQ variant can compute Delta itself (BwdArgs::o / delta_out).
 constexpr int kFusesDelta = 1;
@@ -83,11 +94,12 @@ const Variant* dkdv_variants(int* count);
 const Variant* dq_variants(int* count);
 
 // Sum of the nsplit fp32 partial planes into fp16 dK, dV (fixed order).
+// dtype: kF16 or kBF16 (the element type of the 16-bit tensors).
 hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_t plane_elems,
-                               int nsplit, hipStream_t stream);
+                               int nsplit, int dtype, hipStream_t stream);
 
 hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
-                             int D, hipStream_t stream);
+                             int D, int dtype, hipStream_t stream);
 
 inline int head_dim_index(int64_t D) {
   return D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : -1;

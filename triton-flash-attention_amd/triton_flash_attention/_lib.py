@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FA_OK = 0
 FA_ERR_NULL_POINTER = -1
@@ -63,6 +63,11 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "fa_describe_tiling_variant": (_INT, (_INT, _I64, _INT, _INT, _INT_P)),
     "fa_set_tiling": (_INT, (_INT, _I64, _INT, _INT)),
 }
+# bfloat16 twins of the launches: the same arguments.
+for _name in ("fa_fwd", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dkdv_ws", "fa_bwd_dq",
+              "fa_bwd_dq_delta"):
+    SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
+del _name
 
 
 class FlashAttentionError(RuntimeError):

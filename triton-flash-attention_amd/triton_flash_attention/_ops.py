@@ -91,6 +91,23 @@ def _require(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.devic
         raise ValueError(f"{name} must be a GPU tensor")
 
 
+# Element types of the 16-bit tensors and the suffix of their library entry points.
+_ELEM_SUFFIX = {torch.float16: "", torch.bfloat16: "_bf16"}
+
+
+def _elem_dtype(t: torch.Tensor, name: str) -> torch.dtype:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype not in _ELEM_SUFFIX:
+        raise ValueError(f"{name} must be torch.float16 or torch.bfloat16, got {t.dtype}")
+    return t.dtype
+
+
+def _entry(lib, base: str, dtype: torch.dtype):
+    """The library entry point of ``base`` for tensors of ``dtype``."""
+    return getattr(lib, base + _ELEM_SUFFIX[dtype])
+
+
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     """The kernels move 128-bit vectors: a view whose data pointer is not
     16-byte aligned is copied into a fresh (aligned) allocation."""
@@ -111,9 +128,10 @@ def _qkv_dims(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, i
 def flash_fwd(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """O [B,Hq,N,D] fp16 and base-2 LSE [B,Hq,N] fp32."""
+    """O [B,Hq,N,D] (the inputs' fp16 or bf16) and base-2 LSE [B,Hq,N] fp32."""
+    dt = _elem_dtype(q, "q")
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _require(t, name, torch.float16, q.device)
+        _require(t, name, dt, q.device)
     B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     lib = _lib.load()
@@ -121,7 +139,7 @@ def flash_fwd(
     lse = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
     with torch.cuda.device(q.device):
         rc = _launch(
-            "fwd", lib.fa_fwd,
+            "fwd", _entry(lib, "fa_fwd", dt),
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
             B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
         )
@@ -131,8 +149,9 @@ def flash_fwd(
 
 def flash_bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
     """Delta [B,H,N] fp32 = rowsum(O * dO)."""
-    _require(o, "o", torch.float16, o.device)
-    _require(do, "dO", torch.float16, o.device)
+    dt = _elem_dtype(o, "o")
+    _require(o, "o", dt, o.device)
+    _require(do, "dO", dt, o.device)
     if do.shape != o.shape or o.ndim != 4:
         raise ValueError("o and dO must have the same 4-D shape")
     B, H, N, D = o.shape
@@ -140,15 +159,16 @@ def flash_bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
     lib = _lib.load()
     delta = torch.empty((B, H, N), device=o.device, dtype=torch.float32)
     with torch.cuda.device(o.device):
-        rc = _launch("preprocess", lib.fa_bwd_preprocess,
+        rc = _launch("preprocess", _entry(lib, "fa_bwd_preprocess", dt),
                      o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, H, N, D, _stream(o))
     _lib.check(rc)
     return delta
 
 
 def _check_bwd_inputs(q, k, v, do, lse, delta):
+    dt = _elem_dtype(q, "q")
     for name, t in (("q", q), ("k", k), ("v", v), ("dO", do)):
-        _require(t, name, torch.float16, q.device)
+        _require(t, name, dt, q.device)
     for name, t in (("lse", lse), ("delta", delta)):
         _require(t, name, torch.float32, q.device)
     B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
@@ -166,7 +186,7 @@ def _aligned_all(*tensors):
 def flash_bwd_dkdv(
     q, k, v, do, lse, delta, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """dK, dV [B,Hkv,N,D] fp16 (GQA groups reduced in fp32, deterministic).
+    """dK, dV [B,Hkv,N,D] in q's dtype (GQA groups reduced in fp32, deterministic).
 
     Shapes with too few key tiles to fill the GPU get a workspace (from the
     caching allocator) for the library's split-and-reduce mode."""
@@ -181,7 +201,7 @@ def flash_bwd_dkdv(
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
     with torch.cuda.device(q.device):
         rc = _launch(
-            "dkdv", lib.fa_bwd_dkdv_ws,
+            "dkdv", _entry(lib, "fa_bwd_dkdv_ws", q.dtype),
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
             delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
             B, Hq, Hkv, N, D, float(scale), int(bool(causal)),
@@ -192,14 +212,14 @@ def flash_bwd_dkdv(
 
 
 def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.Tensor:
-    """dQ [B,Hq,N,D] fp16."""
+    """dQ [B,Hq,N,D] in q's dtype."""
     B, Hq, Hkv, N, D = _check_bwd_inputs(q, k, v, do, lse, delta)
     q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
     lib = _lib.load()
     dq = torch.empty_like(q)
     with torch.cuda.device(q.device):
         rc = _launch(
-            "dq", lib.fa_bwd_dq,
+            "dq", _entry(lib, "fa_bwd_dq", q.dtype),
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
             delta.data_ptr(), dq.data_ptr(),
             B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
@@ -209,10 +229,10 @@ def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.T
 
 
 def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
-    """Delta [B,H,N] fp32 = rowsum(O * dO) and dQ [B,Hq,N,D] fp16 in one call
-    (one launch when the dQ tiling computes Delta itself)."""
+    """Delta [B,H,N] fp32 = rowsum(O * dO) and dQ [B,Hq,N,D] (q's dtype) in one
+    call (one launch when the dQ tiling computes Delta itself)."""
     B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
-    _require(o, "o", torch.float16, q.device)
+    _require(o, "o", _elem_dtype(q, "q"), q.device)
     if o.shape != q.shape:
         raise ValueError("o must have the shape of q")
     delta = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
@@ -222,7 +242,7 @@ def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
     dq = torch.empty_like(q)
     with torch.cuda.device(q.device):
         rc = _launch(
-            "dq", lib.fa_bwd_dq_delta,
+            "dq", _entry(lib, "fa_bwd_dq_delta", q.dtype),
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
             lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
             B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),

@@ -10,7 +10,9 @@ Dispatch rules (first match wins; reference rules at attention.py:629-670):
   1. cross-attention (N_q != N_kv)          -> torch   (ref 639-642)
   2. value head size != query head size     -> torch   (ref 643-646)
   3. not a GPU ("cuda") tensor              -> torch   (ref 647-648)
-  4. dtype is not float16                   -> torch   (ref 653-656)
+  4. dtype is not float16 or bfloat16       -> torch   (ref 653-656 accepts float16
+                                                        only; bfloat16 is an added
+                                                        dtype of the gfx950 kernels)
   5. head_dim not in (32, 64, 128)          -> torch   (ref 657-661)
   6. sequence too long for 32-bit offsets   -> torch   (no reference counterpart)
   7. device is not gfx950                   -> torch   (replaces ref 662-666, SM >= 8)
@@ -37,6 +39,7 @@ import torch
 from . import _lib, _ops
 
 _SUPPORTED_HEAD_DIMS = (32, 64, 128)
+_SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
 _SUPPORTED_ARCH = "gfx950"
 # Per-head slabs are addressed with 32-bit byte offsets (include/fa_gfx950.h).
 _MAX_SLAB_BYTES = (1 << 31) - 4096 * 128 * 2
@@ -137,9 +140,9 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         )
     if facts.device_type != "cuda":
         return DispatchDecision("torch", "the Triton kernel requires a CUDA tensor")
-    if facts.dtype != torch.float16:
+    if facts.dtype not in _SUPPORTED_DTYPES:
         return DispatchDecision(
-            "torch", "the custom mixed-precision path currently supports float16"
+            "torch", "the custom mixed-precision path currently supports float16 and bfloat16"
         )
     if facts.head_dim not in _SUPPORTED_HEAD_DIMS:
         supported = ", ".join(str(dim) for dim in _SUPPORTED_HEAD_DIMS)
@@ -161,7 +164,8 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         return DispatchDecision("torch", f"{_REASON_LIBRARY}: {facts.library_error}")
     return DispatchDecision(
         "triton",
-        "gfx950 float16 self-attention with a supported head dimension",
+        f"gfx950 {str(facts.dtype).removeprefix('torch.')} self-attention with a supported "
+        "head dimension",
     )
 
 
@@ -244,8 +248,8 @@ def scaled_dot_product_attention(
     """Compute scaled dot-product attention with safe backend selection.
 
     The custom gfx950 path supports forward/backward, causal and bidirectional
-    attention, arbitrary positive sequence lengths, and GQA, for float16
-    self-attention with head_dim 32, 64 or 128. Other inputs fall back to
+    attention, arbitrary positive sequence lengths, and GQA, for float16 or
+    bfloat16 self-attention with head_dim 32, 64 or 128. Other inputs fall back to
     PyTorch when ``backend="auto"``; ``backend="triton"`` requires the custom
     kernel and raises RuntimeError otherwise; ``backend="torch"`` always uses
     PyTorch SDPA.

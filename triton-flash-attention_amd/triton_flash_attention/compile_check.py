@@ -29,20 +29,24 @@ from . import _build
 SUPPORTED_ARCHS = ("gfx950",)
 
 # Kernel instances the default tiling table (kDefault in csrc/fa_capi.hip)
-# selects, as demangled name prefixes, for D = 32, 64, 128, both mask modes.
-DEFAULT_KERNELS = (
-    "fa::fwd_pipe_kernel<32, false, 4, 1>", "fa::fwd_pipe_kernel<32, true, 4, 1>",
-    "fa::fwd_pipe_kernel<64, false, 4, 1>", "fa::fwd_pipe_kernel<64, true, 4, 1>",
-    "fa::fwd_kernel<128, false, 4, 32>", "fa::fwd_kernel<128, true, 4, 32>",
-    "fa::dkdv_pipe_kernel<32, false, 4>", "fa::dkdv_pipe_kernel<32, true, 4>",
-    "fa::dkdv_pipe_kernel<64, false, 4>", "fa::dkdv_pipe_kernel<64, true, 4>",
-    "fa::dkdv_pipe_kernel<128, false, 4>", "fa::dkdv_pipe_kernel<128, true, 4>",
-    "fa::dq_pipe_kernel<32, false, 4>", "fa::dq_pipe_kernel<32, true, 4>",
-    "fa::dq_pipe_kernel<64, false, 4>", "fa::dq_pipe_kernel<64, true, 4>",
-    "fa::dq_kernel<128, false, 4, 32>", "fa::dq_kernel<128, true, 4, 32>",
-    "fa::preprocess_kernel<32>", "fa::preprocess_kernel<64>", "fa::preprocess_kernel<128>",
-    "fa::split_reduce_kernel",
-)
+# selects, as demangled name prefixes, for D = 32, 64, 128, both mask modes
+# and both element types.
+def _defaults() -> tuple[str, ...]:
+    names = []
+    for e in ("fa::F16", "fa::BF16"):
+        for c in ("false", "true"):
+            names += [f"fa::fwd_pipe_kernel<32, {c}, 4, 1, {e}>", f"fa::fwd_pipe_kernel<64, {c}, 4, 1, {e}>",
+                      f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
+                      f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
+                      f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
+                      f"fa::dq_pipe_kernel<32, {c}, 4, {e}>", f"fa::dq_pipe_kernel<64, {c}, 4, {e}>",
+                      f"fa::dq_kernel<128, {c}, 4, 32, {e}>"]
+        names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
+        names.append(f"fa::split_reduce_kernel<{e}>")
+    return tuple(names)
+
+
+DEFAULT_KERNELS = _defaults()
 # The same table as (kernel kind, head_dim) -> default variant index, for the
 # test that keeps this list in step with kDefault (kinds: 0 fwd, 1 dK/dV, 2 dQ).
 DEFAULT_VARIANTS = {
@@ -73,7 +77,7 @@ _NAME = re.compile(r"remark: Function Name: (\S+)")
 
 
 _MANGLED = re.compile(r"^_ZN2fa(\d+)")
-_TARG = re.compile(r"L([ib])(\d+)E")
+_TARG = re.compile(r"L([ib])(\d+)E|NS_\d+(F16|BF16)E")
 
 
 def _short_name(mangled: str) -> str:
@@ -89,8 +93,11 @@ def _short_name(mangled: str) -> str:
     args = []
     if rest.startswith("I"):
         body = rest[1:rest.index("EE") + 1] if "EE" in rest else ""
-        for kind, val in _TARG.findall(body):
-            args.append(("true" if val == "1" else "false") if kind == "b" else val)
+        for kind, val, elem in _TARG.findall(body):
+            if elem:
+                args.append("fa::" + elem)
+            else:
+                args.append(("true" if val == "1" else "false") if kind == "b" else val)
     return f"fa::{name}<{', '.join(args)}>(...)" if args else f"fa::{name}(...)"
 
 
