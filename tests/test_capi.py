@@ -154,6 +154,28 @@ def test_launch_without_a_device_reports_the_hip_error(lib):
     assert "fa_fwd launch" in _lib.last_error()
 
 
+def test_bf16_twins_check_like_fp16_and_fall_back_to_the_default_tiling(lib):
+    """The _bf16 entry points share the fp16 argument checks (named after the
+    bf16 symbol), and a bf16 call whose kernel has an fp16-only tiling
+    override runs the default tiling instead of failing."""
+    import torch
+
+    rc = lib.fa_fwd_bf16(None, P, P, P, P, 1, 2, 2, 64, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_NULL_POINTER and "fa_fwd_bf16" in _lib.last_error()
+    rc = lib.fa_bwd_dq_bf16(P, P, P, P, P, P, P, 1, 2, 2, 64, 48, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_HEAD_DIM
+    fp16_only = [v["variant"] for v in _lib.tiling_variants(_lib.KERNEL_FWD, 64, True)
+                 if v["variant"] != _lib.get_tiling(_lib.KERNEL_FWD, 64, True)["variant"]][0]
+    try:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, fp16_only)
+        rc = lib.fa_fwd_bf16(P, P, P, P, P, 1, 2, 2, 64, 64, 0.125, 1, None)
+        assert rc != _lib.FA_ERR_BAD_TILING
+        if not torch.cuda.is_available():
+            assert rc > 0 and "fa_fwd_bf16 launch" in _lib.last_error()
+    finally:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, -1)
+
+
 def test_dkdv_workspace_sizing_and_rejection(lib):
     # MHA with many key tiles: single pass, no workspace
     assert lib.fa_bwd_dkdv_workspace_bytes(4, 16, 16, 4096, 64, 1) == 0
