@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 /* Error codes returned before any HIP call is made. */
 #define FA_OK 0
@@ -161,6 +161,50 @@ int fa_bwd_dq_delta_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t
                          float* delta, fa_half_t* dq,
                          int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                          float scale, int causal, void* stream);
+
+/* Cross-attention launches: the query length N_q and the key/value length
+ * N_kv differ (q, o, dO, dq, lse, delta are [B, Hq, N_q, ...]; k, v, dk, dv
+ * are [B, Hkv, N_kv, D]); otherwise the same arguments, semantics and checks
+ * as fa_fwd, fa_bwd_dkdv_workspace_bytes, fa_bwd_dkdv_ws and fa_bwd_dq_delta,
+ * with N_kv bounded like N. No counterpart in the reference kernels: the
+ * reference sends N_q != N_kv to torch SDPA (attention.py:639-642, 830-838),
+ * and these compute what that fallback does. Causal masking stays top-left,
+ * query i sees keys j <= i, SDPA's is_causal mask for unequal lengths (the
+ * lower triangle of the N_q x N_kv all-ones matrix); no row is fully masked.
+ * With N_q < N_kv, keys past the last query get dk = dv = 0 under the causal
+ * mask. fa_bwd_preprocess works on the query side and needs no twin. */
+int fa_fwd_kv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+              fa_half_t* o, float* lse,
+              int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+              float scale, int causal, void* stream);
+int fa_fwd_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   fa_half_t* o, float* lse,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                   float scale, int causal, void* stream);
+int64_t fa_bwd_dkdv_workspace_bytes_kv(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q,
+                                        int64_t N_kv, int64_t D, int causal);
+int fa_bwd_dkdv_ws_kv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                      const fa_half_t* dO, const float* lse, const float* delta,
+                      fa_half_t* dk, fa_half_t* dv,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                      float scale, int causal, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+int fa_bwd_dkdv_ws_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                           const fa_half_t* dO, const float* lse, const float* delta,
+                           fa_half_t* dk, fa_half_t* dv,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                           int64_t D, float scale, int causal, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+int fa_bwd_dq_delta_kv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                       const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                       float* delta, fa_half_t* dq,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                       float scale, int causal, void* stream);
+int fa_bwd_dq_delta_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                            const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                            float* delta, fa_half_t* dq,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                            int64_t D, float scale, int causal, void* stream);
 
 /* Thread-local description of the last failure on the calling thread
  * ("" if none). The pointer stays valid until the next call on the thread. */

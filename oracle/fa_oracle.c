@@ -10,19 +10,25 @@
  * Every function cites the reference lines it restates
  * (/root/reference/triton_flash_attention/attention.py, docs/architecture.md).
  * Inputs are the fp16 values of the tensors, widened exactly to double.
- * Layouts: q, o, dO, dq [B,Hq,N,D]; k, v, dk, dv [B,Hkv,N,D]; lse2, delta
- * [B,Hq,N]; all contiguous row-major.
+ * Layouts: q, o, dO, dq [B,Hq,N,D]; k, v, dk, dv [B,Hkv,Nkv,D]; lse2, delta
+ * [B,Hq,N]; all contiguous row-major. The reference kernels are
+ * self-attention (Nkv == N); the closed forms also take Nkv != N, the
+ * cross-attention the reference hands to torch SDPA (attention.py:639-642,
+ * 830-838), with SDPA's causal mask for unequal lengths: query i sees keys
+ * j <= i (the lower triangle of the N x Nkv all-ones matrix).
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
  *   oracle_round_half      numpy float16 conversion on 10^5 values incl. ties,
  *                          subnormals and overflow
- *   oracle_fwd_direct      torch fp64 SDPA and logsumexp; golden fixtures;
- *                          closed forms (causal row 0, Q=0 uniform attention,
- *                          constant V, N=1)
+ *   oracle_fwd_direct      torch fp64 SDPA and logsumexp (Nkv == N and
+ *                          Nkv != N); golden fixtures; closed forms (causal
+ *                          row 0, Q=0 uniform attention, constant V, N=1)
  *   oracle_fwd_online      oracle_fwd_direct (tiling independence at fp64),
  *                          and with round_p=1 the fp16-P rounding bound
  *   oracle_bwd_preprocess  exact dot products of small integers; golden Delta
- *   oracle_bwd             torch fp64 autograd through SDPA; golden fixtures;
+ *   oracle_bwd             torch fp64 autograd through SDPA (Nkv == N and
+ *                          Nkv != N, where keys past the last causal query
+ *                          get zero gradients); golden fixtures;
  *                          closed forms (constant V -> dQ = dK = 0, N=1);
  *                          GQA group sum == MHA with repeated K/V
  *   oracle_bwd, fold = 1/2 equal to fold = 0 when c32 is a power of two (the
@@ -74,24 +80,24 @@ static int64_t kv_head_of(int64_t b, int64_t hq, int64_t Hq, int64_t Hkv) {
 
 /* Closed form of the forward: per query row i,
  *   s_ij  = (q_i . k_j) * scale * log2(e)      (log2 domain, attention.py:61, 177)
- *   valid = j < N and (not causal or j <= i)   (attention.py:57, 63-66)
+ *   valid = j < Nkv and (not causal or j <= i) (attention.py:57, 63-66)
  *   lse2_i = log2(sum_valid exp2(s_ij))        (attention.py:230)
  *   o_i    = sum_valid exp2(s_ij - lse2_i) v_j (attention.py:231)
  * Two passes over the keys, no tiling, no intermediate rounding. */
 void oracle_fwd_direct(const double* q, const double* k, const double* v, int64_t B, int64_t Hq,
-                       int64_t Hkv, int64_t N, int64_t D, double scale, int causal, double* o,
-                       double* lse2) {
+                       int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, double scale, int causal,
+                       double* o, double* lse2) {
   const double c = scale * INV_LN2;
 #pragma omp parallel for schedule(dynamic)
   for (int64_t bh = 0; bh < B * Hq; ++bh) {
     const int64_t b = bh / Hq, hq = bh % Hq;
     const int64_t kvh = kv_head_of(b, hq, Hq, Hkv);
     const double* Q = q + bh * N * D;
-    const double* K = k + kvh * N * D;
-    const double* V = v + kvh * N * D;
-    double* s = (double*)malloc(sizeof(double) * (size_t)N);
+    const double* K = k + kvh * Nkv * D;
+    const double* V = v + kvh * Nkv * D;
+    double* s = (double*)malloc(sizeof(double) * (size_t)Nkv);
     for (int64_t i = 0; i < N; ++i) {
-      const int64_t last = causal ? i : N - 1;
+      const int64_t last = causal && i < Nkv - 1 ? i : Nkv - 1;
       double mx = -INFINITY;
       for (int64_t j = 0; j <= last; ++j) {
         s[j] = dot(Q + i * D, K + j * D, D) * c;
@@ -242,23 +248,23 @@ static void scaled_operand(const double* x, int64_t n, float c32, int fold, doub
  * head so each output row has one writer. */
 void oracle_bwd(const double* q, const double* k, const double* v, const double* dO,
                 const double* lse2, const double* delta, int64_t B, int64_t Hq, int64_t Hkv,
-                int64_t N, int64_t D, double scale, int causal, int fold, double* dq,
-                double* dk, double* dv) {
+                int64_t N, int64_t Nkv, int64_t D, double scale, int causal, int fold,
+                double* dq, double* dk, double* dv) {
   const double c = scale * INV_LN2;
   const float c32 = (float)scale * (float)INV_LN2;
   const int64_t group = Hq / Hkv;
 #pragma omp parallel for schedule(dynamic)
   for (int64_t bkv = 0; bkv < B * Hkv; ++bkv) {
     const int64_t b = bkv / Hkv, hkv = bkv % Hkv;
-    const double* K = k + bkv * N * D;
-    const double* V = v + bkv * N * D;
-    double* dK = dk + bkv * N * D;
-    double* dV = dv + bkv * N * D;
-    memset(dK, 0, sizeof(double) * (size_t)(N * D));
-    memset(dV, 0, sizeof(double) * (size_t)(N * D));
-    double* ks = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
+    const double* K = k + bkv * Nkv * D;
+    const double* V = v + bkv * Nkv * D;
+    double* dK = dk + bkv * Nkv * D;
+    double* dV = dv + bkv * Nkv * D;
+    memset(dK, 0, sizeof(double) * (size_t)(Nkv * D));
+    memset(dV, 0, sizeof(double) * (size_t)(Nkv * D));
+    double* ks = fold ? (double*)malloc(sizeof(double) * (size_t)(Nkv * D)) : NULL;
     double* qs = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
-    if (fold) scaled_operand(K, N * D, c32, fold, ks);
+    if (fold) scaled_operand(K, Nkv * D, c32, fold, ks);
     for (int64_t gi = 0; gi < group; ++gi) {
       const int64_t bh = b * Hq + hkv * group + gi;
       const double* Q = q + bh * N * D;
@@ -272,7 +278,7 @@ void oracle_bwd(const double* q, const double* k, const double* v, const double*
         for (int64_t d = 0; d < D; ++d) dqi[d] = 0.0;
         const double lse = lse2[bh * N + i];
         const double dlt = delta[bh * N + i];
-        const int64_t last = causal ? i : N - 1;
+        const int64_t last = causal && i < Nkv - 1 ? i : Nkv - 1;
         for (int64_t j = 0; j <= last; ++j) {
           /* p_k feeds dK and dV, p_q feeds dQ; equal unless fold */
           const double p_k = fold ? exp2(dot(qi, ks + j * D, D) - lse)

@@ -88,15 +88,21 @@ def test_explicit_torch_backend_honors_custom_scale() -> None:
 
 
 def test_cross_attention_fallback_matches_reference() -> None:
+    # The reference's cross-attention test inputs: value head size 16 != 32
+    # still sends them to SDPA, now by the value-head-size rule.
     query = torch.randn(1, 2, 3, 32)
     key = torch.randn(1, 2, 5, 32)
     value = torch.randn(1, 2, 5, 16)
     decision = explain_dispatch(query, key, value)
     assert decision.backend == "torch"
-    assert "self-attention" in decision.reason
+    assert "equal query/key and value head sizes" in decision.reason
     actual = scaled_dot_product_attention(query, key, value)
     expected = torch.nn.functional.scaled_dot_product_attention(query, key, value)
     torch.testing.assert_close(actual, expected)
+    # Equal head sizes on the CPU: the device rule, not the lengths, decides.
+    value = torch.randn(1, 2, 5, 32)
+    decision = explain_dispatch(query, key, value)
+    assert decision.backend == "torch" and "CUDA tensor" in decision.reason
 
 
 # --- remaining validation and argument checks (ref attention.py:584-626, 806-815)
@@ -155,18 +161,24 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
     # bfloat16 is served too (the reference sends it to SDPA, attention.py:653-656)
     d = attn._decide(_facts(dtype=torch.bfloat16))
     assert d.backend == "triton" and "bfloat16" in d.reason
+    # Cross-attention is served too (the reference sends it to SDPA, attention.py:639-642).
+    for q_len, kv_len in ((128, 64), (3, 5000)):
+        d = attn._decide(_facts(q_len=q_len, kv_len=kv_len))
+        assert d.backend == "triton" and "cross-attention" in d.reason
+    assert "self-attention" in attn._decide(_facts()).reason
 
 
 @pytest.mark.parametrize(
     ("overrides", "reason"),
     [
-        (dict(kv_len=64), "self-attention"),
         (dict(value_head_dim=32), "equal query/key and value head sizes"),
         (dict(device_type="cpu"), "requires a CUDA tensor"),
         (dict(dtype=torch.float32), "supports float16 and bfloat16"),
         (dict(dtype=torch.float64), "supports float16 and bfloat16"),
         (dict(head_dim=96, value_head_dim=96), "head_dim must be one of (32, 64, 128)"),
         (dict(q_len=1 << 24, kv_len=1 << 24), "too long"),
+        (dict(q_len=1 << 24), "too long"),
+        (dict(kv_len=1 << 24), "too long"),
         (dict(arch="gfx942:sramecc+:xnack-"), "gfx950"),
         (dict(arch=""), "gfx950"),
         (dict(library_error="missing"), "kernel library is not available"),
@@ -179,9 +191,9 @@ def test_rule_fallback_reasons(overrides, reason) -> None:
 
 
 def test_rule_order_is_first_match() -> None:
-    # cross-attention wins over everything, dtype wins over head_dim and arch
-    d = attn._decide(_facts(kv_len=3, dtype=torch.float32, arch="gfx90a"))
-    assert "self-attention" in d.reason
+    # value head size wins over everything, dtype wins over head_dim and arch
+    d = attn._decide(_facts(kv_len=3, value_head_dim=32, dtype=torch.float32, arch="gfx90a"))
+    assert "value head sizes" in d.reason
     d = attn._decide(_facts(dtype=torch.float32, head_dim=48, value_head_dim=48, arch="gfx90a"))
     assert "float16" in d.reason
 

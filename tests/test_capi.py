@@ -188,3 +188,40 @@ def test_dkdv_workspace_sizing_and_rejection(lib):
     rc = lib.fa_bwd_dkdv_ws(P, P, P, P, P, P, P, P, 1, 8, 2, 16381, 32, 0.17, 1, P, ws - 16, None)
     assert rc == _lib.FA_ERR_BAD_SHAPE
     assert "smaller than" in _lib.last_error()
+
+
+def test_cross_attention_entries_check_both_lengths(lib):
+    # fa_fwd_kv(q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale, causal, stream)
+    rc = lib.fa_fwd_kv(None, P, P, P, P, 1, 2, 2, 64, 80, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_NULL_POINTER and "fa_fwd_kv: null pointer" in _lib.last_error()
+    rc = lib.fa_fwd_kv_bf16(P, P, P, P, P, 1, 2, 2, 64, 0, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE and "N_kv must be positive" in _lib.last_error()
+    rc = lib.fa_fwd_kv(P, P, P, P, P, 1, 2, 2, 0, 80, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE
+    rc = lib.fa_fwd_kv(P, P, P, P, P, 1, 2, 2, 64, 1 << 24, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_TOO_LARGE and "key/value sequence length" in _lib.last_error()
+    rc = lib.fa_bwd_dq_delta_kv(P, P, P, P, P, P, P, P, 1, 4, 2, 64, 80, 96, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_HEAD_DIM
+    rc = lib.fa_bwd_dq_delta_kv_bf16(P, P, P, P, P, P, P, P, 1, 4, 2, 64, -3, 64, 0.125, 1, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE
+    rc = lib.fa_bwd_dkdv_ws_kv(P, P, P, P, P, P, P, P + 8, 1, 4, 2, 64, 80, 64, 0.125, 1,
+                               None, 0, None)
+    assert rc == _lib.FA_ERR_MISALIGNED
+    rc = lib.fa_bwd_dkdv_ws_kv_bf16(P, P, P, P, P, P, P, P, 1, 4, 2, 64, 80, 64, -1.0, 1,
+                                    None, 0, None)
+    assert rc == _lib.FA_ERR_BAD_SCALE
+
+
+def test_cross_attention_workspace_follows_the_key_length(lib):
+    for args in ((4, 16, 16, 4096, 64, 1), (1, 8, 2, 16381, 32, 1), (1, 8, 2, 700, 64, 0)):
+        B, Hq, Hkv, N, D, causal = args
+        assert lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, N, D, causal) == \
+            lib.fa_bwd_dkdv_workspace_bytes(*args)
+    # the split partials are [nsplit, 2, B, Hkv, N_kv, D] fp32: N_q does not enter
+    ws = lib.fa_bwd_dkdv_workspace_bytes_kv(1, 8, 2, 5000, 300, 64, 1)
+    plane = 1 * 2 * 300 * 64 * 4
+    assert ws > 0 and ws % (2 * plane) == 0 and ws // (2 * plane) <= 8
+    assert lib.fa_bwd_dkdv_workspace_bytes_kv(1, 8, 2, 300, 300, 64, 1) == ws
+    rc = lib.fa_bwd_dkdv_ws_kv(P, P, P, P, P, P, P, P, 1, 8, 2, 5000, 300, 64, 0.125, 1,
+                               P, ws - 16, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()

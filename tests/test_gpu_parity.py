@@ -450,3 +450,106 @@ def test_bf16_full_c2_matches_fp32_reference():
                               max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL)
         _note(f"  bf16 c2 {tname}: max-abs {ma:.3e} rel-L2 {rl:.3e}")
     assert float((lse - ref["lse"]).abs().max()) <= LSE_TOL
+
+
+# ---------------------------------------------------------------------------
+# Cross-attention (N_q != N_kv): the reference sends it to torch SDPA
+# (attention.py:639-642); the kernels compute that fallback's result, with
+# SDPA's top-left causal mask, checked against the oracle's closed form (pinned
+# to torch fp64 SDPA for unequal lengths on the CPU).
+# ---------------------------------------------------------------------------
+CROSS_CASES = [
+    # (B, Hq, Hkv, N_q, N_kv): fewer queries than keys (GQA, split dK/dV),
+    # more queries than keys, one query, one key
+    (1, 4, 2, 300, 700),
+    (2, 4, 4, 777, 129),
+    (1, 2, 1, 1, 513),
+    (1, 2, 2, 1000, 1),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("case", CROSS_CASES, ids=lambda c: f"B{c[0]}H{c[1]}-{c[2]}Nq{c[3]}Nkv{c[4]}")
+def test_cross_attention_matches_oracle(case, head_dim, causal):
+    B, Hq, Hkv, N, Nkv = case
+    tag = f"cross B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={head_dim} causal={causal}"
+    _note(tag)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, head_dim, seed=N + Nkv + head_dim, mult=0.5,
+                              n_kv=Nkv)
+    assert explain_dispatch(q.to(DEV), k.to(DEV), v.to(DEV),
+                            enable_gqa=Hq != Hkv).backend == "triton"
+    got = run_kernel(q, k, v, do, causal)
+    assert got["dk"].shape == (B, Hkv, Nkv, head_dim)
+    check_against_oracle(got, q, k, v, do, causal, tag=tag)
+    if causal and N < Nkv:
+        # keys past the last query are never seen: exactly zero gradients
+        assert not got["dk"][:, :, N:].any() and not got["dv"][:, :, N:].any()
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_cross_attention_every_tiling_variant(head_dim, causal):
+    """Each compiled tiling of each kernel with N_q != N_kv in both directions:
+    forward, dK/dV split and single pass, dQ with Delta."""
+    scale = head_dim ** -0.5
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    for B, Hq, Hkv, N, Nkv in ((1, 4, 2, 200, 450), (1, 4, 2, 450, 200)):
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, head_dim, seed=5 * N + Nkv, mult=0.5, n_kv=Nkv)
+        qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+        o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
+        delta = _ops.flash_bwd_preprocess(o, dod)
+        torch.cuda.synchronize()
+        ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
+                               o16=o.cpu().numpy(), fold_bwd=True)
+
+        def close(tag, got, name):
+            assert_close(tag, torch.as_tensor(got).double().cpu().numpy(), ref[name])
+
+        kinds = ((_lib.KERNEL_FWD, "fwd"), (_lib.KERNEL_DKDV, "dkdv"), (_lib.KERNEL_DQ, "dq"))
+        for kind, kname in kinds:
+            for var in _lib.tiling_variants(kind, head_dim, causal):
+                tag = f"cross N_q={N} N_kv={Nkv} D={head_dim} causal={causal} {kname} " \
+                      f"variant {var['variant']} ({var['waves']} waves, tile {var['tile']})"
+                _note(tag)
+                _lib.set_tiling(kind, head_dim, causal, var["variant"])
+                try:
+                    if kind == _lib.KERNEL_FWD:
+                        o2, lse2 = _ops.flash_fwd(qd, kd, vd, causal, scale)
+                        torch.cuda.synchronize()
+                        close(tag + " o", o2, "o")
+                        lse_err = float(np.max(np.abs(lse2.double().cpu().numpy() - ref["lse"])))
+                        assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"
+                    elif kind == _lib.KERNEL_DKDV:
+                        dk1, dv1 = _ops.flash_bwd_dkdv(qd, kd, vd, dod, lse, delta, causal, scale)
+                        dk2, dv2 = torch.empty_like(kd), torch.empty_like(vd)
+                        _lib.check(lib.fa_bwd_dkdv_ws_kv(
+                            qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), dod.data_ptr(),
+                            lse.data_ptr(), delta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
+                            B, Hq, Hkv, N, Nkv, head_dim, scale, int(causal), None, 0, stream))
+                        torch.cuda.synchronize()
+                        close(tag + " dk (split)", dk1, "dk")
+                        close(tag + " dv (split)", dv1, "dv")
+                        close(tag + " dk", dk2, "dk")
+                        close(tag + " dv", dv2, "dv")
+                    else:
+                        delta2, dq = _ops.flash_bwd_dq_delta(qd, kd, vd, o, dod, lse, causal, scale)
+                        torch.cuda.synchronize()
+                        torch.testing.assert_close(delta2, delta, rtol=1e-5, atol=1e-5, msg=tag)
+                        close(tag + " dq", dq, "dq")
+                finally:
+                    _lib.set_tiling(kind, head_dim, causal, -1)
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_bf16_cross_attention_matches_oracle(head_dim):
+    for B, Hq, Hkv, N, Nkv in ((1, 6, 3, 300, 611), (2, 4, 2, 333, 97)):
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, head_dim, seed=N * Nkv, dtype=torch.bfloat16,
+                                  n_kv=Nkv)
+        for causal in (False, True):
+            got = run_kernel(q, k, v, do, causal)
+            assert got["o16"].dtype == torch.bfloat16
+            check_bf16_against_oracle(
+                got, q, k, v, do, causal,
+                tag=f"bf16 cross N_q={N} N_kv={Nkv} D={head_dim} causal={causal}")

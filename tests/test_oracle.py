@@ -26,17 +26,19 @@ from oracle import oracle
 GOLDEN = Path(__file__).resolve().parent / "golden" / "attention_fp64.npz"
 
 
-def _inputs(B, Hq, Hkv, N, D, seed, mult=1.0):
+def _inputs(B, Hq, Hkv, N, D, seed, mult=1.0, n_kv=None):
     g = torch.Generator("cpu").manual_seed(seed)
+    n_kv = N if n_kv is None else n_kv
     q = (torch.randn((B, Hq, N, D), generator=g) * mult).half()
-    k = (torch.randn((B, Hkv, N, D), generator=g) * mult).half()
-    v = (torch.randn((B, Hkv, N, D), generator=g) * mult).half()
+    k = (torch.randn((B, Hkv, n_kv, D), generator=g) * mult).half()
+    v = (torch.randn((B, Hkv, n_kv, D), generator=g) * mult).half()
     do = (torch.randn((B, Hq, N, D), generator=g) * mult).half()
     return q, k, v, do
 
 
 def _torch_fp64(q, k, v, do, causal, scale=None):
     Hq, Hkv, N, D = q.shape[1], k.shape[1], q.shape[2], q.shape[3]
+    Nkv = k.shape[2]
     q64, k64, v64 = (t.double().requires_grad_() for t in (q, k, v))
     o = torch.nn.functional.scaled_dot_product_attention(
         q64, k64, v64, is_causal=causal, scale=scale, enable_gqa=Hq != Hkv)
@@ -45,7 +47,8 @@ def _torch_fp64(q, k, v, do, causal, scale=None):
     with torch.no_grad():
         s = q64 @ k64.repeat_interleave(Hq // Hkv, 1).transpose(-1, -2) * sc
         if causal:
-            s = s.masked_fill(torch.ones(N, N, dtype=torch.bool).triu(1), -math.inf)
+            # top-left: query i sees keys j <= i (SDPA's mask for N != Nkv too)
+            s = s.masked_fill(torch.ones(N, Nkv, dtype=torch.bool).triu(1), -math.inf)
         lse2 = torch.logsumexp(s, -1) / math.log(2.0)
     exact_delta = (o.detach() * do.double()).sum(-1)
     return {"o": o.detach().numpy(), "lse": lse2.numpy(), "dq": dq.numpy(),
@@ -183,6 +186,56 @@ def test_backward_closed_forms():
                          o16=vn[:, :, :1])
     assert np.max(np.abs(r["dq"])) < 1e-15 and np.max(np.abs(r["dk"])) < 1e-15
     np.testing.assert_allclose(r["dv"], don[:, :, :1].astype(np.float64), atol=1e-15)
+
+
+# ---------------------------------------------------------------------------
+# Cross-attention (Nkv != N): the reference's SDPA fallback, attention.py:639-642
+# ---------------------------------------------------------------------------
+CROSS_SHAPES = [(1, 2, 2, 17, 40, 32), (2, 4, 2, 65, 23, 64), (1, 3, 1, 1, 50, 128),
+                (1, 2, 1, 50, 1, 64), (1, 4, 4, 33, 97, 32)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", CROSS_SHAPES)
+def test_cross_attention_matches_torch_fp64(shape, causal):
+    B, Hq, Hkv, N, Nkv, D = shape
+    q, k, v, do = _inputs(B, Hq, Hkv, N, D, seed=N + 3 * Nkv + D, n_kv=Nkv)
+    ref = _torch_fp64(q, k, v, do, causal)
+    o, lse = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    assert o.shape == (B, Hq, N, D) and lse.shape == (B, Hq, N)
+    assert _maxdiff(o, ref["o"]) < 1e-12
+    assert _maxdiff(lse, ref["lse"]) < 1e-12
+    dq, dk, dv = oracle.bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), lse, ref["delta"], causal)
+    assert dk.shape == (B, Hkv, Nkv, D)
+    assert _maxdiff(dq, ref["dq"]) < 1e-12
+    assert _maxdiff(dk, ref["dk"]) < 1e-12
+    assert _maxdiff(dv, ref["dv"]) < 1e-12
+
+
+def test_cross_attention_causal_closed_forms():
+    """Top-left causal with unequal lengths reduces to self-attention pieces:
+    N < Nkv never looks past key N-1 (keys beyond get zero gradients);
+    N > Nkv gives rows i >= Nkv the bidirectional result over all keys. A
+    bottom-right mask (the other convention for unequal lengths) fails both."""
+    q, k, v, do = _inputs(1, 2, 2, 40, 64, seed=12, n_kv=100)
+    qn, kn, vn, don = q.numpy(), k.numpy(), v.numpy(), do.numpy()
+    cross = oracle.attention(qn, kn, vn, don, True)
+    self_ = oracle.attention(qn, kn[:, :, :40], vn[:, :, :40], don, True)
+    for name in ("o", "lse", "dq"):
+        assert _maxdiff(cross[name], self_[name]) < 1e-12
+    assert _maxdiff(cross["dk"][:, :, :40], self_["dk"]) < 1e-12
+    assert np.all(cross["dk"][:, :, 40:] == 0) and np.all(cross["dv"][:, :, 40:] == 0)
+    # bottom-right alignment would let query 0 see keys 0..60: a different O
+    shifted = oracle.fwd(qn[:, :, :1], kn[:, :, :61], vn[:, :, :61], False)[0]
+    assert _maxdiff(cross["o"][:, :, :1], shifted) > 1e-3
+
+    q, k, v, do = _inputs(1, 2, 1, 90, 32, seed=13, n_kv=30)
+    qn, kn, vn, don = q.numpy(), k.numpy(), v.numpy(), do.numpy()
+    o, lse = oracle.fwd(qn, kn, vn, True)
+    o_top, lse_top = oracle.fwd(qn[:, :, :30], kn, vn, True)
+    o_all, lse_all = oracle.fwd(qn[:, :, 30:], kn, vn, False)
+    assert _maxdiff(o[:, :, :30], o_top) < 1e-12 and _maxdiff(lse[:, :, :30], lse_top) < 1e-12
+    assert _maxdiff(o[:, :, 30:], o_all) < 1e-12 and _maxdiff(lse[:, :, 30:], lse_all) < 1e-12
 
 
 def test_gqa_group_sum_identity():

@@ -191,11 +191,13 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const int b = kvh / a.Hkv;
   const int hkv = kvh - b * a.Hkv;
   const int G = a.group;
-  const int N = a.N;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
   const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
   const uint32_t aux_bytes = (uint32_t)N * 4u;
-  const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * N * D, slab);
-  const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * N * D, slab);
+  const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
   const int k0 = kvtile * T::BKV;
   const int k0w = k0 + 32 * wave;
@@ -220,7 +222,9 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   }
 
   const int q_begin = CAUSAL ? (k0 / QT) * QT : 0;
-  const int ntq = (N - q_begin + QT - 1) / QT;
+  // Under the causal mask a key tile past the last query (N < Nkv) sees no
+  // query; it still takes one (empty) step, so its dK = dV = 0 are written.
+  const int ntq = max(1, (N - q_begin + QT - 1) / QT);
   // This work-group's chunk [s_lo, s_lo + nsteps) of the tile's G * ntq steps.
   const int total_steps = G * ntq;
   const int chunk = (total_steps + a.nsplit - 1) / a.nsplit;
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
       dv[db][j] = 0.f;
     }
 
-  const bool wave_live = k0w < N;
+  const bool wave_live = k0w < Nkv;
 
   auto step = [&](auto slot_c, int u) {
     constexpr int SLOT = decltype(slot_c)::value;
@@ -391,10 +395,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
   const float scale = a.scale;
   if (a.nsplit > 1) {
     // fp32 partials (dK already scaled); an empty chunk writes zeros.
-    const int64_t plane = (int64_t)a.BHkv * N * D;
-    float* pk = a.part + (int64_t)split * 2 * plane + (int64_t)kvh * N * D;
+    const int64_t plane = (int64_t)a.BHkv * Nkv * D;
+    float* pk = a.part + (int64_t)split * 2 * plane + (int64_t)kvh * Nkv * D;
     float* pv = pk + plane;
-    if (krow < N) {
+    if (krow < Nkv) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -412,8 +416,8 @@ __global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
     }
     return;
   }
-  const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * N * D, slab);
-  const rsrc_t rdv = make_rsrc(a.dv + (int64_t)kvh * N * D, slab);
+  const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * Nkv * D, kv_slab);
+  const rsrc_t rdv = make_rsrc(a.dv + (int64_t)kvh * Nkv * D, kv_slab);
 #pragma unroll
   for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -432,7 +436,7 @@ template <int D, bool CAUSAL, int NW, int QT, class E = F16>
 hipError_t dkdv_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DkdvTile<D, NW, QT>;
   BwdArgs b = a;
-  b.num_tiles = (a.N + T::BKV - 1) / T::BKV;
+  b.num_tiles = (a.Nkv + T::BKV - 1) / T::BKV;
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -526,11 +530,13 @@ void dkdv_pipe_kernel(BwdArgs a) {
   const int b = kvh / a.Hkv;
   const int hkv = kvh - b * a.Hkv;
   const int G = a.group;
-  const int N = a.N;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
   const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
   const uint32_t aux_bytes = (uint32_t)N * 4u;
-  const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * N * D, slab);
-  const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * N * D, slab);
+  const rsrc_t rk = make_rsrc(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const rsrc_t rv = make_rsrc(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
   const int k0 = th.tile_rank * T::BKV;
   const int k0w = k0 + 32 * wave;
@@ -558,7 +564,10 @@ void dkdv_pipe_kernel(BwdArgs a) {
   for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(kf[kk]), "+v"(vn[kk]));
 
   const int q_begin = CAUSAL ? k0 : 0;  // k0 is a multiple of 32
-  const int ntq = (N - q_begin + T::QT - 1) / T::QT;
+  // Under the causal mask a key tile past the last query (N < Nkv) sees no
+  // query; it still takes one unit (all rows read as zeros), so its
+  // dK = dV = 0 are written.
+  const int ntq = max(1, (N - q_begin + T::QT - 1) / T::QT);
   const int total_units = G * ntq;
   const int chunk = (total_units + a.nsplit - 1) / a.nsplit;
   const int u_lo = min(split * chunk, total_units);
@@ -894,10 +903,10 @@ void dkdv_pipe_kernel(BwdArgs a) {
 
   const float nscale = -a.scale;  // dK accumulated -dS
   if (a.nsplit > 1) {
-    const int64_t plane = (int64_t)a.BHkv * N * D;
-    float* pk = a.part + (int64_t)split * 2 * plane + (int64_t)kvh * N * D;
+    const int64_t plane = (int64_t)a.BHkv * Nkv * D;
+    float* pk = a.part + (int64_t)split * 2 * plane + (int64_t)kvh * Nkv * D;
     float* pv = pk + plane;
-    if (krow < N) {
+    if (krow < Nkv) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -915,8 +924,8 @@ void dkdv_pipe_kernel(BwdArgs a) {
     }
     return;
   }
-  const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * N * D, slab);
-  const rsrc_t rdv = make_rsrc(a.dv + (int64_t)kvh * N * D, slab);
+  const rsrc_t rdk = make_rsrc(a.dk + (int64_t)kvh * Nkv * D, kv_slab);
+  const rsrc_t rdv = make_rsrc(a.dv + (int64_t)kvh * Nkv * D, kv_slab);
 #pragma unroll
   for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -935,7 +944,7 @@ template <int D, bool CAUSAL, int NW, class E = F16>
 hipError_t dkdv_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DkdvPipeTile<D, NW>;
   BwdArgs b = a;
-  b.num_tiles = (a.N + T::BKV - 1) / T::BKV;
+  b.num_tiles = (a.Nkv + T::BKV - 1) / T::BKV;
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -991,15 +1000,17 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
-  const int N = a.N;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
   const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
   const uint32_t aux = (uint32_t)N * 4u;
   const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
   const rsrc_t rdo = make_rsrc(a.dO + (int64_t)head * N * D, slab);
   const rsrc_t rl = make_rsrc(a.lse + (int64_t)head * N, aux);
   const rsrc_t rd = make_rsrc(a.delta + (int64_t)head * N, aux);
-  const int4v rk = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
-  const int4v rv = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
+  const int4v rk = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const int4v rv = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
   const int q0 = qtile * T::BQ;
   const int q0w = q0 + 32 * wave;
@@ -1023,7 +1034,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
     asm volatile("" : "+v"(qf[kk]));
   }
 
-  const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
+  const int kv_end = CAUSAL ? min(Nkv, q0 + T::BQ) : Nkv;
   const int ntiles = (kv_end + KT - 1) / KT;
 
   Dma dma;
@@ -1086,7 +1097,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int kb = 0; kb < NB; ++kb) {
       const int ka = kt0 + 32 * kb;
-      act[kb] = q0w < N && ka < N && !(CAUSAL && ka > q0w + 31);
+      act[kb] = q0w < N && ka < Nkv && !(CAUSAL && ka > q0w + 31);
       if (act[kb]) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -1110,14 +1121,14 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) kt_f[h][db] = tr8(Ks + (32 * kb + 16 * h) * D, db);
-      const bool need_mask = (CAUSAL && ka + 31 > q0w) || (ka + 32 > N);
+      const bool need_mask = (CAUSAL && ka + 31 > q0w) || (ka + 32 > Nkv);
       half8 sa[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float pj = exp2_fast(s[kb][j] + nl);
         if (need_mask) {
           const int key = ka + result_row(j, g);
-          if (key >= N || (CAUSAL && key > qrow)) pj = 0.f;
+          if (key >= Nkv || (CAUSAL && key > qrow)) pj = 0.f;
         }
         sa[j >> 3][j & 7] = to_elem<E>(pj * (dp[kb][j] - delta));
       }
@@ -1231,15 +1242,17 @@ void dq_pipe_kernel(BwdArgs a) {
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
-  const int N = a.N;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
   const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
   const uint32_t aux = (uint32_t)N * 4u;
   const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
   const rsrc_t rdo = make_rsrc(a.dO + (int64_t)head * N * D, slab);
   const rsrc_t rl = make_rsrc(a.lse + (int64_t)head * N, aux);
   const rsrc_t rd = make_rsrc(a.delta + (int64_t)head * N, aux);
-  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
-  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
+  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
   const int q0 = qtile * T::BQ;
   const int q0w = q0 + 32 * wave;
@@ -1281,7 +1294,7 @@ void dq_pipe_kernel(BwdArgs a) {
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[kk]), "+v"(don[kk]));
 
-  const int kv_end = CAUSAL ? min(N, q0 + T::BQ) : N;
+  const int kv_end = CAUSAL ? min(Nkv, q0 + T::BQ) : Nkv;
   const int nunits = (kv_end + T::KT - 1) / T::KT;
   const int npad = (nunits + NS - 1) / NS * NS;
 
@@ -1290,7 +1303,7 @@ void dq_pipe_kernel(BwdArgs a) {
   const uint32_t lds0 = lds_addr(lds);
   int i_row = 0;  // first key row of the next unit to fetch
   auto issue = [&](int slot) {
-    const int row0 = i_row < kv_end ? i_row : N;  // past the end: zeros
+    const int row0 = i_row < kv_end ? i_row : Nkv;  // past the end: zeros
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;

@@ -119,6 +119,15 @@ int check_common(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D) {
   return FA_OK;
 }
 
+// The key/value length of the *_kv entry points (the same bounds as N).
+int check_kv_length(int64_t Nkv, int64_t D) {
+  if (Nkv <= 0) return fail(FA_ERR_BAD_SHAPE, "N_kv must be positive (got %lld)", (long long)Nkv);
+  if (Nkv * D * 2 + 4096 * D * 2 >= ((int64_t)1 << 31))
+    return fail(FA_ERR_TOO_LARGE, "key/value sequence length %lld is too large for head_dim %lld",
+                (long long)Nkv, (long long)D);
+  return FA_OK;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_aligned(const char* fn, std::initializer_list<const void*> ptrs) {
@@ -136,7 +145,7 @@ int check_scale(float scale) {
 
 fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                      const fa_half_t* dO, const float* lse, const float* delta, int64_t B,
-                     int64_t Hq, int64_t Hkv, int64_t N, float scale) {
+                     int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv, float scale) {
   fa::BwdArgs a;
   a.q = reinterpret_cast<const fa::half_t*>(q);
   a.k = reinterpret_cast<const fa::half_t*>(k);
@@ -148,6 +157,7 @@ fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
   a.dk = nullptr;
   a.dv = nullptr;
   a.N = (int)N;
+  a.Nkv = (int)Nkv;
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
   a.group = (int)(Hq / Hkv);
@@ -169,8 +179,8 @@ fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
 constexpr int64_t kSplitTargetWorkgroups = 768;
 constexpr int kMaxSplit = 8;
 
-int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hkv, int64_t N) {
-  const int64_t tiles = (N + var.rows - 1) / var.rows;
+int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hkv, int64_t Nkv) {
+  const int64_t tiles = (Nkv + var.rows - 1) / var.rows;
   const int64_t wgs = tiles * B * Hkv;
   if (wgs >= kSplitTargetWorkgroups) return 1;
   int64_t s = (kSplitTargetWorkgroups + wgs - 1) / wgs;
@@ -178,8 +188,8 @@ int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hkv, int64_t N) {
   return (int)s;
 }
 
-int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  return nsplit > 1 ? (int64_t)nsplit * 2 * B * Hkv * N * D * 4 : 0;
+int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D) {
+  return nsplit > 1 ? (int64_t)nsplit * 2 * B * Hkv * Nkv * D * 4 : 0;
 }
 
 }  // namespace
@@ -192,10 +202,11 @@ const char* fa_last_error(void) { return g_last_error; }
 
 static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
                     const fa_half_t* v, fa_half_t* o, float* lse, int64_t B, int64_t Hq,
-                    int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
+                    int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal, void* stream) {
   if (!q || !k || !v || !o || !lse) return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, lse}))) return rc;
   if ((rc = check_scale(scale))) return rc;
   const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
@@ -207,6 +218,7 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   a.o = reinterpret_cast<fa::half_t*>(o);
   a.lse = lse;
   a.N = (int)N;
+  a.Nkv = (int)Nkv;
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
   a.group = (int)(Hq / Hkv);
@@ -233,49 +245,57 @@ static int preprocess_impl(int dt, const char* name, const fa_half_t* o, const f
 static int dkdv_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
                      const fa_half_t* v, const fa_half_t* dO, const float* lse,
                      const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq,
-                     int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
+                     int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal, void* stream) {
   if (!q || !k || !v || !dO || !lse || !delta || !dk || !dv)
     return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
   const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
   a.dv = reinterpret_cast<fa::half_t*>(dv);
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   return launch_result(fn(a, static_cast<hipStream_t>(stream)), name);
 }
 
-int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
-                                     int causal) {
+static int64_t dkdv_workspace_impl(const char* name, int64_t B, int64_t Hq, int64_t Hkv,
+                                   int64_t N, int64_t Nkv, int64_t D, int causal) {
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
   const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dkdv_workspace_bytes: no kernel for the selected tiling");
-  return split_workspace_bytes(dkdv_split(*var, B, Hkv, N), B, Hkv, N, D);
+  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
+  return split_workspace_bytes(dkdv_split(*var, B, Hkv, Nkv), B, Hkv, Nkv, D);
+}
+
+int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                     int causal) {
+  return dkdv_workspace_impl("fa_bwd_dkdv_workspace_bytes", B, Hq, Hkv, N, N, D, causal);
 }
 
 static int dkdv_ws_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
                         const fa_half_t* v, const fa_half_t* dO, const float* lse,
                         const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq,
-                        int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+                        int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
                         void* workspace, int64_t workspace_bytes, void* stream) {
   if (!q || !k || !v || !dO || !lse || !delta || !dk || !dv)
     return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
   const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
   a.dv = reinterpret_cast<fa::half_t*>(dv);
-  const int nsplit = dkdv_split(*var, B, Hkv, N);
-  const int64_t need = split_workspace_bytes(nsplit, B, Hkv, N, D);
+  const int nsplit = dkdv_split(*var, B, Hkv, Nkv);
+  const int64_t need = split_workspace_bytes(nsplit, B, Hkv, Nkv, D);
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   if (need == 0 || workspace == nullptr || workspace_bytes < need) {
@@ -290,23 +310,24 @@ static int dkdv_ws_impl(int dt, const char* name, const fa_half_t* q, const fa_h
   a.part = static_cast<float*>(workspace);
   hipError_t e = fn(a, s);
   if (e != hipSuccess) return launch_result(e, name);
-  return launch_result(fa::launch_split_reduce(a.part, a.dk, a.dv, B * Hkv * N * D, nsplit, dt, s),
+  return launch_result(fa::launch_split_reduce(a.part, a.dk, a.dv, B * Hkv * Nkv * D, nsplit, dt, s),
                     name);
 }
 
 static int dq_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
                    const fa_half_t* v, const fa_half_t* dO, const float* lse, const float* delta,
-                   fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                   fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv, int64_t D,
                    float scale, int causal, void* stream) {
   if (!q || !k || !v || !dO || !lse || !delta || !dq)
     return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
   const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   return launch_result(fn(a, static_cast<hipStream_t>(stream)), name);
@@ -315,18 +336,19 @@ static int dq_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t
 static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
                          const fa_half_t* v, const fa_half_t* o, const fa_half_t* dO,
                          const float* lse, float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
-                         int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
+                         int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
                          void* stream) {
   if (!q || !k || !v || !o || !dO || !lse || !delta || !dq)
     return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
   const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, scale);
+  fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
   if (var->flags & fa::kFusesDelta) {
     a.o = reinterpret_cast<const fa::half_t*>(o);
@@ -345,12 +367,13 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
 int fa_fwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o, float* lse,
            int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
            void* stream) {
-  return fwd_impl(fa::kF16, "fa_fwd", q, k, v, o, lse, B, Hq, Hkv, N, D, scale, causal, stream);
+  return fwd_impl(fa::kF16, "fa_fwd", q, k, v, o, lse, B, Hq, Hkv, N, N, D, scale, causal,
+                  stream);
 }
 int fa_fwd_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
                 float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale,
                 int causal, void* stream) {
-  return fwd_impl(fa::kBF16, "fa_fwd_bf16", q, k, v, o, lse, B, Hq, Hkv, N, D, scale, causal,
+  return fwd_impl(fa::kBF16, "fa_fwd_bf16", q, k, v, o, lse, B, Hq, Hkv, N, N, D, scale, causal,
                   stream);
 }
 int fa_bwd_preprocess(const fa_half_t* o, const fa_half_t* dO, float* delta, int64_t B,
@@ -365,7 +388,7 @@ int fa_bwd_dkdv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, cons
                 const float* lse, const float* delta, fa_half_t* dk, fa_half_t* dv, int64_t B,
                 int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale, int causal,
                 void* stream) {
-  return dkdv_impl(fa::kF16, "fa_bwd_dkdv", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv, N, D,
+  return dkdv_impl(fa::kF16, "fa_bwd_dkdv", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv, N, N, D,
                    scale, causal, stream);
 }
 int fa_bwd_dkdv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
@@ -373,7 +396,7 @@ int fa_bwd_dkdv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                      fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                      float scale, int causal, void* stream) {
   return dkdv_impl(fa::kBF16, "fa_bwd_dkdv_bf16", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv,
-                   N, D, scale, causal, stream);
+                   N, N, D, scale, causal, stream);
 }
 int fa_bwd_dkdv_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                    const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dk,
@@ -381,7 +404,7 @@ int fa_bwd_dkdv_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                    float scale, int causal, void* workspace, int64_t workspace_bytes,
                    void* stream) {
   return dkdv_ws_impl(fa::kF16, "fa_bwd_dkdv_ws", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv,
-                      N, D, scale, causal, workspace, workspace_bytes, stream);
+                      N, N, D, scale, causal, workspace, workspace_bytes, stream);
 }
 int fa_bwd_dkdv_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                         const fa_half_t* dO, const float* lse, const float* delta,
@@ -389,19 +412,19 @@ int fa_bwd_dkdv_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t*
                         int64_t N, int64_t D, float scale, int causal, void* workspace,
                         int64_t workspace_bytes, void* stream) {
   return dkdv_ws_impl(fa::kBF16, "fa_bwd_dkdv_ws_bf16", q, k, v, dO, lse, delta, dk, dv, B, Hq,
-                      Hkv, N, D, scale, causal, workspace, workspace_bytes, stream);
+                      Hkv, N, N, D, scale, causal, workspace, workspace_bytes, stream);
 }
 int fa_bwd_dq(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* dO,
               const float* lse, const float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
               int64_t Hkv, int64_t N, int64_t D, float scale, int causal, void* stream) {
-  return dq_impl(fa::kF16, "fa_bwd_dq", q, k, v, dO, lse, delta, dq, B, Hq, Hkv, N, D, scale,
+  return dq_impl(fa::kF16, "fa_bwd_dq", q, k, v, dO, lse, delta, dq, B, Hq, Hkv, N, N, D, scale,
                  causal, stream);
 }
 int fa_bwd_dq_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                    const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dq,
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, float scale,
                    int causal, void* stream) {
-  return dq_impl(fa::kBF16, "fa_bwd_dq_bf16", q, k, v, dO, lse, delta, dq, B, Hq, Hkv, N, D,
+  return dq_impl(fa::kBF16, "fa_bwd_dq_bf16", q, k, v, dO, lse, delta, dq, B, Hq, Hkv, N, N, D,
                  scale, causal, stream);
 }
 int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
@@ -409,14 +432,63 @@ int fa_bwd_dq_delta(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                     fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                     float scale, int causal, void* stream) {
   return dq_delta_impl(fa::kF16, "fa_bwd_dq_delta", q, k, v, o, dO, lse, delta, dq, B, Hq, Hkv,
-                       N, D, scale, causal, stream);
+                       N, N, D, scale, causal, stream);
 }
 int fa_bwd_dq_delta_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                          const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
                          fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                          float scale, int causal, void* stream) {
   return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_bf16", q, k, v, o, dO, lse, delta, dq, B, Hq,
-                       Hkv, N, D, scale, causal, stream);
+                       Hkv, N, N, D, scale, causal, stream);
+}
+
+// ---- exported launches with separate query and key/value lengths --------
+int fa_fwd_kv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
+              float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+              int64_t D, float scale, int causal, void* stream) {
+  return fwd_impl(fa::kF16, "fa_fwd_kv", q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale, causal,
+                  stream);
+}
+int fa_fwd_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
+                   float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                   int64_t D, float scale, int causal, void* stream) {
+  return fwd_impl(fa::kBF16, "fa_fwd_kv_bf16", q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale,
+                  causal, stream);
+}
+int64_t fa_bwd_dkdv_workspace_bytes_kv(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q,
+                                        int64_t N_kv, int64_t D, int causal) {
+  return dkdv_workspace_impl("fa_bwd_dkdv_workspace_bytes_kv", B, Hq, Hkv, N_q, N_kv, D, causal);
+}
+int fa_bwd_dkdv_ws_kv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                      const fa_half_t* dO, const float* lse, const float* delta, fa_half_t* dk,
+                      fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q,
+                      int64_t N_kv, int64_t D, float scale, int causal, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  return dkdv_ws_impl(fa::kF16, "fa_bwd_dkdv_ws_kv", q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv,
+                      N_q, N_kv, D, scale, causal, workspace, workspace_bytes, stream);
+}
+int fa_bwd_dkdv_ws_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                           const fa_half_t* dO, const float* lse, const float* delta,
+                           fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv,
+                           int64_t N_q, int64_t N_kv, int64_t D, float scale, int causal,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  return dkdv_ws_impl(fa::kBF16, "fa_bwd_dkdv_ws_kv_bf16", q, k, v, dO, lse, delta, dk, dv, B, Hq,
+                      Hkv, N_q, N_kv, D, scale, causal, workspace, workspace_bytes, stream);
+}
+int fa_bwd_dq_delta_kv(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                       const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
+                       fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q,
+                       int64_t N_kv, int64_t D, float scale, int causal, void* stream) {
+  return dq_delta_impl(fa::kF16, "fa_bwd_dq_delta_kv", q, k, v, o, dO, lse, delta, dq, B, Hq, Hkv,
+                       N_q, N_kv, D, scale, causal, stream);
+}
+int fa_bwd_dq_delta_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                            const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                            float* delta, fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv,
+                            int64_t N_q, int64_t N_kv, int64_t D, float scale, int causal,
+                            void* stream) {
+  return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_kv_bf16", q, k, v, o, dO, lse, delta, dq, B,
+                       Hq, Hkv, N_q, N_kv, D, scale, causal, stream);
 }
 
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4) {

@@ -77,18 +77,20 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
-  const int N = a.N;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
   const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
   const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
   const rsrc_t ro = make_rsrc(a.o + (int64_t)head * N * D, slab);
-  const int4v rk = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
-  const int4v rv = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
+  const int4v rk = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const int4v rv = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
   const int q0 = qtile * T::BM;
   const int q0w = q0 + 32 * wave;
   const int qrow = q0w + ql;
 
-  const int kv_end = CAUSAL ? min(N, q0 + T::BM) : N;
+  const int kv_end = CAUSAL ? min(Nkv, q0 + T::BM) : Nkv;
   const int ntiles = (kv_end + BN - 1) / BN;
 
   // Q^T operand fragments: lane (query ql, k-half g), d = 16*kk + 8*g .. +7.
@@ -203,14 +205,14 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
     if (act) {
       float16v* sc = sbuf[SB];
-      const bool need_mask = uniform((CAUSAL && kv0 + BN - 1 > q0w) || (kv0 + BN > N)) != 0;
+      const bool need_mask = uniform((CAUSAL && kv0 + BN - 1 > q0w) || (kv0 + BN > Nkv)) != 0;
       if (need_mask) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int key = kv0 + 32 * kb + result_row(j, g);
-            const bool ok = key < N && (!CAUSAL || key <= qrow);
+            const bool ok = key < Nkv && (!CAUSAL || key <= qrow);
             if (!ok) sc[kb][j] = -INFINITY;
           }
       }
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int key = kv0 + 32 * kb + result_row(j, g);
-            if (need_mask && (key >= N || (CAUSAL && key > qrow))) s2[kb][j] = -INFINITY;
+            if (need_mask && (key >= Nkv || (CAUSAL && key > qrow))) s2[kb][j] = -INFINITY;
             mx = fmaxf(mx, s2[kb][j]);
           }
         mx = halves_max(mx) * c;
@@ -390,12 +392,14 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
-  const int N = a.N;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
   const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
   const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
   const rsrc_t ro = make_rsrc(a.o + (int64_t)head * N * D, slab);
-  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * N * D, slab);
-  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * N * D, slab);
+  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
   const int q0 = qtile * T::BM;
   const int q0w = q0 + 32 * wave;
@@ -408,7 +412,7 @@ void fwd_pipe_kernel(FwdArgs a) {
     qf[kk] = __builtin_bit_cast(half8, buf_load_b128(rq, (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u));
   wait_all_vm();
 
-  const int kv_end = CAUSAL ? min(N, q0 + T::BM) : N;
+  const int kv_end = CAUSAL ? min(Nkv, q0 + T::BM) : Nkv;
   const int nunits = (kv_end + T::KT - 1) / T::KT;
   const int npad = (nunits + NS - 1) / NS * NS;
 
@@ -417,7 +421,7 @@ void fwd_pipe_kernel(FwdArgs a) {
   const uint32_t lds0 = lds_addr(lds);
   int i_row = 0;  // first key row of the next unit to fetch
   auto issue = [&](int slot) {
-    const int row0 = i_row < kv_end ? i_row : N;  // past the end: zeros
+    const int row0 = i_row < kv_end ? i_row : Nkv;  // past the end: zeros
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;
@@ -517,13 +521,13 @@ void fwd_pipe_kernel(FwdArgs a) {
 
     // Unit modes (wave-uniform): keys all past the queries (or past N), or
     // a diagonal / tail unit whose masked scores become -inf.
-    const bool dead = (CAUSAL && ka > q0w) || ka >= N;
+    const bool dead = (CAUSAL && ka > q0w) || ka >= Nkv;
     float m_eff = dead ? inf : m;
-    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > N)) {
+    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > Nkv)) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int key = ka + result_row(j, g);
-        if (key >= N || (CAUSAL && key > qrow)) s_cur[j] = -inf;
+        if (key >= Nkv || (CAUSAL && key > qrow)) s_cur[j] = -inf;
       }
     }
 

@@ -20,7 +20,8 @@ struct FwdArgs {
   const half_t* v;
   half_t* o;
   float* lse;
-  int N;           // sequence length (queries == keys)
+  int N;           // query sequence length
+  int Nkv;         // key/value sequence length (== N for self-attention)
   int Hq, Hkv;     // query heads, key/value heads
   int group;       // Hq / Hkv
   int BH;          // B * Hq
@@ -39,7 +40,8 @@ struct BwdArgs {
   half_t* dq;
   half_t* dk;
   half_t* dv;
-  int N;
+  int N;           // query sequence length
+  int Nkv;         // key/value sequence length (== N for self-attention)
   int Hq, Hkv, group;
   int BH;          // B * Hq
   int BHkv;        // B * Hkv

@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FA_OK = 0
 FA_ERR_NULL_POINTER = -1
@@ -67,7 +67,14 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
 for _name in ("fa_fwd", "fa_bwd_preprocess", "fa_bwd_dkdv", "fa_bwd_dkdv_ws", "fa_bwd_dq",
               "fa_bwd_dq_delta"):
     SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
-del _name
+# Cross-attention launches: one more length (N_kv) after N, fp16 and bf16.
+SIGNATURES["fa_bwd_dkdv_workspace_bytes_kv"] = (_I64, (_I64, _I64, _I64, _I64, _I64, _I64, _INT))
+for _name, _n_ptr in (("fa_fwd", 5), ("fa_bwd_dkdv_ws", 8), ("fa_bwd_dq_delta", 8)):
+    _res, _args = SIGNATURES[_name]
+    _kv = (_res, _args[:_n_ptr + 4] + (_I64,) + _args[_n_ptr + 4:])  # ..., N_q, N_kv, D, ...
+    SIGNATURES[_name + "_kv"] = _kv
+    SIGNATURES[_name + "_kv_bf16"] = _kv
+del _name, _n_ptr, _res, _args, _kv
 
 
 class FlashAttentionError(RuntimeError):

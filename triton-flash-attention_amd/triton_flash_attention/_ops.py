@@ -12,6 +12,10 @@ Reference launches replaced (triton_flash_attention/attention.py):
     flash_bwd_dkdv       -> _attn_bwd[grid], phase 1     754-770 (428-505)
     flash_bwd_dq         -> _attn_bwd[grid], phase 2     754-770 (507-573)
     flash_bwd_dq_delta   -> preprocess + phase 2         736-744, 754-770
+
+The forward and the backward also serve cross-attention (key/value length
+N_kv != query length N), which the reference sends to torch SDPA
+(attention.py:639-642): those calls go to the library's ``*_kv`` entry points.
 """
 
 from __future__ import annotations
@@ -108,21 +112,30 @@ def _entry(lib, base: str, dtype: torch.dtype):
     return getattr(lib, base + _ELEM_SUFFIX[dtype])
 
 
+def _entry_lengths(lib, base: str, dtype: torch.dtype, n: int, n_kv: int):
+    """(entry point, length arguments): the self-attention entry with (N,),
+    or its cross-attention twin ``base_kv`` with (N_q, N_kv)."""
+    if n == n_kv:
+        return _entry(lib, base, dtype), (n,)
+    return _entry(lib, base + "_kv", dtype), (n, n_kv)
+
+
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     """The kernels move 128-bit vectors: a view whose data pointer is not
     16-byte aligned is copied into a fresh (aligned) allocation."""
     return t if t.data_ptr() % 16 == 0 else t.clone(memory_format=torch.contiguous_format)
 
 
-def _qkv_dims(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, int, int, int, int]:
+def _qkv_dims(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, ...]:
+    """(B, Hq, Hkv, N, N_kv, D) of q [B,Hq,N,D] and k, v [B,Hkv,N_kv,D]."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k, v must be 4-D [batch, heads, sequence, head_dim]")
     B, Hq, N, D = q.shape
-    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != N or k.shape[3] != D:
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
         raise ValueError(
-            f"k and v must have shape [{B}, Hkv, {N}, {D}]; got {tuple(k.shape)}, {tuple(v.shape)}"
+            f"k and v must have shape [{B}, Hkv, N_kv, {D}]; got {tuple(k.shape)}, {tuple(v.shape)}"
         )
-    return B, Hq, k.shape[1], N, D
+    return B, Hq, k.shape[1], N, k.shape[2], D
 
 
 def flash_fwd(
@@ -132,16 +145,17 @@ def flash_fwd(
     dt = _elem_dtype(q, "q")
     for name, t in (("q", q), ("k", k), ("v", v)):
         _require(t, name, dt, q.device)
-    B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
+    B, Hq, Hkv, N, Nkv, D = _qkv_dims(q, k, v)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     lib = _lib.load()
+    fn, lengths = _entry_lengths(lib, "fa_fwd", dt, N, Nkv)
     o = torch.empty_like(q)
     lse = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
     with torch.cuda.device(q.device):
         rc = _launch(
-            "fwd", _entry(lib, "fa_fwd", dt),
+            "fwd", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+            B, Hq, Hkv, *lengths, D, float(scale), int(bool(causal)), _stream(q),
         )
     _lib.check(rc)
     return o, lse
@@ -171,12 +185,13 @@ def _check_bwd_inputs(q, k, v, do, lse, delta):
         _require(t, name, dt, q.device)
     for name, t in (("lse", lse), ("delta", delta)):
         _require(t, name, torch.float32, q.device)
-    B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
+    dims = _qkv_dims(q, k, v)
+    B, Hq, _, N, _, _ = dims
     if do.shape != q.shape:
         raise ValueError("dO must have the shape of q")
     if lse.shape != (B, Hq, N) or delta.shape != (B, Hq, N):
         raise ValueError("lse and delta must have shape [B, Hq, N]")
-    return B, Hq, Hkv, N, D
+    return dims
 
 
 def _aligned_all(*tensors):
@@ -186,25 +201,29 @@ def _aligned_all(*tensors):
 def flash_bwd_dkdv(
     q, k, v, do, lse, delta, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """dK, dV [B,Hkv,N,D] in q's dtype (GQA groups reduced in fp32, deterministic).
+    """dK, dV [B,Hkv,N_kv,D] in q's dtype (GQA groups reduced in fp32, deterministic).
 
     Shapes with too few key tiles to fill the GPU get a workspace (from the
     caching allocator) for the library's split-and-reduce mode."""
-    B, Hq, Hkv, N, D = _check_bwd_inputs(q, k, v, do, lse, delta)
+    B, Hq, Hkv, N, Nkv, D = _check_bwd_inputs(q, k, v, do, lse, delta)
     q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
     lib = _lib.load()
+    fn, lengths = _entry_lengths(lib, "fa_bwd_dkdv_ws", q.dtype, N, Nkv)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    ws_bytes = lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, int(bool(causal)))
+    if N == Nkv:
+        ws_bytes = lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, int(bool(causal)))
+    else:
+        ws_bytes = lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, Nkv, D, int(bool(causal)))
     if ws_bytes < 0:
         _lib.check(ws_bytes)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
     with torch.cuda.device(q.device):
         rc = _launch(
-            "dkdv", _entry(lib, "fa_bwd_dkdv_ws", q.dtype),
+            "dkdv", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
             delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-            B, Hq, Hkv, N, D, float(scale), int(bool(causal)),
+            B, Hq, Hkv, *lengths, D, float(scale), int(bool(causal)),
             ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q),
         )
     _lib.check(rc)
@@ -212,8 +231,11 @@ def flash_bwd_dkdv(
 
 
 def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.Tensor:
-    """dQ [B,Hq,N,D] in q's dtype."""
-    B, Hq, Hkv, N, D = _check_bwd_inputs(q, k, v, do, lse, delta)
+    """dQ [B,Hq,N,D] in q's dtype (self-attention; cross-attention takes
+    :func:`flash_bwd_dq_delta`)."""
+    B, Hq, Hkv, N, Nkv, D = _check_bwd_inputs(q, k, v, do, lse, delta)
+    if N != Nkv:
+        raise ValueError("flash_bwd_dq serves N_kv == N; use flash_bwd_dq_delta for cross-attention")
     q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
     lib = _lib.load()
     dq = torch.empty_like(q)
@@ -231,7 +253,7 @@ def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.T
 def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
     """Delta [B,H,N] fp32 = rowsum(O * dO) and dQ [B,Hq,N,D] (q's dtype) in one
     call (one launch when the dQ tiling computes Delta itself)."""
-    B, Hq, Hkv, N, D = _qkv_dims(q, k, v)
+    B, Hq, Hkv, N, Nkv, D = _qkv_dims(q, k, v)
     _require(o, "o", _elem_dtype(q, "q"), q.device)
     if o.shape != q.shape:
         raise ValueError("o must have the shape of q")
@@ -239,13 +261,14 @@ def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
     _check_bwd_inputs(q, k, v, do, lse, delta)
     q, k, v, o, do, lse = _aligned_all(q, k, v, o, do, lse)
     lib = _lib.load()
+    fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", q.dtype, N, Nkv)
     dq = torch.empty_like(q)
     with torch.cuda.device(q.device):
         rc = _launch(
-            "dq", _entry(lib, "fa_bwd_dq_delta", q.dtype),
+            "dq", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
             lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
-            B, Hq, Hkv, N, D, float(scale), int(bool(causal)), _stream(q),
+            B, Hq, Hkv, *lengths, D, float(scale), int(bool(causal)), _stream(q),
         )
     _lib.check(rc)
     return delta, dq

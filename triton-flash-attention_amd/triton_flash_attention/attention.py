@@ -7,18 +7,22 @@ eligible inputs run the hand-written gfx950 HIP kernels of libfa_gfx950.so
 through :mod:`._ops` instead of Triton kernels.
 
 Dispatch rules (first match wins; reference rules at attention.py:629-670):
-  1. cross-attention (N_q != N_kv)          -> torch   (ref 639-642)
-  2. value head size != query head size     -> torch   (ref 643-646)
-  3. not a GPU ("cuda") tensor              -> torch   (ref 647-648)
-  4. dtype is not float16 or bfloat16       -> torch   (ref 653-656 accepts float16
+  1. value head size != query head size     -> torch   (ref 643-646)
+  2. not a GPU ("cuda") tensor              -> torch   (ref 647-648)
+  3. dtype is not float16 or bfloat16       -> torch   (ref 653-656 accepts float16
                                                         only; bfloat16 is an added
                                                         dtype of the gfx950 kernels)
-  5. head_dim not in (32, 64, 128)          -> torch   (ref 657-661)
-  6. sequence too long for 32-bit offsets   -> torch   (no reference counterpart)
-  7. device is not gfx950                   -> torch   (replaces ref 662-666, SM >= 8)
-  8. libfa_gfx950.so not loadable           -> torch   (replaces ref 649-652, the ROCm
+  4. head_dim not in (32, 64, 128)          -> torch   (ref 657-661)
+  5. sequence too long for 32-bit offsets   -> torch   (no reference counterpart)
+  6. device is not gfx950                   -> torch   (replaces ref 662-666, SM >= 8)
+  7. libfa_gfx950.so not loadable           -> torch   (replaces ref 649-652, the ROCm
                                                         reject); see below
-  9. otherwise                              -> "triton" (the custom kernel backend)
+  8. otherwise                              -> "triton" (the custom kernel backend)
+
+The reference's first rule, cross-attention (N_q != N_kv) -> torch (ref 639-642),
+is gone: the gfx950 kernels take separate query and key/value lengths and
+compute what that SDPA fallback does, top-left causal mask included (query i
+sees keys j <= i).
 
 The backend keeps the reference's name "triton" so existing call sites
 (``backend="triton"``) run unchanged; it now means "the custom fused kernel".
@@ -130,10 +134,6 @@ class _DispatchFacts:
 
 def _decide(facts: _DispatchFacts) -> DispatchDecision:
     """First-match dispatch rules (ref attention.py:639-670, module docstring)."""
-    if facts.q_len != facts.kv_len:
-        return DispatchDecision(
-            "torch", "the custom kernel currently specializes in self-attention"
-        )
     if facts.value_head_dim != facts.head_dim:
         return DispatchDecision(
             "torch", "the custom kernel requires equal query/key and value head sizes"
@@ -149,7 +149,7 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         return DispatchDecision(
             "torch", f"head_dim must be one of ({supported}) for the Triton path"
         )
-    if facts.q_len * facts.head_dim * 2 > _MAX_SLAB_BYTES:
+    if max(facts.q_len, facts.kv_len) * facts.head_dim * 2 > _MAX_SLAB_BYTES:
         return DispatchDecision(
             "torch", "the sequence is too long for the 32-bit addressed gfx950 kernel"
         )
@@ -162,9 +162,10 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         )
     if facts.library_error is not None:
         return DispatchDecision("torch", f"{_REASON_LIBRARY}: {facts.library_error}")
+    kind = "self-attention" if facts.q_len == facts.kv_len else "cross-attention"
     return DispatchDecision(
         "triton",
-        f"gfx950 {str(facts.dtype).removeprefix('torch.')} self-attention with a supported "
+        f"gfx950 {str(facts.dtype).removeprefix('torch.')} {kind} with a supported "
         "head dimension",
     )
 
@@ -198,7 +199,8 @@ class TritonAttention(torch.autograd.Function):
 
     Same contract as the reference class (attention.py:673-771):
     ``apply(query, key, value, causal, softmax_scale) -> output`` on contiguous
-    fp16 [B, H, N, D] tensors; backward returns ``(dQ, dK, dV, None, None)``.
+    fp16 or bf16 query [B, Hq, N, D] and key/value [B, Hkv, N_kv, D] tensors;
+    backward returns ``(dQ, dK, dV, None, None)``.
     """
 
     @staticmethod
@@ -249,10 +251,10 @@ def scaled_dot_product_attention(
 
     The custom gfx950 path supports forward/backward, causal and bidirectional
     attention, arbitrary positive sequence lengths, and GQA, for float16 or
-    bfloat16 self-attention with head_dim 32, 64 or 128. Other inputs fall back to
-    PyTorch when ``backend="auto"``; ``backend="triton"`` requires the custom
-    kernel and raises RuntimeError otherwise; ``backend="torch"`` always uses
-    PyTorch SDPA.
+    bfloat16 self- or cross-attention with head_dim 32, 64 or 128. Other inputs
+    fall back to PyTorch when ``backend="auto"``; ``backend="triton"`` requires
+    the custom kernel and raises RuntimeError otherwise; ``backend="torch"``
+    always uses PyTorch SDPA.
     """
     if backend not in ("auto", "triton", "torch"):
         raise ValueError("backend must be one of: 'auto', 'triton', 'torch'")
