@@ -10,25 +10,27 @@
  * Every function cites the reference lines it restates
  * (/root/reference/triton_flash_attention/attention.py, docs/architecture.md).
  * Inputs are the fp16 values of the tensors, widened exactly to double.
- * Layouts: q, o, dO, dq [B,Hq,N,D]; k, v, dk, dv [B,Hkv,Nkv,D]; lse2, delta
- * [B,Hq,N]; all contiguous row-major. The reference kernels are
- * self-attention (Nkv == N); the closed forms also take Nkv != N, the
- * cross-attention the reference hands to torch SDPA (attention.py:639-642,
- * 830-838), with SDPA's causal mask for unequal lengths: query i sees keys
- * j <= i (the lower triangle of the N x Nkv all-ones matrix).
+ * Layouts: q, dq [B,Hq,N,D]; k, dk [B,Hkv,Nkv,D]; v, dv [B,Hkv,Nkv,Dv];
+ * o, dO [B,Hq,N,Dv]; lse2, delta [B,Hq,N]; all contiguous row-major. The
+ * reference kernels are self-attention with one head size (Nkv == N,
+ * Dv == D); the closed forms also take Nkv != N and Dv != D, inputs the
+ * reference hands to torch SDPA (attention.py:639-646, 830-838), with SDPA's
+ * causal mask for unequal lengths: query i sees keys j <= i (the lower
+ * triangle of the N x Nkv all-ones matrix).
  *
  * Pinning (what checks each function; see tests/test_oracle.py):
  *   oracle_round_half      numpy float16 conversion on 10^5 values incl. ties,
  *                          subnormals and overflow
  *   oracle_fwd_direct      torch fp64 SDPA and logsumexp (Nkv == N and
- *                          Nkv != N); golden fixtures; closed forms (causal
+ *                          Nkv != N, Dv == D and Dv != D); golden fixtures;
+ *                          closed forms (causal
  *                          row 0, Q=0 uniform attention, constant V, N=1)
  *   oracle_fwd_online      oracle_fwd_direct (tiling independence at fp64),
  *                          and with round_p=1 the fp16-P rounding bound
  *   oracle_bwd_preprocess  exact dot products of small integers; golden Delta
  *   oracle_bwd             torch fp64 autograd through SDPA (Nkv == N and
  *                          Nkv != N, where keys past the last causal query
- *                          get zero gradients); golden fixtures;
+ *                          get zero gradients; Dv != D); golden fixtures;
  *                          closed forms (constant V -> dQ = dK = 0, N=1);
  *                          GQA group sum == MHA with repeated K/V
  *   oracle_bwd, fold = 1/2 equal to fold = 0 when c32 is a power of two (the
@@ -85,8 +87,8 @@ static int64_t kv_head_of(int64_t b, int64_t hq, int64_t Hq, int64_t Hkv) {
  *   o_i    = sum_valid exp2(s_ij - lse2_i) v_j (attention.py:231)
  * Two passes over the keys, no tiling, no intermediate rounding. */
 void oracle_fwd_direct(const double* q, const double* k, const double* v, int64_t B, int64_t Hq,
-                       int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, double scale, int causal,
-                       double* o, double* lse2) {
+                       int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, int64_t Dv, double scale,
+                       int causal, double* o, double* lse2) {
   const double c = scale * INV_LN2;
 #pragma omp parallel for schedule(dynamic)
   for (int64_t bh = 0; bh < B * Hq; ++bh) {
@@ -94,7 +96,7 @@ void oracle_fwd_direct(const double* q, const double* k, const double* v, int64_
     const int64_t kvh = kv_head_of(b, hq, Hq, Hkv);
     const double* Q = q + bh * N * D;
     const double* K = k + kvh * Nkv * D;
-    const double* V = v + kvh * Nkv * D;
+    const double* V = v + kvh * Nkv * Dv;
     double* s = (double*)malloc(sizeof(double) * (size_t)Nkv);
     for (int64_t i = 0; i < N; ++i) {
       const int64_t last = causal && i < Nkv - 1 ? i : Nkv - 1;
@@ -106,12 +108,12 @@ void oracle_fwd_direct(const double* q, const double* k, const double* v, int64_
       double l = 0.0;
       for (int64_t j = 0; j <= last; ++j) l += exp2(s[j] - mx);
       const double lse = mx + log2(l);
-      double* out = o + (bh * N + i) * D;
-      for (int64_t d = 0; d < D; ++d) out[d] = 0.0;
+      double* out = o + (bh * N + i) * Dv;
+      for (int64_t d = 0; d < Dv; ++d) out[d] = 0.0;
       for (int64_t j = 0; j <= last; ++j) {
         const double p = exp2(s[j] - lse);
-        const double* vj = V + j * D;
-        for (int64_t d = 0; d < D; ++d) out[d] += p * vj[d];
+        const double* vj = V + j * Dv;
+        for (int64_t d = 0; d < Dv; ++d) out[d] += p * vj[d];
       }
       lse2[bh * N + i] = lse;
     }
@@ -248,8 +250,8 @@ static void scaled_operand(const double* x, int64_t n, float c32, int fold, doub
  * head so each output row has one writer. */
 void oracle_bwd(const double* q, const double* k, const double* v, const double* dO,
                 const double* lse2, const double* delta, int64_t B, int64_t Hq, int64_t Hkv,
-                int64_t N, int64_t Nkv, int64_t D, double scale, int causal, int fold,
-                double* dq, double* dk, double* dv) {
+                int64_t N, int64_t Nkv, int64_t D, int64_t Dv, double scale, int causal,
+                int fold, double* dq, double* dk, double* dv) {
   const double c = scale * INV_LN2;
   const float c32 = (float)scale * (float)INV_LN2;
   const int64_t group = Hq / Hkv;
@@ -257,23 +259,23 @@ void oracle_bwd(const double* q, const double* k, const double* v, const double*
   for (int64_t bkv = 0; bkv < B * Hkv; ++bkv) {
     const int64_t b = bkv / Hkv, hkv = bkv % Hkv;
     const double* K = k + bkv * Nkv * D;
-    const double* V = v + bkv * Nkv * D;
+    const double* V = v + bkv * Nkv * Dv;
     double* dK = dk + bkv * Nkv * D;
-    double* dV = dv + bkv * Nkv * D;
+    double* dV = dv + bkv * Nkv * Dv;
     memset(dK, 0, sizeof(double) * (size_t)(Nkv * D));
-    memset(dV, 0, sizeof(double) * (size_t)(Nkv * D));
+    memset(dV, 0, sizeof(double) * (size_t)(Nkv * Dv));
     double* ks = fold ? (double*)malloc(sizeof(double) * (size_t)(Nkv * D)) : NULL;
     double* qs = fold ? (double*)malloc(sizeof(double) * (size_t)(N * D)) : NULL;
     if (fold) scaled_operand(K, Nkv * D, c32, fold, ks);
     for (int64_t gi = 0; gi < group; ++gi) {
       const int64_t bh = b * Hq + hkv * group + gi;
       const double* Q = q + bh * N * D;
-      const double* G = dO + bh * N * D;
+      const double* G = dO + bh * N * Dv;
       double* dQ = dq + bh * N * D;
       if (fold) scaled_operand(Q, N * D, c32, fold, qs);
       for (int64_t i = 0; i < N; ++i) {
         const double* qi = Q + i * D;
-        const double* gi_row = G + i * D;
+        const double* gi_row = G + i * Dv;
         double* dqi = dQ + i * D;
         for (int64_t d = 0; d < D; ++d) dqi[d] = 0.0;
         const double lse = lse2[bh * N + i];
@@ -284,14 +286,14 @@ void oracle_bwd(const double* q, const double* k, const double* v, const double*
           const double p_k = fold ? exp2(dot(qi, ks + j * D, D) - lse)
                                   : exp2(dot(qi, K + j * D, D) * c - lse);
           const double p_q = fold ? exp2(dot(qs + i * D, K + j * D, D) - lse) : p_k;
-          const double dp = dot(gi_row, V + j * D, D);
+          const double dp = dot(gi_row, V + j * Dv, Dv);
           const double ds_k = p_k * (dp - dlt);
           const double ds_q = p_q * (dp - dlt);
-          double* dvj = dV + j * D;
+          double* dvj = dV + j * Dv;
           double* dkj = dK + j * D;
           const double* kj = K + j * D;
+          for (int64_t d = 0; d < Dv; ++d) dvj[d] += p_k * gi_row[d];
           for (int64_t d = 0; d < D; ++d) {
-            dvj[d] += p_k * gi_row[d];
             dkj[d] += scale * ds_k * qi[d];
             dqi[d] += scale * ds_q * kj[d];
           }

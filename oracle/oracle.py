@@ -13,6 +13,7 @@ Functions and the reference lines they restate
                             scores c q.k in exact arithmetic
     fwd / bwd with k, v of length Nkv != N: cross-attention as the reference's SDPA
                             fallback computes it (639-642, 830-838; top-left causal mask)
+    fwd / bwd with v of head size Dv != D: the same fallback's other case (643-646)
     bwd(..., fold=True)     the same with the reference's fp16-rounded score operands,
                             fp16(c k) for dK/dV and fp16(c q) for dQ (435, 515);
                             fold="bfloat16" rounds them to bf16 (the added bf16 path)
@@ -56,14 +57,14 @@ def _load():
     lib.oracle_round_half_array.restype = None
     lib.oracle_round_half_array.argtypes = [P, P, I64]
     lib.oracle_fwd_direct.restype = None
-    lib.oracle_fwd_direct.argtypes = [P, P, P, I64, I64, I64, I64, I64, I64, F64, INT, P, P]
+    lib.oracle_fwd_direct.argtypes = [P, P, P, I64, I64, I64, I64, I64, I64, I64, F64, INT, P, P]
     lib.oracle_fwd_online.restype = None
     lib.oracle_fwd_online.argtypes = [P, P, P, I64, I64, I64, I64, I64, F64, INT, I64, I64, INT, P, P]
     lib.oracle_bwd_preprocess.restype = None
     lib.oracle_bwd_preprocess.argtypes = [P, P, I64, I64, P]
     lib.oracle_bwd.restype = None
-    lib.oracle_bwd.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, F64, INT, INT, P, P,
-                               P]
+    lib.oracle_bwd.argtypes = [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, F64, INT, INT,
+                               P, P, P]
     _lib = lib
     return lib
 
@@ -77,16 +78,16 @@ def _ptr(a: np.ndarray) -> int:
 
 
 def _dims(q, k, v):
-    """(B, Hq, Hkv, N, Nkv, D) of q [B,Hq,N,D] and k, v [B,Hkv,Nkv,D]."""
+    """(B, Hq, Hkv, N, Nkv, D, Dv) of q [B,Hq,N,D], k [B,Hkv,Nkv,D], v [B,Hkv,Nkv,Dv]."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k, v must be 4-D [B, H, N, D]")
     B, Hq, N, D = q.shape
-    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != D:
+    if k.shape[:3] != v.shape[:3] or k.shape[0] != B or k.shape[3] != D:
         raise ValueError("k/v shape mismatch")
     Hkv = k.shape[1]
     if Hq % Hkv:
         raise ValueError("Hq must be a multiple of Hkv")
-    return B, Hq, Hkv, N, k.shape[2], D
+    return B, Hq, Hkv, N, k.shape[2], D, v.shape[3]
 
 
 def round_half(x) -> np.ndarray:
@@ -98,22 +99,23 @@ def round_half(x) -> np.ndarray:
 
 def fwd(q, k, v, causal: bool, scale: float | None = None, *, online: bool = False,
         block_m: int = 128, block_n: int = 32, round_p: bool = True):
-    """(O, LSE2): O [B,Hq,N,D] and base-2 LSE [B,Hq,N], float64. The closed
-    form also takes k, v of another length Nkv (SDPA's top-left causal mask);
-    the online form restates the reference's self-attention tiling only."""
+    """(O, LSE2): O [B,Hq,N,Dv] and base-2 LSE [B,Hq,N], float64. The closed
+    form also takes k, v of another length Nkv (SDPA's top-left causal mask)
+    and v of another head size Dv; the online form restates the reference's
+    self-attention tiling only."""
     q, k, v = _f64(q), _f64(k), _f64(v)
-    B, Hq, Hkv, N, Nkv, D = _dims(q, k, v)
-    if online and Nkv != N:
-        raise ValueError("the online form is self-attention only (Nkv == N)")
+    B, Hq, Hkv, N, Nkv, D, Dv = _dims(q, k, v)
+    if online and (Nkv != N or Dv != D):
+        raise ValueError("the online form is self-attention with one head size only")
     scale = D ** -0.5 if scale is None else float(scale)
-    o = np.empty((B, Hq, N, D), dtype=np.float64)
+    o = np.empty((B, Hq, N, Dv), dtype=np.float64)
     lse = np.empty((B, Hq, N), dtype=np.float64)
     lib = _load()
     if online:
         lib.oracle_fwd_online(_ptr(q), _ptr(k), _ptr(v), B, Hq, Hkv, N, D, scale, int(causal),
                               block_m, block_n, int(round_p), _ptr(o), _ptr(lse))
     else:
-        lib.oracle_fwd_direct(_ptr(q), _ptr(k), _ptr(v), B, Hq, Hkv, N, Nkv, D, scale,
+        lib.oracle_fwd_direct(_ptr(q), _ptr(k), _ptr(v), B, Hq, Hkv, N, Nkv, D, Dv, scale,
                               int(causal), _ptr(o), _ptr(lse))
     return o, lse
 
@@ -141,14 +143,14 @@ def bwd(q, k, v, do, lse2, delta, causal: bool, scale: float | None = None, *,
         raise ValueError(f"fold must be one of {list(_FOLD_MODES)}")
     q, k, v, do = _f64(q), _f64(k), _f64(v), _f64(do)
     lse2, delta = _f64(lse2), _f64(delta)
-    B, Hq, Hkv, N, Nkv, D = _dims(q, k, v)
+    B, Hq, Hkv, N, Nkv, D, Dv = _dims(q, k, v)
     scale = D ** -0.5 if scale is None else float(scale)
     dq = np.empty_like(q)
     dk = np.empty_like(k)
     dv = np.empty_like(v)
     _load().oracle_bwd(_ptr(q), _ptr(k), _ptr(v), _ptr(do), _ptr(lse2), _ptr(delta),
-                       B, Hq, Hkv, N, Nkv, D, scale, int(causal), _FOLD_MODES[fold], _ptr(dq),
-                       _ptr(dk), _ptr(dv))
+                       B, Hq, Hkv, N, Nkv, D, Dv, scale, int(causal), _FOLD_MODES[fold],
+                       _ptr(dq), _ptr(dk), _ptr(dv))
     return dq, dk, dv
 
 

@@ -23,18 +23,20 @@ REL_L2_TOL = 5e-3
 LSE_TOL = 1e-4
 
 
-def make_inputs(B, Hq, Hkv, N, D, seed, mult=1.0, do_mult=None, dtype=torch.float16, n_kv=None):
+def make_inputs(B, Hq, Hkv, N, D, seed, mult=1.0, do_mult=None, dtype=torch.float16, n_kv=None,
+                d_v=None):
     """q, k, v, dO as CPU tensors of ``dtype`` (fp16 by default): fp32 N(0,1)
     from a seeded CPU generator drawn in the order q, k, v, dO, times ``mult``
     (dO times ``do_mult``, default ``mult``), then cast. k and v have ``n_kv``
-    rows (default N)."""
+    rows (default N); v and dO have head size ``d_v`` (default D)."""
     g = torch.Generator("cpu").manual_seed(seed)
     do_mult = mult if do_mult is None else do_mult
     n_kv = N if n_kv is None else n_kv
+    d_v = D if d_v is None else d_v
     q = torch.randn((B, Hq, N, D), generator=g, dtype=torch.float32) * mult
     k = torch.randn((B, Hkv, n_kv, D), generator=g, dtype=torch.float32) * mult
-    v = torch.randn((B, Hkv, n_kv, D), generator=g, dtype=torch.float32) * mult
-    do = torch.randn((B, Hq, N, D), generator=g, dtype=torch.float32) * do_mult
+    v = torch.randn((B, Hkv, n_kv, d_v), generator=g, dtype=torch.float32) * mult
+    do = torch.randn((B, Hq, N, d_v), generator=g, dtype=torch.float32) * do_mult
     return q.to(dtype), k.to(dtype), v.to(dtype), do.to(dtype)
 
 

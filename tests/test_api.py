@@ -161,6 +161,11 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
     # bfloat16 is served too (the reference sends it to SDPA, attention.py:653-656)
     d = attn._decide(_facts(dtype=torch.bfloat16))
     assert d.backend == "triton" and "bfloat16" in d.reason
+    # A value head size other than D is served when both are supported sizes
+    # (the reference sends D_v != D to SDPA, attention.py:643-646).
+    for D, Dv in ((64, 32), (32, 128), (128, 64)):
+        d = attn._decide(_facts(head_dim=D, value_head_dim=Dv))
+        assert d.backend == "triton" and f"zero-padded to {max(D, Dv)}" in d.reason
     # Cross-attention is served too (the reference sends it to SDPA, attention.py:639-642).
     for q_len, kv_len in ((128, 64), (3, 5000)):
         d = attn._decide(_facts(q_len=q_len, kv_len=kv_len))
@@ -171,7 +176,9 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
 @pytest.mark.parametrize(
     ("overrides", "reason"),
     [
-        (dict(value_head_dim=32), "equal query/key and value head sizes"),
+        (dict(value_head_dim=48), "equal query/key and value head sizes"),
+        (dict(value_head_dim=16, head_dim=32), "two different ones from (32, 64, 128)"),
+        (dict(head_dim=48, value_head_dim=64), "equal query/key and value head sizes"),
         (dict(device_type="cpu"), "requires a CUDA tensor"),
         (dict(dtype=torch.float32), "supports float16 and bfloat16"),
         (dict(dtype=torch.float64), "supports float16 and bfloat16"),
@@ -192,7 +199,7 @@ def test_rule_fallback_reasons(overrides, reason) -> None:
 
 def test_rule_order_is_first_match() -> None:
     # value head size wins over everything, dtype wins over head_dim and arch
-    d = attn._decide(_facts(kv_len=3, value_head_dim=32, dtype=torch.float32, arch="gfx90a"))
+    d = attn._decide(_facts(kv_len=3, value_head_dim=40, dtype=torch.float32, arch="gfx90a"))
     assert "value head sizes" in d.reason
     d = attn._decide(_facts(dtype=torch.float32, head_dim=48, value_head_dim=48, arch="gfx90a"))
     assert "float16" in d.reason

@@ -553,3 +553,47 @@ def test_bf16_cross_attention_matches_oracle(head_dim):
             check_bf16_against_oracle(
                 got, q, k, v, do, causal,
                 tag=f"bf16 cross N_q={N} N_kv={Nkv} D={head_dim} causal={causal}")
+
+
+# ---------------------------------------------------------------------------
+# Value head size != query/key head size (the reference sends it to SDPA,
+# attention.py:643-646): served by zero-padding the narrower operands.
+# ---------------------------------------------------------------------------
+VALUE_HEAD_CASES = [
+    # (B, Hq, Hkv, N_q, N_kv, D, D_v)
+    (1, 4, 2, 300, 300, 64, 32),
+    (2, 4, 4, 129, 257, 32, 128),
+    (1, 2, 1, 333, 97, 128, 64),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", VALUE_HEAD_CASES,
+                         ids=lambda c: f"Nq{c[3]}Nkv{c[4]}-D{c[5]}Dv{c[6]}")
+def test_value_head_size_matches_oracle(case, causal):
+    B, Hq, Hkv, N, Nkv, D, Dv = case
+    tag = f"D_v B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} D_v={Dv} causal={causal}"
+    _note(tag)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D + Dv, mult=0.5, n_kv=Nkv, d_v=Dv)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    gqa = Hq != Hkv
+    decision = explain_dispatch(qd, kd, vd, enable_gqa=gqa)
+    assert decision.backend == "triton" and "zero-padded" in decision.reason, decision.reason
+    out = scaled_dot_product_attention(qd, kd, vd, is_causal=causal, enable_gqa=gqa,
+                                       backend="triton")
+    assert out.shape == (B, Hq, N, Dv) and out.is_contiguous()
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    width = max(D, Dv)
+    pad = lambda t: torch.nn.functional.pad(t, (0, width - t.shape[-1])).to(DEV)
+    _, lse = _ops.flash_fwd(pad(q), pad(k), pad(v), causal, D ** -0.5)
+    torch.cuda.synchronize()
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal,
+                           o16=out.detach().cpu().numpy(), fold_bwd=True)
+    report = {}
+    for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        report[name] = assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name])
+    lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - ref["lse"])))
+    assert lse_err <= LSE_TOL, f"{tag} lse: max-abs {lse_err:.3e}"
+    _note(f"{tag}: " + ", ".join(f"{k}={v[0]:.2e}/{v[1]:.2e}" for k, v in report.items())
+          + f", lse={lse_err:.2e}")

@@ -26,13 +26,14 @@ from oracle import oracle
 GOLDEN = Path(__file__).resolve().parent / "golden" / "attention_fp64.npz"
 
 
-def _inputs(B, Hq, Hkv, N, D, seed, mult=1.0, n_kv=None):
+def _inputs(B, Hq, Hkv, N, D, seed, mult=1.0, n_kv=None, d_v=None):
     g = torch.Generator("cpu").manual_seed(seed)
     n_kv = N if n_kv is None else n_kv
+    d_v = D if d_v is None else d_v
     q = (torch.randn((B, Hq, N, D), generator=g) * mult).half()
     k = (torch.randn((B, Hkv, n_kv, D), generator=g) * mult).half()
-    v = (torch.randn((B, Hkv, n_kv, D), generator=g) * mult).half()
-    do = (torch.randn((B, Hq, N, D), generator=g) * mult).half()
+    v = (torch.randn((B, Hkv, n_kv, d_v), generator=g) * mult).half()
+    do = (torch.randn((B, Hq, N, d_v), generator=g) * mult).half()
     return q, k, v, do
 
 
@@ -236,6 +237,55 @@ def test_cross_attention_causal_closed_forms():
     o_all, lse_all = oracle.fwd(qn[:, :, 30:], kn, vn, False)
     assert _maxdiff(o[:, :, :30], o_top) < 1e-12 and _maxdiff(lse[:, :, :30], lse_top) < 1e-12
     assert _maxdiff(o[:, :, 30:], o_all) < 1e-12 and _maxdiff(lse[:, :, 30:], lse_all) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# Value head size != query/key head size (the fallback's other case, attention.py:643-646)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 2, 2, 33, 33, 64, 32), (2, 4, 2, 40, 70, 32, 128),
+                                   (1, 3, 1, 65, 17, 128, 64)])
+def test_value_head_size_matches_torch_fp64(shape, causal):
+    B, Hq, Hkv, N, Nkv, D, Dv = shape
+    q, k, v, do = _inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D + 7 * Dv, n_kv=Nkv, d_v=Dv)
+    ref = _torch_fp64(q, k, v, do, causal)
+    o, lse = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    assert o.shape == (B, Hq, N, Dv)
+    assert _maxdiff(o, ref["o"]) < 1e-12
+    assert _maxdiff(lse, ref["lse"]) < 1e-12
+    for fold in (False, True):
+        dq, dk, dv = oracle.bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), lse, ref["delta"],
+                                causal, fold=fold)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+        tol = 1e-12 if not fold else 5e-2  # fold rounds the score operands to fp16
+        assert _maxdiff(dq, ref["dq"]) < tol
+        assert _maxdiff(dk, ref["dk"]) < tol
+        assert _maxdiff(dv, ref["dv"]) < tol
+
+
+def test_zero_padding_a_head_size_is_exact():
+    """Zero columns appended to the narrower of (q, k) and v leave O, LSE and
+    the gradients of the real columns unchanged and give zero gradients in the
+    padded ones: the identity the library's D_v != D path relies on."""
+    q, k, v, do = _inputs(1, 4, 2, 50, 32, seed=21, n_kv=61, d_v=128)
+    qn, kn, vn, don = q.numpy(), k.numpy(), v.numpy(), do.numpy()
+    r = oracle.attention(qn, kn, vn, don, True, fold_bwd=True)
+    pad = lambda a, w: np.concatenate([a, np.zeros(a.shape[:-1] + (w - a.shape[-1],))], -1)
+    p = oracle.attention(pad(qn, 128), pad(kn, 128), vn, don, True, 32 ** -0.5, fold_bwd=True)
+    for name in ("o", "lse", "delta", "dv"):
+        assert _maxdiff(r[name], p[name]) == 0.0
+    for name in ("dq", "dk"):
+        assert _maxdiff(r[name], p[name][..., :32]) == 0.0
+        assert not p[name][..., 32:].any()
+    q, k, v, do = _inputs(1, 2, 2, 40, 128, seed=22, d_v=64)
+    qn, kn, vn, don = q.numpy(), k.numpy(), v.numpy(), do.numpy()
+    r = oracle.attention(qn, kn, vn, don, False, fold_bwd=True)
+    p = oracle.attention(qn, kn, pad(vn, 128), pad(don, 128), False, fold_bwd=True)
+    for name in ("lse", "delta", "dq", "dk"):
+        assert _maxdiff(r[name], p[name]) == 0.0
+    for name in ("o", "dv"):
+        assert _maxdiff(r[name], p[name][..., :64]) == 0.0
+        assert not p[name][..., 64:].any()
 
 
 def test_gqa_group_sum_identity():

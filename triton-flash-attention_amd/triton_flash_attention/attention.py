@@ -7,7 +7,8 @@ eligible inputs run the hand-written gfx950 HIP kernels of libfa_gfx950.so
 through :mod:`._ops` instead of Triton kernels.
 
 Dispatch rules (first match wins; reference rules at attention.py:629-670):
-  1. value head size != query head size     -> torch   (ref 643-646)
+  1. value head size != query head size     -> torch   (ref 643-646), unless both are
+     and not both supported                            supported head sizes (added)
   2. not a GPU ("cuda") tensor              -> torch   (ref 647-648)
   3. dtype is not float16 or bfloat16       -> torch   (ref 653-656 accepts float16
                                                         only; bfloat16 is an added
@@ -22,7 +23,10 @@ Dispatch rules (first match wins; reference rules at attention.py:629-670):
 The reference's first rule, cross-attention (N_q != N_kv) -> torch (ref 639-642),
 is gone: the gfx950 kernels take separate query and key/value lengths and
 compute what that SDPA fallback does, top-left causal mask included (query i
-sees keys j <= i).
+sees keys j <= i). A value head size other than the query/key one is served
+when both are supported sizes: :class:`TritonAttention` zero-pads the narrower
+operands to the wider size (zero columns add exact zeros to every dot product)
+and slices the results back.
 
 The backend keeps the reference's name "triton" so existing call sites
 (``backend="triton"``) run unchanged; it now means "the custom fused kernel".
@@ -134,9 +138,15 @@ class _DispatchFacts:
 
 def _decide(facts: _DispatchFacts) -> DispatchDecision:
     """First-match dispatch rules (ref attention.py:639-670, module docstring)."""
-    if facts.value_head_dim != facts.head_dim:
+    if facts.value_head_dim != facts.head_dim and (
+        facts.value_head_dim not in _SUPPORTED_HEAD_DIMS
+        or facts.head_dim not in _SUPPORTED_HEAD_DIMS
+    ):
+        supported = ", ".join(str(dim) for dim in _SUPPORTED_HEAD_DIMS)
         return DispatchDecision(
-            "torch", "the custom kernel requires equal query/key and value head sizes"
+            "torch",
+            "the custom kernel requires equal query/key and value head sizes, or two "
+            f"different ones from ({supported})",
         )
     if facts.device_type != "cuda":
         return DispatchDecision("torch", "the Triton kernel requires a CUDA tensor")
@@ -149,7 +159,8 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         return DispatchDecision(
             "torch", f"head_dim must be one of ({supported}) for the Triton path"
         )
-    if max(facts.q_len, facts.kv_len) * facts.head_dim * 2 > _MAX_SLAB_BYTES:
+    width = max(facts.head_dim, facts.value_head_dim)
+    if max(facts.q_len, facts.kv_len) * width * 2 > _MAX_SLAB_BYTES:
         return DispatchDecision(
             "torch", "the sequence is too long for the 32-bit addressed gfx950 kernel"
         )
@@ -163,10 +174,14 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
     if facts.library_error is not None:
         return DispatchDecision("torch", f"{_REASON_LIBRARY}: {facts.library_error}")
     kind = "self-attention" if facts.q_len == facts.kv_len else "cross-attention"
+    padded = ""
+    if facts.value_head_dim != facts.head_dim:
+        padded = (f" (value head_dim {facts.value_head_dim} != {facts.head_dim}: the narrower "
+                  f"operands are zero-padded to {width})")
     return DispatchDecision(
         "triton",
         f"gfx950 {str(facts.dtype).removeprefix('torch.')} {kind} with a supported "
-        "head dimension",
+        "head dimension" + padded,
     )
 
 
@@ -199,26 +214,43 @@ class TritonAttention(torch.autograd.Function):
 
     Same contract as the reference class (attention.py:673-771):
     ``apply(query, key, value, causal, softmax_scale) -> output`` on contiguous
-    fp16 or bf16 query [B, Hq, N, D] and key/value [B, Hkv, N_kv, D] tensors;
-    backward returns ``(dQ, dK, dV, None, None)``.
+    fp16 or bf16 query [B, Hq, N, D], key [B, Hkv, N_kv, D] and value
+    [B, Hkv, N_kv, D_v] tensors; backward returns ``(dQ, dK, dV, None, None)``.
+    With D_v != D the kernels run at width max(D, D_v) on zero-padded copies of
+    the narrower operands (and of dO), and the outputs are sliced back: zero
+    columns change no dot product, and their gradients are exactly zero.
     """
 
     @staticmethod
     def forward(ctx, query, key, value, causal, softmax_scale):
+        head_dim, value_head_dim = query.shape[-1], value.shape[-1]
+        width = max(head_dim, value_head_dim)
+        query, key, value = (_pad_head(t, width) for t in (query, key, value))
         output, lse = _ops.flash_fwd(query, key, value, bool(causal), float(softmax_scale))
         ctx.save_for_backward(query, key, value, output, lse)
+        ctx.head_dims = (head_dim, value_head_dim)
         ctx.softmax_scale = float(softmax_scale)
         ctx.causal = bool(causal)
-        return output
+        return output if value_head_dim == width else output[..., :value_head_dim].contiguous()
 
     @staticmethod
     def backward(ctx, grad_output):
         query, key, value, output, lse = ctx.saved_tensors
-        grad_output = grad_output.contiguous()
+        head_dim, value_head_dim = ctx.head_dims
+        grad_output = _pad_head(grad_output.contiguous(), query.shape[-1])
         grad_query, grad_key, grad_value = _ops.flash_bwd(
             query, key, value, output, lse, grad_output, ctx.causal, ctx.softmax_scale
         )
+        if head_dim != query.shape[-1]:
+            grad_query, grad_key = grad_query[..., :head_dim], grad_key[..., :head_dim]
+        if value_head_dim != query.shape[-1]:
+            grad_value = grad_value[..., :value_head_dim]
         return grad_query, grad_key, grad_value, None, None
+
+
+def _pad_head(t: torch.Tensor, width: int) -> torch.Tensor:
+    """``t``, or a contiguous copy with its last dimension zero-padded to ``width``."""
+    return t if t.shape[-1] == width else torch.nn.functional.pad(t, (0, width - t.shape[-1]))
 
 
 def _torch_sdpa(
@@ -251,7 +283,8 @@ def scaled_dot_product_attention(
 
     The custom gfx950 path supports forward/backward, causal and bidirectional
     attention, arbitrary positive sequence lengths, and GQA, for float16 or
-    bfloat16 self- or cross-attention with head_dim 32, 64 or 128. Other inputs
+    bfloat16 self- or cross-attention with head_dim 32, 64 or 128 (the value
+    head_dim too, equal to it or not). Other inputs
     fall back to PyTorch when ``backend="auto"``; ``backend="triton"`` requires
     the custom kernel and raises RuntimeError otherwise; ``backend="torch"``
     always uses PyTorch SDPA.
