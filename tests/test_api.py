@@ -88,21 +88,22 @@ def test_explicit_torch_backend_honors_custom_scale() -> None:
 
 
 def test_cross_attention_fallback_matches_reference() -> None:
-    # The reference's cross-attention test inputs: value head size 16 != 32
-    # still sends them to SDPA, now by the value-head-size rule.
+    # The reference's cross-attention test inputs (N_q 3, N_kv 5, value head
+    # size 16 != 32): on the CPU the device rule sends them to SDPA; neither the
+    # lengths nor the head sizes decide any more.
     query = torch.randn(1, 2, 3, 32)
     key = torch.randn(1, 2, 5, 32)
     value = torch.randn(1, 2, 5, 16)
     decision = explain_dispatch(query, key, value)
     assert decision.backend == "torch"
-    assert "equal query/key and value head sizes" in decision.reason
+    assert "CUDA tensor" in decision.reason
     actual = scaled_dot_product_attention(query, key, value)
     expected = torch.nn.functional.scaled_dot_product_attention(query, key, value)
     torch.testing.assert_close(actual, expected)
-    # Equal head sizes on the CPU: the device rule, not the lengths, decides.
-    value = torch.randn(1, 2, 5, 32)
+    # a value head size the kernels cannot hold is rejected before the device rule
+    value = torch.randn(1, 2, 5, 160)
     decision = explain_dispatch(query, key, value)
-    assert decision.backend == "torch" and "CUDA tensor" in decision.reason
+    assert decision.backend == "torch" and "equal query/key and value head sizes" in decision.reason
 
 
 # --- remaining validation and argument checks (ref attention.py:584-626, 806-815)
@@ -166,6 +167,12 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
     for D, Dv in ((64, 32), (32, 128), (128, 64)):
         d = attn._decide(_facts(head_dim=D, value_head_dim=Dv))
         assert d.backend == "triton" and f"zero-padded to {max(D, Dv)}" in d.reason
+    # Other head sizes up to 128 run zero-padded to the next kernel size (the
+    # reference sends every size but 32, 64, 128 to SDPA, attention.py:657-661).
+    for D, Dv, width in ((16, 16, 32), (40, 40, 64), (96, 96, 128), (80, 48, 128), (1, 33, 64)):
+        d = attn._decide(_facts(head_dim=D, value_head_dim=Dv))
+        assert d.backend == "triton" and f"zero-padded to {width}" in d.reason, (D, Dv)
+    assert "zero-padded" not in attn._decide(_facts()).reason
     # Cross-attention is served too (the reference sends it to SDPA, attention.py:639-642).
     for q_len, kv_len in ((128, 64), (3, 5000)):
         d = attn._decide(_facts(q_len=q_len, kv_len=kv_len))
@@ -176,13 +183,13 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
 @pytest.mark.parametrize(
     ("overrides", "reason"),
     [
-        (dict(value_head_dim=48), "equal query/key and value head sizes"),
-        (dict(value_head_dim=16, head_dim=32), "two different ones from (32, 64, 128)"),
-        (dict(head_dim=48, value_head_dim=64), "equal query/key and value head sizes"),
+        (dict(value_head_dim=160), "equal query/key and value head sizes"),
+        (dict(value_head_dim=16, head_dim=256), "two different ones of at most 128"),
         (dict(device_type="cpu"), "requires a CUDA tensor"),
         (dict(dtype=torch.float32), "supports float16 and bfloat16"),
         (dict(dtype=torch.float64), "supports float16 and bfloat16"),
-        (dict(head_dim=96, value_head_dim=96), "head_dim must be one of (32, 64, 128)"),
+        (dict(head_dim=160, value_head_dim=160), "head_dim must be one of (32, 64, 128)"),
+        (dict(head_dim=256, value_head_dim=256), "zero-padded to one of them"),
         (dict(q_len=1 << 24, kv_len=1 << 24), "too long"),
         (dict(q_len=1 << 24), "too long"),
         (dict(kv_len=1 << 24), "too long"),
@@ -199,9 +206,9 @@ def test_rule_fallback_reasons(overrides, reason) -> None:
 
 def test_rule_order_is_first_match() -> None:
     # value head size wins over everything, dtype wins over head_dim and arch
-    d = attn._decide(_facts(kv_len=3, value_head_dim=40, dtype=torch.float32, arch="gfx90a"))
+    d = attn._decide(_facts(kv_len=3, value_head_dim=200, dtype=torch.float32, arch="gfx90a"))
     assert "value head sizes" in d.reason
-    d = attn._decide(_facts(dtype=torch.float32, head_dim=48, value_head_dim=48, arch="gfx90a"))
+    d = attn._decide(_facts(dtype=torch.float32, head_dim=192, value_head_dim=192, arch="gfx90a"))
     assert "float16" in d.reason
 
 

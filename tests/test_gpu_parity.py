@@ -323,8 +323,10 @@ def test_dispatch_selects_custom_kernel_on_gfx950():
     assert decision.backend == "triton", decision.reason
     q32 = q.float()
     assert explain_dispatch(q32, q32, q32).backend == "torch"
+    q160 = torch.randn(1, 2, 64, 160, device=DEV, dtype=torch.float16)
+    assert explain_dispatch(q160, q160, q160).backend == "torch"
     q48 = torch.randn(1, 2, 64, 48, device=DEV, dtype=torch.float16)
-    assert explain_dispatch(q48, q48, q48).backend == "torch"
+    assert "zero-padded to 64" in explain_dispatch(q48, q48, q48).reason
     out = scaled_dot_product_attention(q32, q32, q32)  # auto falls back to SDPA
     ref = torch.nn.functional.scaled_dot_product_attention(q32, q32, q32)
     torch.testing.assert_close(out, ref)
@@ -556,25 +558,35 @@ def test_bf16_cross_attention_matches_oracle(head_dim):
 
 
 # ---------------------------------------------------------------------------
-# Value head size != query/key head size (the reference sends it to SDPA,
-# attention.py:643-646): served by zero-padding the narrower operands.
+# Head sizes other than the kernels' (the reference sends them to SDPA,
+# attention.py:643-646, 657-661): served by zero-padding to a kernel size.
 # ---------------------------------------------------------------------------
 VALUE_HEAD_CASES = [
-    # (B, Hq, Hkv, N_q, N_kv, D, D_v)
-    (1, 4, 2, 300, 300, 64, 32),
-    (2, 4, 4, 129, 257, 32, 128),
-    (1, 2, 1, 333, 97, 128, 64),
+    # (B, Hq, Hkv, N_q, N_kv, D, D_v, dtype): value head size != query/key head size
+    (1, 4, 2, 300, 300, 64, 32, torch.float16),
+    (2, 4, 4, 129, 257, 32, 128, torch.float16),
+    (1, 2, 1, 333, 97, 128, 64, torch.float16),
+    # head sizes between the kernel sizes, equal or not
+    (1, 4, 2, 200, 200, 16, 16, torch.float16),
+    (1, 2, 2, 150, 150, 40, 40, torch.float16),
+    (2, 4, 2, 129, 300, 80, 80, torch.float16),
+    (1, 4, 4, 257, 257, 96, 96, torch.float16),
+    (1, 2, 1, 100, 333, 112, 48, torch.float16),
+    (1, 2, 2, 64, 64, 8, 24, torch.float16),
+    (1, 4, 2, 190, 190, 96, 96, torch.bfloat16),
 ]
 
 
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("case", VALUE_HEAD_CASES,
-                         ids=lambda c: f"Nq{c[3]}Nkv{c[4]}-D{c[5]}Dv{c[6]}")
+                         ids=lambda c: f"Nq{c[3]}Nkv{c[4]}-D{c[5]}Dv{c[6]}-{str(c[7])[6:]}")
 def test_value_head_size_matches_oracle(case, causal):
-    B, Hq, Hkv, N, Nkv, D, Dv = case
-    tag = f"D_v B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} D_v={Dv} causal={causal}"
+    B, Hq, Hkv, N, Nkv, D, Dv, dtype = case
+    tag = (f"D_v B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} D_v={Dv} {dtype} "
+           f"causal={causal}")
     _note(tag)
-    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D + Dv, mult=0.5, n_kv=Nkv, d_v=Dv)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D + Dv, mult=0.5, n_kv=Nkv, d_v=Dv,
+                              dtype=dtype)
     qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
     gqa = Hq != Hkv
     decision = explain_dispatch(qd, kd, vd, enable_gqa=gqa)
@@ -584,15 +596,20 @@ def test_value_head_size_matches_oracle(case, causal):
     assert out.shape == (B, Hq, N, Dv) and out.is_contiguous()
     dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
     assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
-    width = max(D, Dv)
+    width = next(w for w in (32, 64, 128) if w >= max(D, Dv))
     pad = lambda t: torch.nn.functional.pad(t, (0, width - t.shape[-1])).to(DEV)
     _, lse = _ops.flash_fwd(pad(q), pad(k), pad(v), causal, D ** -0.5)
     torch.cuda.synchronize()
-    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal,
-                           o16=out.detach().cpu().numpy(), fold_bwd=True)
+    f = lambda t: t.float().numpy()
+    bf16 = dtype == torch.bfloat16
+    ref = oracle.attention(f(q), f(k), f(v), f(do), causal,
+                           o16=out.detach().float().cpu().numpy(),
+                           fold_bwd="bfloat16" if bf16 else True)
+    tols = dict(max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL) if bf16 else {}
     report = {}
     for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
-        report[name] = assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name])
+        assert t.dtype == dtype
+        report[name] = assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name], **tols)
     lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - ref["lse"])))
     assert lse_err <= LSE_TOL, f"{tag} lse: max-abs {lse_err:.3e}"
     _note(f"{tag}: " + ", ".join(f"{k}={v[0]:.2e}/{v[1]:.2e}" for k, v in report.items())

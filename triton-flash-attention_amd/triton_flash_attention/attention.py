@@ -8,12 +8,13 @@ through :mod:`._ops` instead of Triton kernels.
 
 Dispatch rules (first match wins; reference rules at attention.py:629-670):
   1. value head size != query head size     -> torch   (ref 643-646), unless both are
-     and not both supported                            supported head sizes (added)
+     and either is above 128                           at most 128 (added)
   2. not a GPU ("cuda") tensor              -> torch   (ref 647-648)
   3. dtype is not float16 or bfloat16       -> torch   (ref 653-656 accepts float16
                                                         only; bfloat16 is an added
                                                         dtype of the gfx950 kernels)
-  4. head_dim not in (32, 64, 128)          -> torch   (ref 657-661)
+  4. head_dim above 128                     -> torch   (ref 657-661 also rejects every
+                                                        size other than 32, 64, 128)
   5. sequence too long for 32-bit offsets   -> torch   (no reference counterpart)
   6. device is not gfx950                   -> torch   (replaces ref 662-666, SM >= 8)
   7. libfa_gfx950.so not loadable           -> torch   (replaces ref 649-652, the ROCm
@@ -23,10 +24,11 @@ Dispatch rules (first match wins; reference rules at attention.py:629-670):
 The reference's first rule, cross-attention (N_q != N_kv) -> torch (ref 639-642),
 is gone: the gfx950 kernels take separate query and key/value lengths and
 compute what that SDPA fallback does, top-left causal mask included (query i
-sees keys j <= i). A value head size other than the query/key one is served
-when both are supported sizes: :class:`TritonAttention` zero-pads the narrower
-operands to the wider size (zero columns add exact zeros to every dot product)
-and slices the results back.
+sees keys j <= i). Head sizes other than the kernels' 32, 64 and 128, and a
+value head size other than the query/key one, are served up to 128:
+:class:`TritonAttention` zero-pads the operands to the smallest kernel width
+that holds both sizes (zero columns add exact zeros to every dot product) and
+slices the results back.
 
 The backend keeps the reference's name "triton" so existing call sites
 (``backend="triton"``) run unchanged; it now means "the custom fused kernel".
@@ -46,7 +48,7 @@ import torch
 
 from . import _lib, _ops
 
-_SUPPORTED_HEAD_DIMS = (32, 64, 128)
+_SUPPORTED_HEAD_DIMS = (32, 64, 128)  # the kernels' widths; smaller sizes are zero-padded
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
 _SUPPORTED_ARCH = "gfx950"
 # Per-head slabs are addressed with 32-bit byte offsets (include/fa_gfx950.h).
@@ -136,17 +138,21 @@ class _DispatchFacts:
     library_error: str | None = None  # None when libfa_gfx950.so loaded
 
 
+def _kernel_width(head_dim: int, value_head_dim: int) -> int | None:
+    """The smallest kernel head size that holds both sizes, or None above 128."""
+    need = max(head_dim, value_head_dim)
+    return next((w for w in _SUPPORTED_HEAD_DIMS if w >= need), None)
+
+
 def _decide(facts: _DispatchFacts) -> DispatchDecision:
     """First-match dispatch rules (ref attention.py:639-670, module docstring)."""
     if facts.value_head_dim != facts.head_dim and (
-        facts.value_head_dim not in _SUPPORTED_HEAD_DIMS
-        or facts.head_dim not in _SUPPORTED_HEAD_DIMS
+        _kernel_width(facts.head_dim, facts.value_head_dim) is None
     ):
-        supported = ", ".join(str(dim) for dim in _SUPPORTED_HEAD_DIMS)
         return DispatchDecision(
             "torch",
             "the custom kernel requires equal query/key and value head sizes, or two "
-            f"different ones from ({supported})",
+            f"different ones of at most {_SUPPORTED_HEAD_DIMS[-1]}",
         )
     if facts.device_type != "cuda":
         return DispatchDecision("torch", "the Triton kernel requires a CUDA tensor")
@@ -154,12 +160,14 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         return DispatchDecision(
             "torch", "the custom mixed-precision path currently supports float16 and bfloat16"
         )
-    if facts.head_dim not in _SUPPORTED_HEAD_DIMS:
+    width = _kernel_width(facts.head_dim, facts.value_head_dim)
+    if width is None:
         supported = ", ".join(str(dim) for dim in _SUPPORTED_HEAD_DIMS)
         return DispatchDecision(
-            "torch", f"head_dim must be one of ({supported}) for the Triton path"
+            "torch",
+            f"head_dim must be one of ({supported}) for the Triton path, or a smaller size "
+            "that is zero-padded to one of them",
         )
-    width = max(facts.head_dim, facts.value_head_dim)
     if max(facts.q_len, facts.kv_len) * width * 2 > _MAX_SLAB_BYTES:
         return DispatchDecision(
             "torch", "the sequence is too long for the 32-bit addressed gfx950 kernel"
@@ -175,9 +183,10 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
         return DispatchDecision("torch", f"{_REASON_LIBRARY}: {facts.library_error}")
     kind = "self-attention" if facts.q_len == facts.kv_len else "cross-attention"
     padded = ""
-    if facts.value_head_dim != facts.head_dim:
-        padded = (f" (value head_dim {facts.value_head_dim} != {facts.head_dim}: the narrower "
-                  f"operands are zero-padded to {width})")
+    if (facts.head_dim, facts.value_head_dim) != (width, width):
+        sizes = (str(facts.head_dim) if facts.value_head_dim == facts.head_dim
+                 else f"{facts.head_dim} / value {facts.value_head_dim}")
+        padded = f" (head_dim {sizes}: zero-padded to {width})"
     return DispatchDecision(
         "triton",
         f"gfx950 {str(facts.dtype).removeprefix('torch.')} {kind} with a supported "
@@ -216,15 +225,21 @@ class TritonAttention(torch.autograd.Function):
     ``apply(query, key, value, causal, softmax_scale) -> output`` on contiguous
     fp16 or bf16 query [B, Hq, N, D], key [B, Hkv, N_kv, D] and value
     [B, Hkv, N_kv, D_v] tensors; backward returns ``(dQ, dK, dV, None, None)``.
-    With D_v != D the kernels run at width max(D, D_v) on zero-padded copies of
-    the narrower operands (and of dO), and the outputs are sliced back: zero
-    columns change no dot product, and their gradients are exactly zero.
+    Unless D and D_v are the same kernel size (32, 64 or 128), the kernels run
+    at the smallest kernel size that holds both, on zero-padded copies of the
+    operands (and of dO), and the outputs are sliced back: zero columns change
+    no dot product, and their gradients are exactly zero.
     """
 
     @staticmethod
     def forward(ctx, query, key, value, causal, softmax_scale):
         head_dim, value_head_dim = query.shape[-1], value.shape[-1]
-        width = max(head_dim, value_head_dim)
+        width = _kernel_width(head_dim, value_head_dim)
+        if width is None:
+            raise ValueError(
+                f"head sizes {head_dim} / {value_head_dim}: the gfx950 kernels serve at most "
+                f"{_SUPPORTED_HEAD_DIMS[-1]}"
+            )
         query, key, value = (_pad_head(t, width) for t in (query, key, value))
         output, lse = _ops.flash_fwd(query, key, value, bool(causal), float(softmax_scale))
         ctx.save_for_backward(query, key, value, output, lse)
@@ -283,8 +298,8 @@ def scaled_dot_product_attention(
 
     The custom gfx950 path supports forward/backward, causal and bidirectional
     attention, arbitrary positive sequence lengths, and GQA, for float16 or
-    bfloat16 self- or cross-attention with head_dim 32, 64 or 128 (the value
-    head_dim too, equal to it or not). Other inputs
+    bfloat16 self- or cross-attention with head_dim and value head_dim up to 128
+    (32, 64 and 128 natively, other sizes zero-padded). Other inputs
     fall back to PyTorch when ``backend="auto"``; ``backend="triton"`` requires
     the custom kernel and raises RuntimeError otherwise; ``backend="torch"``
     always uses PyTorch SDPA.
