@@ -20,6 +20,7 @@ N_kv != query length N), which the reference sends to torch SDPA
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -29,6 +30,13 @@ from . import _lib
 
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _device_guard(device: torch.device):
+    """Make ``device`` current for the launches (a no-op when it already is)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 class LaunchTimer:
@@ -151,7 +159,7 @@ def flash_fwd(
     fn, lengths = _entry_lengths(lib, "fa_fwd", dt, N, Nkv)
     o = torch.empty_like(q)
     lse = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
-    with torch.cuda.device(q.device):
+    with _device_guard(q.device):
         rc = _launch(
             "fwd", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
@@ -172,7 +180,7 @@ def flash_bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
     o, do = _aligned(o), _aligned(do)
     lib = _lib.load()
     delta = torch.empty((B, H, N), device=o.device, dtype=torch.float32)
-    with torch.cuda.device(o.device):
+    with _device_guard(o.device):
         rc = _launch("preprocess", _entry(lib, "fa_bwd_preprocess", dt),
                      o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, H, N, D, _stream(o))
     _lib.check(rc)
@@ -218,7 +226,7 @@ def flash_bwd_dkdv(
     if ws_bytes < 0:
         _lib.check(ws_bytes)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
-    with torch.cuda.device(q.device):
+    with _device_guard(q.device):
         rc = _launch(
             "dkdv", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
@@ -239,7 +247,7 @@ def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.T
     q, k, v, do, lse, delta = _aligned_all(q, k, v, do, lse, delta)
     lib = _lib.load()
     dq = torch.empty_like(q)
-    with torch.cuda.device(q.device):
+    with _device_guard(q.device):
         rc = _launch(
             "dq", _entry(lib, "fa_bwd_dq", q.dtype),
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
@@ -263,7 +271,7 @@ def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
     lib = _lib.load()
     fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", q.dtype, N, Nkv)
     dq = torch.empty_like(q)
-    with torch.cuda.device(q.device):
+    with _device_guard(q.device):
         rc = _launch(
             "dq", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
@@ -278,7 +286,48 @@ def flash_bwd(
     q, k, v, o, lse, do, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """dQ, dK, dV: dQ together with Delta (the reference's preprocess), then
-    dK/dV, which reads that Delta."""
-    delta, dq = flash_bwd_dq_delta(q, k, v, o, do, lse, causal, scale)
-    dk, dv = flash_bwd_dkdv(q, k, v, do, lse, delta, causal, scale)
+    dK/dV, which reads that Delta — what :func:`flash_bwd_dq_delta` followed by
+    :func:`flash_bwd_dkdv` do, with one pass of checks, allocations and stream
+    lookup for both launches (the host cost matters at small shapes)."""
+    dt = _elem_dtype(q, "q")
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("dO", do)):
+        _require(t, name, dt, q.device)
+    _require(lse, "lse", torch.float32, q.device)
+    B, Hq, Hkv, N, Nkv, D = _qkv_dims(q, k, v)
+    if o.shape != q.shape or do.shape != q.shape:
+        raise ValueError("o and dO must have the shape of q")
+    if lse.shape != (B, Hq, N):
+        raise ValueError("lse must have shape [B, Hq, N]")
+    q, k, v, o, do, lse = _aligned_all(q, k, v, o, do, lse)
+    lib = _lib.load()
+    dq_fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", dt, N, Nkv)
+    dkdv_fn, _ = _entry_lengths(lib, "fa_bwd_dkdv_ws", dt, N, Nkv)
+    c = int(bool(causal))
+    if N == Nkv:
+        ws_bytes = lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, c)
+    else:
+        ws_bytes = lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, Nkv, D, c)
+    if ws_bytes < 0:
+        _lib.check(ws_bytes)
+    delta = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
+    scale = float(scale)
+    with _device_guard(q.device):
+        stream = _stream(q)
+        _lib.check(_launch(
+            "dq", dq_fn,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+            lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+            B, Hq, Hkv, *lengths, D, scale, c, stream,
+        ))
+        _lib.check(_launch(
+            "dkdv", dkdv_fn,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
+            delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+            B, Hq, Hkv, *lengths, D, scale, c,
+            ws.data_ptr() if ws is not None else None, ws_bytes, stream,
+        ))
     return dq, dk, dv
