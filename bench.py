@@ -13,7 +13,10 @@ Prints ONE JSON line with the driver's fields plus
                 each launch on the launch stream) against the MFMA peak;
   cpu_baseline: the reference's CPU path (its public API on CPU tensors
                 dispatches to torch SDPA, attention.py:647-648 -> 774-786)
-                timed on this host over the same workload.
+                timed on this host over the same workload;
+  parity:       after the timed regions, the measured path's O, LSE, dQ, dK,
+                dV on the bench inputs against a plain PyTorch fp32 attention
+                on the GPU, with the north-star tolerances.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -55,6 +58,40 @@ def make_inputs(B, Hq, Hkv, N, D, seed, mult):
     g = torch.Generator("cpu").manual_seed(seed)
     shapes = ((B, Hq, N, D), (B, Hkv, N, D), (B, Hkv, N, D), (B, Hq, N, D))
     return [(torch.randn(s, generator=g, dtype=torch.float32) * mult).half() for s in shapes]
+
+
+def parity_check(q, k, v, do, causal: bool) -> dict:
+    """O, LSE, dQ, dK, dV of the measured path on the bench inputs against a
+    plain PyTorch fp32 attention on the GPU (explicit contiguous matmuls per
+    key/value head, tests/fa_testutil.py), at BASELINE.json's tolerances."""
+    import torch
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from fa_testutil import LSE_TOL, MAX_ABS_TOL, REL_L2_TOL, errors_torch, torch_reference_fp32
+    from triton_flash_attention import _ops, scaled_dot_product_attention
+
+    D = q.shape[-1]
+    q, k, v = q.detach(), k.detach(), v.detach()
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    out = scaled_dot_product_attention(qa, ka, va, is_causal=causal,
+                                       enable_gqa=q.shape[1] != k.shape[1], backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qa, ka, va), do)
+    _, lse = _ops.flash_fwd(q, k, v, causal, D ** -0.5)
+    ref = torch_reference_fp32(q, k, v, do, causal, o16=out.detach())
+    torch.cuda.synchronize()
+    result = {"reference": "plain PyTorch fp32 attention on the GPU, same fp16 inputs"}
+    ok = True
+    for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        ma, rl = errors_torch(t.float(), ref[name])
+        result[name] = {"max_abs": float(f"{ma:.3e}"), "rel_l2": float(f"{rl:.3e}")}
+        ok = ok and ma <= MAX_ABS_TOL and rl <= REL_L2_TOL
+    lse_err = float((lse - ref["lse"]).abs().max())
+    result["lse_max_abs"] = float(f"{lse_err:.3e}")
+    result["tolerance"] = {"max_abs": MAX_ABS_TOL, "rel_l2": REL_L2_TOL, "lse_max_abs": LSE_TOL}
+    result["pass"] = bool(ok and lse_err <= LSE_TOL)
+    del ref, out, dq, dk, dv, lse
+    torch.cuda.empty_cache()
+    return result
 
 
 def kernel_flops(kernel: str, B: int, Hq: int, N: int, D: int, causal: bool) -> int:
@@ -131,6 +168,8 @@ def main(argv=None) -> int:
                     help="c2 is the metric's configuration; the others are for exploration")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU-work budget of the CPU baseline (0 disables it)")
+    ap.add_argument("--no-parity", action="store_true",
+                    help="skip the parity check of the measured path after timing")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, copy a device buffer of this many MiB once (a "
                          "plain copy of known size that calibrates rocprofv3's "
@@ -259,6 +298,11 @@ def main(argv=None) -> int:
                          "(Triton path, RTX 5050 Laptop GPU, README.md:159)",
         "device": torch.cuda.get_device_name(),
     }
+
+    if not args.no_parity:
+        record["parity"] = parity_check(q, k, v, do, causal)
+        print(f"[bench] parity vs fp32 reference: {'pass' if record['parity']['pass'] else 'FAIL'}",
+              file=sys.stderr, flush=True)
 
     if args.calibrate_copy_mib > 0:
         src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device="cuda")
