@@ -667,3 +667,54 @@ def test_hip_graph_capture_replays_match_eager():
     for name, got, want, old in zip(names, captured, eager2, eager):
         assert torch.equal(got, want), f"replay on new inputs: {name} differs from eager"
         assert not torch.equal(got, old), f"replay on new inputs: {name} unchanged"
+
+
+# ---------------------------------------------------------------------------
+# Seeded random sweep over the envelope the GPU path serves
+# ---------------------------------------------------------------------------
+def _random_cases(count=24, seed=2024):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        Hkv = int(rng.choice([1, 2, 4]))
+        Hq = Hkv * int(rng.choice([1, 2, 3, 4]))
+        N = int(rng.integers(1, 400))
+        Nkv = N if rng.random() < 0.5 else int(rng.integers(1, 400))
+        D = int(rng.choice([16, 32, 48, 64, 96, 128]))
+        Dv = D if rng.random() < 0.7 else int(rng.choice([32, 64, 80, 128]))
+        cases.append(dict(
+            B=int(rng.choice([1, 2, 3])), Hq=Hq, Hkv=Hkv, N=N, Nkv=Nkv, D=D, Dv=Dv,
+            causal=bool(rng.random() < 0.5),
+            dtype=torch.bfloat16 if rng.random() < 0.25 else torch.float16,
+            scale=None if rng.random() < 0.6 else float(rng.uniform(0.05, 0.5)),
+            seed=seed + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(), ids=lambda c: f"seed{c['seed']}")
+def test_random_envelope_matches_oracle(case):
+    c = case
+    tag = (f"random seed={c['seed']} B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} N_q={c['N']} "
+           f"N_kv={c['Nkv']} D={c['D']} D_v={c['Dv']} causal={c['causal']} "
+           f"{str(c['dtype'])[6:]} scale={c['scale']}")
+    _note(tag)
+    q, k, v, do = make_inputs(c["B"], c["Hq"], c["Hkv"], c["N"], c["D"], seed=c["seed"], mult=0.5,
+                              dtype=c["dtype"], n_kv=c["Nkv"], d_v=c["Dv"])
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    gqa = c["Hq"] != c["Hkv"]
+    assert explain_dispatch(qd, kd, vd, enable_gqa=gqa).backend == "triton"
+    out = scaled_dot_product_attention(qd, kd, vd, is_causal=c["causal"], scale=c["scale"],
+                                       enable_gqa=gqa, backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
+    torch.cuda.synchronize()
+    f = lambda t: t.float().numpy()
+    bf16 = c["dtype"] == torch.bfloat16
+    ref = oracle.attention(f(q), f(k), f(v), f(do), c["causal"], c["scale"],
+                           o16=out.detach().float().cpu().numpy(),
+                           fold_bwd="bfloat16" if bf16 else True)
+    tols = dict(max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL) if bf16 else {}
+    for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert t.dtype == c["dtype"] and t.shape == {"o": (c["B"], c["Hq"], c["N"], c["Dv"]),
+                                                    "dq": q.shape, "dk": k.shape,
+                                                    "dv": v.shape}[name]
+        assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name], **tols)
