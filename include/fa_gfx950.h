@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 /* Error codes returned before any HIP call is made. */
 #define FA_OK 0
@@ -205,6 +205,33 @@ int fa_bwd_dq_delta_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_hal
                             float* delta, fa_half_t* dq,
                             int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
                             int64_t D, float scale, int causal, void* stream);
+
+/* Forward with split-KV for launches with few work-groups (decoding: a few
+ * queries against a long key sequence, or few heads): fa_fwd_kv's arguments
+ * plus a caller-provided device workspace. fa_fwd_workspace_bytes returns the
+ * bytes a call with these sizes needs (0 when it does not split, for either
+ * element type). With workspace == NULL, or when no split is needed, the call
+ * is fa_fwd_kv; a non-NULL workspace smaller than needed is rejected
+ * (FA_ERR_BAD_SHAPE). Splitting, the launch computes fp32 partial O and LSE
+ * per key range of at least 512 keys into the workspace and merges them
+ * (O = sum_s w_s O_s / sum_s w_s, w_s = exp2(lse_s - max lse), LSE = max +
+ * log2 sum w_s) in a second launch on the same stream; results agree with
+ * the unsplit forward up to fp32 summation order. No counterpart in the
+ * reference (its forward, attention.py:690-718, is one launch per
+ * (query tile, head)); it serves the cross-attention the library takes over
+ * from SDPA. The workspace is [nsplit, B, Hq, N_q, D + 1] fp32; concurrent
+ * calls need separate workspaces. */
+int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                               int64_t D, int causal);
+int fa_fwd_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+              fa_half_t* o, float* lse,
+              int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+              float scale, int causal, void* workspace, int64_t workspace_bytes, void* stream);
+int fa_fwd_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   fa_half_t* o, float* lse,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                   float scale, int causal, void* workspace, int64_t workspace_bytes,
+                   void* stream);
 
 /* Thread-local description of the last failure on the calling thread
  * ("" if none). The pointer stays valid until the next call on the thread. */

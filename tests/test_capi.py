@@ -225,3 +225,22 @@ def test_cross_attention_workspace_follows_the_key_length(lib):
     rc = lib.fa_bwd_dkdv_ws_kv(P, P, P, P, P, P, P, P, 1, 8, 2, 5000, 300, 64, 0.125, 1,
                                P, ws - 16, None)
     assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()
+
+
+def test_split_forward_workspace_sizing_and_rejection(lib):
+    # enough work-groups (the headline shape, or a long prompt): no split
+    assert lib.fa_fwd_workspace_bytes(4, 16, 16, 4096, 4096, 64, 1) == 0
+    assert lib.fa_fwd_workspace_bytes(1, 32, 8, 4096, 4096, 128, 1) == 0
+    # too few keys to split
+    assert lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 700, 128, 0) == 0
+    # decoding: one query against 32768 keys, 32 heads -> split, [nsplit, B, Hq, N_q, D + 1] fp32
+    ws = lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 32768, 128, 0)
+    per_split = 1 * 32 * 1 * (128 + 1) * 4
+    assert ws > 0 and ws % per_split == 0 and 2 <= ws // per_split <= 64
+    assert lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 32768, 96, 0) == _lib.FA_ERR_HEAD_DIM
+    assert lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 0, 128, 0) == _lib.FA_ERR_BAD_SHAPE
+    # a workspace smaller than required is rejected before any launch
+    rc = lib.fa_fwd_ws(P, P, P, P, P, 1, 32, 8, 1, 32768, 128, 0.09, 0, P, ws - 16, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()
+    rc = lib.fa_fwd_ws_bf16(P, P, P, P, P, 1, 32, 8, 1, 32768, 128, 0.09, 0, P + 8, ws, None)
+    assert rc == _lib.FA_ERR_MISALIGNED

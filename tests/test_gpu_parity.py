@@ -718,3 +718,52 @@ def test_random_envelope_matches_oracle(case):
                                                     "dq": q.shape, "dk": k.shape,
                                                     "dv": v.shape}[name]
         assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name], **tols)
+
+
+# ---------------------------------------------------------------------------
+# Split-KV forward (few work-groups: decoding, few heads)
+# ---------------------------------------------------------------------------
+SPLIT_FWD_CASES = [
+    # (B, Hq, Hkv, N_q, N_kv, D, causal, dtype)
+    (1, 32, 8, 1, 4000, 128, False, torch.float16),   # decoding, GQA
+    (2, 4, 2, 16, 3000, 64, False, torch.float16),
+    (2, 4, 2, 16, 3000, 64, True, torch.float16),     # top-left causal: most splits empty
+    (1, 2, 2, 2048, 2048, 32, True, torch.float16),   # self-attention with few heads
+    (1, 3, 1, 77, 5000, 64, False, torch.bfloat16),
+    (1, 4, 4, 5, 1537, 128, True, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_FWD_CASES,
+                         ids=lambda c: f"Nq{c[3]}Nkv{c[4]}D{c[5]}{'c' if c[6] else 'b'}-{str(c[7])[6:]}")
+def test_split_forward_matches_unsplit_and_oracle(case):
+    """The split-KV forward (fa_fwd_ws, chosen by the op layer when the
+    workspace query asks for it) agrees with the one-pass forward (fa_fwd_kv,
+    no workspace) up to fp32 summation order, and with the oracle."""
+    B, Hq, Hkv, N, Nkv, D, causal, dtype = case
+    tag = f"split fwd B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} causal={causal} {dtype}"
+    _note(tag)
+    lib = _lib.load()
+    ws = lib.fa_fwd_workspace_bytes(B, Hq, Hkv, N, Nkv, D, int(causal))
+    assert ws > 0, "the case must take the split path"
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D, n_kv=Nkv, dtype=dtype)
+    qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+    scale = D ** -0.5
+    o_split, lse_split = _ops.flash_fwd(qd, kd, vd, causal, scale)  # takes the split path
+    o_one, lse_one = torch.empty_like(qd), torch.empty_like(lse_split)
+    bf16 = dtype == torch.bfloat16
+    fn = lib.fa_fwd_kv_bf16 if bf16 else lib.fa_fwd_kv
+    _lib.check(fn(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), o_one.data_ptr(), lse_one.data_ptr(),
+                  B, Hq, Hkv, N, Nkv, D, scale, int(causal), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.isfinite(o_split.float()).all() and torch.isfinite(lse_split).all()
+    assert_close(f"{tag} o split vs one pass", o_split.float(), o_one.float(),
+                 max_abs=4e-3 if not bf16 else 3e-2, rel_l2=1e-3 if not bf16 else 8e-3)
+    assert float((lse_split - lse_one).abs().max()) <= 1e-5, tag
+    f = lambda t: t.float().numpy()
+    o_ref, lse_ref = oracle.fwd(f(q), f(k), f(v), causal, scale)
+    tols = dict(max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL) if bf16 else {}
+    assert_close(f"{tag} o", o_split.double().cpu().numpy(), o_ref, **tols)
+    lse_err = float(np.max(np.abs(lse_split.double().cpu().numpy() - lse_ref)))
+    assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"
+    _note(f"{tag}: lse err {lse_err:.2e}, workspace {ws} bytes")

@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <initializer_list>
 
 #include "../../include/fa_gfx950.h"
@@ -192,6 +193,36 @@ int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, i
   return nsplit > 1 ? (int64_t)nsplit * 2 * B * Hkv * Nkv * D * 4 : 0;
 }
 
+// Forward split-KV factor: launches with few work-groups (decoding: a few
+// queries against a long key sequence, or few heads) split each work-group's
+// keys into up to 64 ranges of at least 512 keys (multiples of 128), run as
+// separate work-groups, then merged (launch_fwd_combine).
+constexpr int64_t kFwdSplitBelowWorkgroups = 512;
+constexpr int64_t kFwdSplitTargetWorkgroups = 1024;
+constexpr int64_t kFwdMinSplitKeys = 512;
+constexpr int kMaxFwdSplit = 64;
+
+struct FwdSplit {
+  int nsplit;
+  int split_keys;
+};
+
+FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv) {
+  const int64_t wgs = (N + var.rows - 1) / var.rows * B * Hq;
+  const int whole = (int)((Nkv + 127) / 128 * 128);
+  if (wgs >= kFwdSplitBelowWorkgroups || !(var.flags & fa::kSplitsKv)) return {1, whole};
+  int64_t s = (kFwdSplitTargetWorkgroups + wgs - 1) / wgs;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, Nkv / kFwdMinSplitKeys));
+  s = std::min<int64_t>(s, kMaxFwdSplit);
+  if (s <= 1) return {1, whole};
+  const int64_t keys = ((Nkv + s - 1) / s + 127) / 128 * 128;
+  return {(int)((Nkv + keys - 1) / keys), (int)keys};
+}
+
+int64_t fwd_workspace_bytes(const FwdSplit& sp, int64_t B, int64_t Hq, int64_t N, int64_t D) {
+  return sp.nsplit > 1 ? (int64_t)sp.nsplit * B * Hq * N * (D + 1) * 4 : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -202,7 +233,8 @@ const char* fa_last_error(void) { return g_last_error; }
 
 static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
                     const fa_half_t* v, fa_half_t* o, float* lse, int64_t B, int64_t Hq,
-                    int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal, void* stream) {
+                    int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
+                    void* stream, void* workspace = nullptr, int64_t workspace_bytes = 0) {
   if (!q || !k || !v || !o || !lse) return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
@@ -226,7 +258,39 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   a.num_tiles = 0;
   a.c = scale * fa::kLog2e;
   auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
-  return launch_result(fn(a, static_cast<hipStream_t>(stream)), name);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv);
+  const int64_t need = fwd_workspace_bytes(sp, B, Hq, N, D);
+  a.nsplit = 1;
+  a.split_keys = (int)((Nkv + 127) / 128 * 128);
+  a.part = nullptr;
+  if (need == 0 || workspace == nullptr) return launch_result(fn(a, s), name);
+  if (workspace_bytes < need)
+    return fail(FA_ERR_BAD_SHAPE, "%s: workspace of %lld bytes is smaller than the %lld bytes "
+                "fa_fwd_workspace_bytes reports", name, (long long)workspace_bytes, (long long)need);
+  if ((rc = check_aligned(name, {workspace}))) return rc;
+  a.nsplit = sp.nsplit;
+  a.split_keys = sp.split_keys;
+  a.part = static_cast<float*>(workspace);
+  hipError_t e = fn(a, s);
+  if (e != hipSuccess) return launch_result(e, name);
+  return launch_result(fa::launch_fwd_combine(a.part, a.o, lse, B * Hq * N, (int)D, sp.nsplit, dt, s),
+                       name);
+}
+
+int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                               int64_t D, int causal) {
+  int rc = check_common(B, Hq, Hkv, N_q, D);
+  if (rc) return rc;
+  if ((rc = check_kv_length(N_kv, D))) return rc;
+  // Enough for either element type (their tilings can differ when overridden).
+  int64_t bytes = 0;
+  for (int dt : {fa::kF16, fa::kBF16}) {
+    const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
+    if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_workspace_bytes: no kernel for the selected tiling");
+    bytes = std::max(bytes, fwd_workspace_bytes(fwd_split(*var, B, Hq, N_q, N_kv), B, Hq, N_q, D));
+  }
+  return bytes;
 }
 
 static int preprocess_impl(int dt, const char* name, const fa_half_t* o, const fa_half_t* dO,
@@ -440,6 +504,21 @@ int fa_bwd_dq_delta_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t
                          float scale, int causal, void* stream) {
   return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_bf16", q, k, v, o, dO, lse, delta, dq, B, Hq,
                        Hkv, N, N, D, scale, causal, stream);
+}
+
+int fa_fwd_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
+              float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+              int64_t D, float scale, int causal, void* workspace, int64_t workspace_bytes,
+              void* stream) {
+  return fwd_impl(fa::kF16, "fa_fwd_ws", q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale, causal,
+                  stream, workspace, workspace_bytes);
+}
+int fa_fwd_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
+                   float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                   int64_t D, float scale, int causal, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
+  return fwd_impl(fa::kBF16, "fa_fwd_ws_bf16", q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale,
+                  causal, stream, workspace, workspace_bytes);
 }
 
 // ---- exported launches with separate query and key/value lengths --------

@@ -57,9 +57,58 @@ constexpr float kSumLimit = 256.0f;
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// Epilogue, lane (query qrow, half g) holding d = 32*db + 8*(j/4) + 4*g + j%4
+// of O (unnormalised), the reference max m and the row sum lt:
+//   unsplit: O / lt as 16-bit through the range-checked resource ro, and the
+//            base-2 LSE m + log2(lt);
+//   split:   the fp32 partial O / lt and LSE of split `split` (a query that
+//            saw no key of the split, lt == 0, writes O = 0 and LSE = -inf,
+//            which the combine weighs with 0).
+template <int D, class E, bool SPLITS = true>
+__device__ __forceinline__ void store_fwd_output(const FwdArgs& a, const rsrc_t& ro, int split,
+                                                 int head, int qrow, int g,
+                                                 const float16v (&o)[D / 32], float m, float lt) {
+  const bool split_mode = SPLITS && a.nsplit > 1;
+  const bool seen = lt > 0.f;
+  const float inv = seen ? 1.0f / lt : 0.f;
+  // The lane's half is recomputed here (mbcnt needs no live register), so
+  // no lane value has to stay live, and spill, across the main loop.
+  g = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 5);
+  const int64_t prow = ((int64_t)split * a.BH + head) * a.N + qrow;
+  float* po = a.part + prow * D;
+  const bool row_ok = qrow < a.N;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      float4v v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = o[db][4 * jq + e] * inv;
+      if (split_mode) {
+        if (row_ok) *reinterpret_cast<float4v*>(po + 32 * db + 8 * jq + 4 * g) = v;
+      } else {
+        buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u,
+                      pack4<E>(v[0], v[1], v[2], v[3]));
+      }
+    }
+  if (g == 0 && row_ok) {
+    const float lse = seen ? m + log2_fast(lt) : -INFINITY;
+    if (split_mode) a.part[(int64_t)a.nsplit * a.BH * a.N * D + prow] = lse;
+    else a.lse[(int64_t)head * a.N + qrow] = lse;
+  }
+}
+
+// Split-KV is compiled for key tiles of at most 64 (the 128-key tiling is a
+// sweep variant whose register allocation the split epilogue upsets).
+template <int BN>
+constexpr bool fwd_tile_splits_kv() {
+  return BN <= 64;
+}
+
 template <int D, bool CAUSAL, int NW, int BN, class E = F16>
 __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, NW, BN>;
+  constexpr bool kSplits = fwd_tile_splits_kv<BN>();
   using Dma = DmaStager<D, BN, NW>;
   constexpr int KB = BN / 32;                 // 32-key blocks per tile
   constexpr int IPT = 2 * Dma::PER_WAVE;      // this wave's DMA instructions per tile
@@ -71,7 +120,9 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  const TileHead th = decode_block(blockIdx.x, a.BH);
+  // Split-KV mode: the split index is the slowest-varying part of the block index.
+  const int split = kSplits ? blockIdx.x / (a.num_tiles * a.BH) : 0;
+  const TileHead th = decode_block(blockIdx.x - split * a.num_tiles * a.BH, a.BH);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
@@ -91,7 +142,10 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   const int qrow = q0w + ql;
 
   const int kv_end = CAUSAL ? min(Nkv, q0 + T::BM) : Nkv;
-  const int ntiles = (kv_end + BN - 1) / BN;
+  // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
+  const int kv_lo = kSplits ? split * a.split_keys : 0;
+  const int kv_hi = kSplits ? min(kv_end, kv_lo + a.split_keys) : kv_end;
+  const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + BN - 1) / BN : 0;
 
   // Q^T operand fragments: lane (query ql, k-half g), d = 16*kk + 8*g .. +7.
   // Completed before the first DMA so no later wait on them drains the ring.
@@ -108,8 +162,8 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   dma.init(wave, lane);
   auto issue_tile = [&](int t, int slot) {
     const half_t* base = lds + slot * T::STAGE;
-    dma.issue(rk, t * BN, base, wave);
-    dma.issue(rv, t * BN, base + T::TILE, wave);
+    dma.issue(rk, kv_lo + t * BN, base, wave);
+    dma.issue(rv, kv_lo + t * BN, base + T::TILE, wave);
   };
 #pragma unroll
   for (int t = 0; t < T::AHEAD; ++t) issue_tile(t, t);
@@ -145,7 +199,9 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
   // A wave takes part in tile t unless all its queries are past the end or,
   // causally, before every key of the tile (wave-uniform).
-  auto active = [&](int t) { return uniform((q0w < N) && !(CAUSAL && t * BN > q0w + 31)) != 0; };
+  auto active = [&](int t) {
+    return uniform((q0w < N) && !(CAUSAL && kv_lo + t * BN > q0w + 31)) != 0;
+  };
 
   float16v sbuf[2][KB];  // S^T of two consecutive tiles (software pipeline)
 
@@ -174,7 +230,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
     constexpr int SLOT = decltype(slot_c)::value;
     constexpr int SB = decltype(sb_c)::value;
     const int t = uniform(t_in);
-    const int kv0 = t * BN;
+    const int kv0 = kv_lo + t * BN;
     // (1) tile t+AHEAD -> the slot tile t-1 used (released by the last barrier).
     issue_tile(t + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
     const bool act = active(t);
@@ -205,14 +261,14 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
     if (act) {
       float16v* sc = sbuf[SB];
-      const bool need_mask = uniform((CAUSAL && kv0 + BN - 1 > q0w) || (kv0 + BN > Nkv)) != 0;
+      const bool need_mask = uniform((CAUSAL && kv0 + BN - 1 > q0w) || (kv0 + BN > kv_hi)) != 0;
       if (need_mask) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int key = kv0 + 32 * kb + result_row(j, g);
-            const bool ok = key < Nkv && (!CAUSAL || key <= qrow);
+            const bool ok = key < kv_hi && (!CAUSAL || key <= qrow);
             if (!ok) sc[kb][j] = -INFINITY;
           }
       }
@@ -252,7 +308,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int key = kv0 + 32 * kb + result_row(j, g);
-            if (need_mask && (key >= Nkv || (CAUSAL && key > qrow))) s2[kb][j] = -INFINITY;
+            if (need_mask && (key >= kv_hi || (CAUSAL && key > qrow))) s2[kb][j] = -INFINITY;
             mx = fmaxf(mx, s2[kb][j]);
           }
         mx = halves_max(mx) * c;
@@ -280,7 +336,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
   // Tiles 0 and 1 complete and visible.
   wait_vm_and_barrier<(T::AHEAD - 2) * IPT>();
-  if (active(0)) scores(ic<0>{}, ic<0>{});
+  if (ntiles > 0 && active(0)) scores(ic<0>{}, ic<0>{});
 
   for (int t = 0; t < ntiles; t += T::UNROLL) {
     step(ic<0>{}, ic<0>{}, t);
@@ -296,16 +352,7 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
   // Epilogue: lane (query qrow, half g) holds d = 32*db + 8*(j/4) + 4*g + j%4.
   const float lt = halves_sum(l);
-  const float inv = 1.0f / lt;
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const u32x2 v = pack4<E>(o[db][4 * jq] * inv, o[db][4 * jq + 1] * inv,
-                                 o[db][4 * jq + 2] * inv, o[db][4 * jq + 3] * inv);
-      buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u, v);
-    }
-  if (g == 0 && qrow < N) a.lse[(int64_t)head * N + qrow] = m + log2_fast(lt);
+  store_fwd_output<D, E, kSplits>(a, ro, split, head, qrow, g, o, m, lt);
 }
 
 // ---------------------------------------------------------------------------
@@ -386,7 +433,9 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  const TileHead th = decode_block(blockIdx.x, a.BH);
+  // Split-KV mode: the split index is the slowest-varying part of the block index.
+  const int split = blockIdx.x / (a.num_tiles * a.BH);
+  const TileHead th = decode_block(blockIdx.x - split * a.num_tiles * a.BH, a.BH);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
@@ -413,15 +462,18 @@ void fwd_pipe_kernel(FwdArgs a) {
   wait_all_vm();
 
   const int kv_end = CAUSAL ? min(Nkv, q0 + T::BM) : Nkv;
-  const int nunits = (kv_end + T::KT - 1) / T::KT;
+  // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
+  const int kv_lo = split * a.split_keys;
+  const int kv_hi = min(kv_end, kv_lo + a.split_keys);
+  const int nunits = kv_hi > kv_lo ? (kv_hi - kv_lo + T::KT - 1) / T::KT : 0;
   const int npad = (nunits + NS - 1) / NS * NS;
 
   Dma dma;
   dma.init(wave, lane);
   const uint32_t lds0 = lds_addr(lds);
-  int i_row = 0;  // first key row of the next unit to fetch
+  int i_row = kv_lo;  // first key row of the next unit to fetch
   auto issue = [&](int slot) {
-    const int row0 = i_row < kv_end ? i_row : Nkv;  // past the end: zeros
+    const int row0 = i_row < kv_hi ? i_row : Nkv;  // past the range: zeros
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;
@@ -510,7 +562,7 @@ void fwd_pipe_kernel(FwdArgs a) {
         o[db] = mma<E>(tr8(slot + T::TILE + 16 * h * D, db), pa_prev[h], o[db]);
   };
 
-  int c_key = 0;  // first key of the unit the body works on
+  int c_key = kv_lo;  // first key of the unit the body works on
 
   auto body = [&](auto slot_c) {
     constexpr int SLOT = decltype(slot_c)::value;
@@ -521,13 +573,13 @@ void fwd_pipe_kernel(FwdArgs a) {
 
     // Unit modes (wave-uniform): keys all past the queries (or past N), or
     // a diagonal / tail unit whose masked scores become -inf.
-    const bool dead = (CAUSAL && ka > q0w) || ka >= Nkv;
+    const bool dead = (CAUSAL && ka > q0w) || ka >= kv_hi;
     float m_eff = dead ? inf : m;
-    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > Nkv)) {
+    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > kv_hi)) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int key = ka + result_row(j, g);
-        if (key >= Nkv || (CAUSAL && key > qrow)) s_cur[j] = -inf;
+        if (key >= kv_hi || (CAUSAL && key > qrow)) s_cur[j] = -inf;
       }
     }
 
@@ -649,16 +701,7 @@ void fwd_pipe_kernel(FwdArgs a) {
 
   // Epilogue: lane (query qrow, half g) holds d = 32*db + 8*(j/4) + 4*g + j%4.
   const float lt = halves_sum(l);
-  const float invl = 1.0f / lt;
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const u32x2 v = pack4<E>(o[db][4 * jq] * invl, o[db][4 * jq + 1] * invl,
-                                 o[db][4 * jq + 2] * invl, o[db][4 * jq + 3] * invl);
-      buf_store_b64(ro, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u, v);
-    }
-  if (g == 0 && qrow < N) a.lse[(int64_t)head * N + qrow] = m + log2_fast(lt);
+  store_fwd_output<D, E>(a, ro, split, head, qrow, g, o, m, lt);
 }
 
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
@@ -666,7 +709,10 @@ hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdPipeTile<D, NW, UPS>;
   FwdArgs b = a;
   b.num_tiles = (a.N + T::BM - 1) / T::BM;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BH;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
+      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS, E>), dim3((unsigned)blocks), dim3(T::NT),
                      0, stream, b);
@@ -686,11 +732,71 @@ hipError_t fwd_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdTile<D, NW, BN>;
   FwdArgs b = a;
   b.num_tiles = (a.N + T::BM - 1) / T::BM;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BH;
+  if (b.nsplit < 1 || (b.nsplit > 1 && (b.part == nullptr || !fwd_tile_splits_kv<BN>())) ||
+      b.split_keys % 128 != 0 || (int64_t)b.nsplit * b.split_keys < a.Nkv)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, NW, BN, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
   return hipGetLastError();
+}
+
+// Merge of the split-KV partials: one thread per 4 columns of a query row.
+template <int D, class E>
+__global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restrict__ part,
+                                                          half_t* __restrict__ o,
+                                                          float* __restrict__ lse, int64_t rows,
+                                                          int nsplit) {
+  constexpr int CPR = D / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * CPR) return;
+  const int64_t row = i / CPR;
+  const int c = (int)(i - row * CPR);
+  const float* plse = part + (int64_t)nsplit * rows * D;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, plse[(int64_t)sp * rows + row]);
+  float wsum = 0.f;
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float ls = plse[(int64_t)sp * rows + row];
+    const float w = ls == -INFINITY ? 0.f : exp2_fast(ls - mx);
+    wsum += w;
+    const float4v v =
+        *reinterpret_cast<const float4v*>(part + ((int64_t)sp * rows + row) * D + 4 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = fmaf(w, v[e], acc[e]);
+  }
+  const float inv = 1.0f / wsum;
+  half4 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) h[e] = to_elem<E>(acc[e] * inv);
+  *reinterpret_cast<half4*>(o + row * D + 4 * c) = h;
+  if (c == 0) lse[row] = mx + log2_fast(wsum);
+}
+
+template <int D, class E>
+hipError_t fwd_combine_launch(const float* part, half_t* o, float* lse, int64_t rows, int nsplit,
+                              hipStream_t stream) {
+  const int64_t blocks = (rows * (D / 4) + 255) / 256;
+  if (nsplit < 2 || blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((fwd_combine_kernel<D, E>), dim3((unsigned)blocks), dim3(256), 0, stream,
+                     part, o, lse, rows, nsplit);
+  return hipGetLastError();
+}
+
+hipError_t launch_fwd_combine(const float* part, half_t* o, float* lse, int64_t rows, int D,
+                              int nsplit, int dtype, hipStream_t stream) {
+  const bool bf = dtype == kBF16;
+  switch (D) {
+    case 32: return bf ? fwd_combine_launch<32, BF16>(part, o, lse, rows, nsplit, stream)
+                       : fwd_combine_launch<32, F16>(part, o, lse, rows, nsplit, stream);
+    case 64: return bf ? fwd_combine_launch<64, BF16>(part, o, lse, rows, nsplit, stream)
+                       : fwd_combine_launch<64, F16>(part, o, lse, rows, nsplit, stream);
+    case 128: return bf ? fwd_combine_launch<128, BF16>(part, o, lse, rows, nsplit, stream)
+                        : fwd_combine_launch<128, F16>(part, o, lse, rows, nsplit, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 // A tiling is compiled for a head_dim only if its K/V tiles split into whole
@@ -711,10 +817,12 @@ constexpr void* fwd_entry() {
 
 // FA_FWD_VARIANT_BF also compiles the tiling for bf16; bf16 is compiled only
 // for the tilings the default table uses, to bound the build.
-#define FA_FWD_VARIANT(NW, BN) \
-  {NW, 32 * NW, BN, {FA_ENTRIES(fwd_entry, F16, NW, BN), FA_NO_ENTRIES}, 0}
-#define FA_FWD_VARIANT_BF(NW, BN) \
-  {NW, 32 * NW, BN, {FA_ENTRIES(fwd_entry, F16, NW, BN), FA_ENTRIES(fwd_entry, BF16, NW, BN)}, 0}
+#define FA_FWD_VARIANT(NW, BN)                                        \
+  {NW, 32 * NW, BN, {FA_ENTRIES(fwd_entry, F16, NW, BN), FA_NO_ENTRIES}, \
+   fwd_tile_splits_kv<BN>() ? kSplitsKv : 0}
+#define FA_FWD_VARIANT_BF(NW, BN)                                                          \
+  {NW, 32 * NW, BN, {FA_ENTRIES(fwd_entry, F16, NW, BN), FA_ENTRIES(fwd_entry, BF16, NW, BN)}, \
+   fwd_tile_splits_kv<BN>() ? kSplitsKv : 0}
 
 static const Variant kFwdVariants[] = {
     FA_FWD_VARIANT(4, 64),
@@ -722,8 +830,9 @@ static const Variant kFwdVariants[] = {
     FA_FWD_VARIANT_BF(4, 32),
     FA_FWD_VARIANT(2, 64),
     FA_FWD_VARIANT(4, 128),
-    {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 2), FA_NO_ENTRIES}, 0},
-    {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe_entry, BF16, 4, 1)}, 0},
+    {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 2), FA_NO_ENTRIES}, kSplitsKv},
+    {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe_entry, BF16, 4, 1)},
+     kSplitsKv},
 };
 
 const Variant* fwd_variants(int* count) {

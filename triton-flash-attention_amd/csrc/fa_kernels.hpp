@@ -27,6 +27,14 @@ struct FwdArgs {
   int BH;          // B * Hq
   int num_tiles;   // filled in by the launcher
   float c;         // scale * log2(e)
+  // Split-KV mode (nsplit > 1): work-group split s covers keys
+  // [s * split_keys, (s + 1) * split_keys) and writes its fp32 partial O
+  // ([nsplit, BH, N, D], normalised by its own row sums) and base-2 LSE
+  // ([nsplit, BH, N], -inf where it saw no key) to `part`;
+  // launch_fwd_combine merges them. nsplit = 1: split_keys >= Nkv, part unused.
+  int nsplit;
+  int split_keys;  // a multiple of 128
+  float* part;
 };
 
 // Arguments of the backward launches (attention.py:736-770).
@@ -73,7 +81,7 @@ struct Variant {
   int rows;
   int tile;
   void* fn[2][3][2];  // [element type: fp16, bf16][D index: 32, 64, 128][causal]; null = not compiled
-  int flags;          // kFusesDelta
+  int flags;          // kFusesDelta, kSplitsKv
 };
 
 // Element type index of Variant::fn.
@@ -89,6 +97,8 @@ enum DType { kF16 = 0, kBF16 = 1 };
 
 // The dQ variant can compute Delta itself (BwdArgs::o / delta_out).
 constexpr int kFusesDelta = 1;
+// The forward variant has the split-KV mode (FwdArgs::nsplit > 1).
+constexpr int kSplitsKv = 2;
 
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);
@@ -102,6 +112,12 @@ hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_
 
 hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
                              int D, int dtype, hipStream_t stream);
+
+// Merge of the forward's nsplit partials (FwdArgs::part) into O (16-bit) and
+// base-2 LSE, rows = B * Hq * N: O = sum_s w_s O_s / sum_s w_s with
+// w_s = exp2(lse_s - max_s lse_s), LSE = max + log2(sum_s w_s).
+hipError_t launch_fwd_combine(const float* part, half_t* o, float* lse, int64_t rows, int D,
+                              int nsplit, int dtype, hipStream_t stream);
 
 inline int head_dim_index(int64_t D) {
   return D == 32 ? 0 : D == 64 ? 1 : D == 128 ? 2 : -1;

@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 FA_OK = 0
 FA_ERR_NULL_POINTER = -1
@@ -75,6 +75,10 @@ for _name, _n_ptr in (("fa_fwd", 5), ("fa_bwd_dkdv_ws", 8), ("fa_bwd_dq_delta", 
     SIGNATURES[_name + "_kv"] = _kv
     SIGNATURES[_name + "_kv_bf16"] = _kv
 del _name, _n_ptr, _res, _args, _kv
+# Forward with a split-KV workspace: fa_fwd_kv's arguments, then workspace, its size, stream.
+SIGNATURES["fa_fwd_workspace_bytes"] = (_I64, (_I64, _I64, _I64, _I64, _I64, _I64, _INT))
+SIGNATURES["fa_fwd_ws"] = (_INT, SIGNATURES["fa_fwd_kv"][1][:-1] + (_P, _I64, _P))
+SIGNATURES["fa_fwd_ws_bf16"] = SIGNATURES["fa_fwd_ws"]
 
 
 class FlashAttentionError(RuntimeError):

@@ -149,22 +149,37 @@ def _qkv_dims(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> tuple[int, .
 def flash_fwd(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """O [B,Hq,N,D] (the inputs' fp16 or bf16) and base-2 LSE [B,Hq,N] fp32."""
+    """O [B,Hq,N,D] (the inputs' fp16 or bf16) and base-2 LSE [B,Hq,N] fp32.
+
+    Launches with few work-groups (decoding, few heads) get a workspace from
+    the caching allocator for the library's split-KV mode."""
     dt = _elem_dtype(q, "q")
     for name, t in (("q", q), ("k", k), ("v", v)):
         _require(t, name, dt, q.device)
     B, Hq, Hkv, N, Nkv, D = _qkv_dims(q, k, v)
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     lib = _lib.load()
-    fn, lengths = _entry_lengths(lib, "fa_fwd", dt, N, Nkv)
+    c = int(bool(causal))
+    ws_bytes = lib.fa_fwd_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c)
+    if ws_bytes < 0:
+        _lib.check(ws_bytes)
     o = torch.empty_like(q)
     lse = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
     with _device_guard(q.device):
-        rc = _launch(
-            "fwd", fn,
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-            B, Hq, Hkv, *lengths, D, float(scale), int(bool(causal)), _stream(q),
-        )
+        if ws_bytes > 0:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+            rc = _launch(
+                "fwd", _entry(lib, "fa_fwd_ws", dt),
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                B, Hq, Hkv, N, Nkv, D, float(scale), c, ws.data_ptr(), ws_bytes, _stream(q),
+            )
+        else:
+            fn, lengths = _entry_lengths(lib, "fa_fwd", dt, N, Nkv)
+            rc = _launch(
+                "fwd", fn,
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                B, Hq, Hkv, *lengths, D, float(scale), c, _stream(q),
+            )
     _lib.check(rc)
     return o, lse
 
