@@ -994,7 +994,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  const TileHead th = decode_block(blockIdx.x, a.BH);
+  const TileHead th = decode_block_grouped(blockIdx.x, a.BH, a.group);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
@@ -1236,7 +1236,7 @@ void dq_pipe_kernel(BwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  const TileHead th = decode_block(blockIdx.x, a.BH);
+  const TileHead th = decode_block_grouped(blockIdx.x, a.BH, a.group);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;

@@ -439,4 +439,17 @@ __device__ __forceinline__ TileHead decode_block(int block, int heads) {
   return t;
 }
 
+// The same order for query-head launches (forward, dQ) with GQA groups: when
+// the B * Hkv key/value heads are a multiple of 8, position p of a tile row
+// takes query head (p % BHkv) * group + p / BHkv, so every query head of key/
+// value head j (and each of its tiles and key splits) lands on XCD j % 8 and
+// the group reads its K/V through one L2. A bijection on [0, heads); the
+// identity for MHA or other head counts.
+__device__ __forceinline__ TileHead decode_block_grouped(int block, int heads, int group) {
+  TileHead t = decode_block(block, heads);
+  const int bhkv = heads / group;
+  if (group > 1 && bhkv % 8 == 0) t.head = (t.head % bhkv) * group + t.head / bhkv;
+  return t;
+}
+
 }  // namespace fa

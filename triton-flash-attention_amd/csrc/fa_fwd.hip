@@ -122,7 +122,8 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 
   // Split-KV mode: the split index is the slowest-varying part of the block index.
   const int split = kSplits ? blockIdx.x / (a.num_tiles * a.BH) : 0;
-  const TileHead th = decode_block(blockIdx.x - split * a.num_tiles * a.BH, a.BH);
+  const TileHead th =
+      decode_block_grouped(blockIdx.x - split * a.num_tiles * a.BH, a.BH, a.group);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
@@ -435,7 +436,8 @@ void fwd_pipe_kernel(FwdArgs a) {
 
   // Split-KV mode: the split index is the slowest-varying part of the block index.
   const int split = blockIdx.x / (a.num_tiles * a.BH);
-  const TileHead th = decode_block(blockIdx.x - split * a.num_tiles * a.BH, a.BH);
+  const TileHead th =
+      decode_block_grouped(blockIdx.x - split * a.num_tiles * a.BH, a.BH, a.group);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
