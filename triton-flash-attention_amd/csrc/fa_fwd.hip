@@ -75,7 +75,7 @@ __device__ __forceinline__ void store_fwd_output(const FwdArgs& a, const rsrc_t&
   // no lane value has to stay live, and spill, across the main loop.
   g = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 5);
   const int64_t prow = ((int64_t)split * a.BH + head) * a.N + qrow;
-  float* po = a.part + prow * D;
+  float* po = split_mode ? a.part + prow * D : nullptr;  // part is null in one-pass mode
   const bool row_ok = qrow < a.N;
 #pragma unroll
   for (int db = 0; db < D / 32; ++db)
