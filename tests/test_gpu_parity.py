@@ -800,3 +800,35 @@ def test_split_forward_under_hip_graph_capture():
     torch.cuda.synchronize()
     for got, want in zip(captured, eager2):
         assert torch.equal(got, want), "replay on new inputs differs from eager"
+
+
+# ---------------------------------------------------------------------------
+# Long sequences (32-bit slab offsets, many key splits)
+# ---------------------------------------------------------------------------
+def test_long_sequences():
+    # causal self-attention at N = 32768, D = 128: fwd + bwd against the fp32 reference
+    B, H, N, D = 1, 2, 32768, 128
+    _note(f"long self-attention B={B} H={H} N={N} D={D} causal")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, H, H, N, D, seed=61, mult=0.5))
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+    out = scaled_dot_product_attention(qa, ka, va, is_causal=True, backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qa, ka, va), do)
+    _, lse = _ops.flash_fwd(q, k, v, True, D ** -0.5)
+    ref = torch_reference_fp32(q, k, v, do, True, o16=out.detach())
+    torch.cuda.synchronize()
+    for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        ma, rl = assert_close(f"long N={N} {name}", t.float(), ref[name])
+        _note(f"  {name}: max-abs {ma:.2e} rel-L2 {rl:.2e}")
+    assert float((lse - ref["lse"]).abs().max()) <= LSE_TOL
+    del ref, qa, ka, va, out, dq, dk, dv
+    torch.cuda.empty_cache()
+    # decoding against 262144 keys (GQA 8 -> 1): the split forward against the oracle
+    B, Hq, Hkv, Nq, Nkv, D = 1, 8, 1, 4, 262144, 128
+    _note(f"long decode B={B} Hq={Hq} Hkv={Hkv} N_q={Nq} N_kv={Nkv} D={D}")
+    assert _lib.load().fa_fwd_workspace_bytes(B, Hq, Hkv, Nq, Nkv, D, 0) > 0
+    q, k, v, _ = make_inputs(B, Hq, Hkv, Nq, D, seed=62, n_kv=Nkv)
+    o, lse = _ops.flash_fwd(q.to(DEV), k.to(DEV), v.to(DEV), False, D ** -0.5)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), False)
+    assert_close("long decode o", o.double().cpu().numpy(), o_ref)
+    assert float(np.max(np.abs(lse.double().cpu().numpy() - lse_ref))) <= LSE_TOL
