@@ -16,7 +16,12 @@ Prints ONE JSON line with the driver's fields plus
                 timed on this host over the same workload;
   parity:       after the timed regions, the measured path's O, LSE, dQ, dK,
                 dV on the bench inputs against a plain PyTorch fp32 attention
-                on the GPU, with the north-star tolerances.
+                on the GPU, with the north-star tolerances;
+  reference_protocol: the same step timed the way the reference's harness
+                does (benchmark_attention.py:153-158 via triton.testing.do_bench:
+                a 512 MiB L2/MALL flush before every repetition, median and
+                p20/p80 of HIP-event times) — the number comparable with the
+                reference's published table; `value` is the back-to-back rate.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -191,7 +196,7 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU (MI355X)", file=sys.stderr)
         return 2
-    from benchmarks.benchmark_attention import attention_flops
+    from benchmarks.benchmark_attention import attention_flops, bench_gpu
     from triton_flash_attention import _ops, explain_dispatch, scaled_dot_product_attention
 
     B, Hq, Hkv, N, D, causal, mult, seed = WORKLOADS[args.workload]
@@ -297,6 +302,13 @@ def main(argv=None) -> int:
         "baseline_note": "vs_baseline divides by the reference's published 13.283 TFLOP/s "
                          "(Triton path, RTX 5050 Laptop GPU, README.md:159)",
         "device": torch.cuda.get_device_name(),
+    }
+
+    median, p20, p80 = bench_gpu(step, warmup_ms=100.0, rep_ms=300.0)
+    record["reference_protocol"] = {
+        "median_ms": round(median, 5), "p20_ms": round(p20, 5), "p80_ms": round(p80, 5),
+        "value": round(flops / (median * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+        "flush_bytes": 512 << 20,
     }
 
     if not args.no_parity:
