@@ -213,7 +213,7 @@ int fa_bwd_dq_delta_kv_bf16(const fa_half_t* q, const fa_half_t* k, const fa_hal
  * element type). With workspace == NULL, or when no split is needed, the call
  * is fa_fwd_kv; a non-NULL workspace smaller than needed is rejected
  * (FA_ERR_BAD_SHAPE). Splitting, the launch computes fp32 partial O and LSE
- * per key range of at least 512 keys into the workspace and merges them
+ * per key range of at least 1024 keys into the workspace and merges them
  * (O = sum_s w_s O_s / sum_s w_s, w_s = exp2(lse_s - max lse), LSE = max +
  * log2 sum w_s) in a second launch on the same stream; results agree with
  * the unsplit forward up to fp32 summation order. No counterpart in the

@@ -730,7 +730,7 @@ SPLIT_FWD_CASES = [
     (2, 4, 2, 16, 3000, 64, True, torch.float16),     # top-left causal: most splits empty
     (1, 2, 2, 2048, 2048, 32, True, torch.float16),   # self-attention with few heads
     (1, 3, 1, 77, 5000, 64, False, torch.bfloat16),
-    (1, 4, 4, 5, 1537, 128, True, torch.bfloat16),
+    (1, 4, 4, 5, 2600, 128, True, torch.bfloat16),
 ]
 
 
@@ -832,3 +832,52 @@ def test_long_sequences():
     o_ref, lse_ref = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), False)
     assert_close("long decode o", o.double().cpu().numpy(), o_ref)
     assert float(np.max(np.abs(lse.double().cpu().numpy() - lse_ref))) <= LSE_TOL
+
+
+# ---------------------------------------------------------------------------
+# Packed GQA forward (N_q <= 32: a work-group serves several query heads)
+# ---------------------------------------------------------------------------
+PACKED_CASES = [
+    # (B, Hq, Hkv, N_q, N_kv, D, causal)
+    (2, 8, 4, 1, 700, 64, False),     # group 2 -> 2 heads per work-group
+    (1, 12, 4, 7, 3000, 32, True),    # group 3 -> no packing
+    (2, 16, 4, 32, 1500, 128, True),  # group 4 -> 4 heads, causal
+    (1, 12, 2, 5, 2500, 64, False),   # group 6 -> 2 heads
+    (1, 16, 2, 1, 9000, 128, False),  # group 8 -> 4 heads, split
+    (3, 8, 2, 17, 333, 32, True),     # group 4, short keys (no split)
+]
+
+
+@pytest.mark.parametrize("case", PACKED_CASES,
+                         ids=lambda c: f"H{c[1]}-{c[2]}Nq{c[3]}Nkv{c[4]}D{c[5]}{'c' if c[6] else 'b'}")
+def test_packed_gqa_forward_matches_oracle(case):
+    B, Hq, Hkv, N, Nkv, D, causal = case
+    tag = f"packed B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} causal={causal}"
+    _note(tag)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=3 * N + Nkv + D, mult=0.5, n_kv=Nkv)
+    got = run_kernel(q, k, v, do, causal)
+    check_against_oracle(got, q, k, v, do, causal, tag=tag)
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_packed_gqa_every_forward_tiling(head_dim):
+    """Every compiled forward tiling (2, 4 and 8 waves pack 2, 4 and 8 heads
+    of a group of 8) on decoding shapes, one pass and split."""
+    scale = head_dim ** -0.5
+    for B, Hq, Hkv, N, Nkv, causal in ((1, 16, 2, 3, 600, True), (1, 16, 2, 1, 5000, False)):
+        q, k, v, _ = make_inputs(B, Hq, Hkv, N, head_dim, seed=N + Nkv, mult=0.5, n_kv=Nkv)
+        o_ref, lse_ref = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), causal, scale)
+        qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+        for var in _lib.tiling_variants(_lib.KERNEL_FWD, head_dim, causal):
+            tag = (f"packed N_q={N} N_kv={Nkv} D={head_dim} causal={causal} fwd variant "
+                   f"{var['variant']} ({var['waves']} waves, tile {var['tile']})")
+            _note(tag)
+            _lib.set_tiling(_lib.KERNEL_FWD, head_dim, causal, var["variant"])
+            try:
+                o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
+                torch.cuda.synchronize()
+            finally:
+                _lib.set_tiling(_lib.KERNEL_FWD, head_dim, causal, -1)
+            assert_close(tag + " o", o.double().cpu().numpy(), o_ref)
+            lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - lse_ref)))
+            assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"

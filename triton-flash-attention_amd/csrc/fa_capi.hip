@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <numeric>
 
 #include "../../include/fa_gfx950.h"
 #include "fa_kernels.hpp"
@@ -195,20 +196,32 @@ int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, i
 
 // Forward split-KV factor: launches with few work-groups (decoding: a few
 // queries against a long key sequence, or few heads) split each work-group's
-// keys into up to 64 ranges of at least 512 keys (multiples of 128), run as
-// separate work-groups, then merged (launch_fwd_combine).
+// keys into up to 32 ranges of at least 1024 keys (multiples of 128), run as
+// separate work-groups, then merged (launch_fwd_combine). Swept on MI355X
+// decoding shapes: ~3 work-groups per CU with long ranges beat more, shorter
+// ones (partials and merge cost more than the extra parallelism returns).
 constexpr int64_t kFwdSplitBelowWorkgroups = 512;
-constexpr int64_t kFwdSplitTargetWorkgroups = 1024;
-constexpr int64_t kFwdMinSplitKeys = 512;
-constexpr int kMaxFwdSplit = 64;
+constexpr int64_t kFwdSplitTargetWorkgroups = 768;
+constexpr int64_t kFwdMinSplitKeys = 1024;
+constexpr int kMaxFwdSplit = 32;
 
 struct FwdSplit {
   int nsplit;
   int split_keys;
 };
 
-FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv) {
-  const int64_t wgs = (N + var.rows - 1) / var.rows * B * Hq;
+// Query heads per forward work-group: GQA launches of at most 32 queries
+// (decoding) pack gcd(group, waves) heads, which then share each K/V tile the
+// work-group streams; otherwise 1.
+int fwd_pack(const fa::Variant& var, int64_t group, int64_t N) {
+  if (N > 32 || group < 2) return 1;
+  return (int)std::gcd<int64_t>(group, var.waves);
+}
+
+FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv,
+                   int pack) {
+  const int64_t rows = var.rows / pack;  // query rows per head and work-group
+  const int64_t wgs = (N + rows - 1) / rows * B * Hq / pack;
   const int whole = (int)((Nkv + 127) / 128 * 128);
   if (wgs >= kFwdSplitBelowWorkgroups || !(var.flags & fa::kSplitsKv)) return {1, whole};
   int64_t s = (kFwdSplitTargetWorkgroups + wgs - 1) / wgs;
@@ -259,7 +272,8 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   a.c = scale * fa::kLog2e;
   auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv);
+  a.pack = fwd_pack(*var, Hq / Hkv, N);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv, a.pack);
   const int64_t need = fwd_workspace_bytes(sp, B, Hq, N, D);
   a.nsplit = 1;
   a.split_keys = (int)((Nkv + 127) / 128 * 128);
@@ -288,7 +302,8 @@ int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, 
   for (int dt : {fa::kF16, fa::kBF16}) {
     const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_workspace_bytes: no kernel for the selected tiling");
-    bytes = std::max(bytes, fwd_workspace_bytes(fwd_split(*var, B, Hq, N_q, N_kv), B, Hq, N_q, D));
+    const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, fwd_pack(*var, Hq / Hkv, N_q));
+    bytes = std::max(bytes, fwd_workspace_bytes(sp, B, Hq, N_q, D));
   }
   return bytes;
 }

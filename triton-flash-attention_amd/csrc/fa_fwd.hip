@@ -120,12 +120,15 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  // Split-KV mode: the split index is the slowest-varying part of the block index.
-  const int split = kSplits ? blockIdx.x / (a.num_tiles * a.BH) : 0;
+  // Split-KV mode: the split index is the slowest-varying part of the block
+  // index. Packed GQA: the work-group serves P query heads, wave w head w % P.
+  const int P = a.pack;
+  const int row_wgs = a.BH / P;  // work-groups per tile row
+  const int split = kSplits ? blockIdx.x / (a.num_tiles * row_wgs) : 0;
   const TileHead th =
-      decode_block_grouped(blockIdx.x - split * a.num_tiles * a.BH, a.BH, a.group);
+      decode_block_grouped(blockIdx.x - split * a.num_tiles * row_wgs, row_wgs, a.group / P);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
-  const int head = th.head;
+  const int head = th.head * P + wave % P;  // wave-uniform
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
@@ -138,11 +141,12 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
   const int4v rk = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
   const int4v rv = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
-  const int q0 = qtile * T::BM;
-  const int q0w = q0 + 32 * wave;
+  const int bm = T::BM / P;  // query rows per head
+  const int q0 = qtile * bm;
+  const int q0w = q0 + 32 * (wave / P);
   const int qrow = q0w + ql;
 
-  const int kv_end = CAUSAL ? min(Nkv, q0 + T::BM) : Nkv;
+  const int kv_end = CAUSAL ? min(Nkv, q0 + bm) : Nkv;
   // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
   const int kv_lo = kSplits ? split * a.split_keys : 0;
   const int kv_hi = kSplits ? min(kv_end, kv_lo + a.split_keys) : kv_end;
@@ -434,12 +438,15 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  // Split-KV mode: the split index is the slowest-varying part of the block index.
-  const int split = blockIdx.x / (a.num_tiles * a.BH);
+  // Split-KV mode: the split index is the slowest-varying part of the block
+  // index. Packed GQA: the work-group serves P query heads, wave w head w % P.
+  const int P = a.pack;
+  const int row_wgs = a.BH / P;  // work-groups per tile row
+  const int split = blockIdx.x / (a.num_tiles * row_wgs);
   const TileHead th =
-      decode_block_grouped(blockIdx.x - split * a.num_tiles * a.BH, a.BH, a.group);
+      decode_block_grouped(blockIdx.x - split * a.num_tiles * row_wgs, row_wgs, a.group / P);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
-  const int head = th.head;
+  const int head = th.head * P + wave % P;  // wave-uniform
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
@@ -452,8 +459,9 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
   const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
-  const int q0 = qtile * T::BM;
-  const int q0w = q0 + 32 * wave;
+  const int bm = T::BM / P;  // query rows per head
+  const int q0 = qtile * bm;
+  const int q0w = q0 + 32 * (wave / P);
   const int qrow = q0w + ql;
 
   // Q^T operand fragments: lane (query ql, k-half g), d = 16*kk + 8*g .. +7.
@@ -463,7 +471,7 @@ void fwd_pipe_kernel(FwdArgs a) {
     qf[kk] = __builtin_bit_cast(half8, buf_load_b128(rq, (uint32_t)(qrow * D + 16 * kk + 8 * g) * 2u));
   wait_all_vm();
 
-  const int kv_end = CAUSAL ? min(Nkv, q0 + T::BM) : Nkv;
+  const int kv_end = CAUSAL ? min(Nkv, q0 + bm) : Nkv;
   // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
   const int kv_lo = split * a.split_keys;
   const int kv_hi = min(kv_end, kv_lo + a.split_keys);
@@ -710,11 +718,12 @@ template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdPipeTile<D, NW, UPS>;
   FwdArgs b = a;
-  b.num_tiles = (a.N + T::BM - 1) / T::BM;
+  if (b.pack < 1 || NW % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
+  b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
       (int64_t)b.nsplit * b.split_keys < a.Nkv)
     return hipErrorInvalidValue;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
+  const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS, E>), dim3((unsigned)blocks), dim3(T::NT),
                      0, stream, b);
@@ -733,11 +742,12 @@ template <int D, bool CAUSAL, int NW, int BN, class E = F16>
 hipError_t fwd_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdTile<D, NW, BN>;
   FwdArgs b = a;
-  b.num_tiles = (a.N + T::BM - 1) / T::BM;
+  if (b.pack < 1 || NW % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
+  b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && (b.part == nullptr || !fwd_tile_splits_kv<BN>())) ||
       b.split_keys % 128 != 0 || (int64_t)b.nsplit * b.split_keys < a.Nkv)
     return hipErrorInvalidValue;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
+  const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, NW, BN, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);

@@ -35,6 +35,12 @@ struct FwdArgs {
   int nsplit;
   int split_keys;  // a multiple of 128
   float* part;
+  // Query heads per work-group. 1: a work-group serves 32 * NW query rows of
+  // one head. pack > 1 (GQA, pack dividing both the group and NW): it serves
+  // 32 * NW / pack rows of `pack` consecutive query heads of one key/value
+  // head, wave w taking head w % pack and rows 32 * (w / pack) onward, so the
+  // heads share each K/V tile the work-group streams.
+  int pack;
 };
 
 // Arguments of the backward launches (attention.py:736-770).
