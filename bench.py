@@ -175,6 +175,9 @@ def main(argv=None) -> int:
                     help="CPU-work budget of the CPU baseline (0 disables it)")
     ap.add_argument("--no-parity", action="store_true",
                     help="skip the parity check of the measured path after timing")
+    ap.add_argument("--no-reference-protocol", action="store_true",
+                    help="skip the timing with the reference harness's protocol (profiling "
+                         "runs use this so every dispatch of a kernel sees the same cache state)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after timing, copy a device buffer of this many MiB once (a "
                          "plain copy of known size that calibrates rocprofv3's "
@@ -304,12 +307,13 @@ def main(argv=None) -> int:
         "device": torch.cuda.get_device_name(),
     }
 
-    median, p20, p80 = bench_gpu(step, warmup_ms=100.0, rep_ms=300.0)
-    record["reference_protocol"] = {
-        "median_ms": round(median, 5), "p20_ms": round(p20, 5), "p80_ms": round(p80, 5),
-        "value": round(flops / (median * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-        "flush_bytes": 512 << 20,
-    }
+    if not args.no_reference_protocol:
+        median, p20, p80 = bench_gpu(step, warmup_ms=100.0, rep_ms=300.0)
+        record["reference_protocol"] = {
+            "median_ms": round(median, 5), "p20_ms": round(p20, 5), "p80_ms": round(p80, 5),
+            "value": round(flops / (median * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+            "flush_bytes": 512 << 20,
+        }
 
     if not args.no_parity:
         record["parity"] = parity_check(q, k, v, do, causal)
