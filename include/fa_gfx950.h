@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 4
+#define FA_ABI_VERSION 5
 
 /* Error codes returned before any HIP call is made. */
 #define FA_OK 0
@@ -232,6 +232,32 @@ int fa_fwd_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
                    float scale, int causal, void* workspace, int64_t workspace_bytes,
                    void* stream);
+
+/* dQ (with Delta) with split-KV for launches with few work-groups (a few
+ * queries against many keys, or few heads): fa_bwd_dq_delta_kv's arguments
+ * plus a caller-provided device workspace, sized by
+ * fa_bwd_dq_workspace_bytes (0 when it does not split, for either element
+ * type). With workspace == NULL, or when no split is needed, the call is
+ * fa_bwd_dq_delta_kv; a non-NULL workspace smaller than needed is rejected
+ * (FA_ERR_BAD_SHAPE). Splitting, work-groups over key ranges of at least
+ * 1024 keys write fp32 partial dQ ([nsplit, B, Hq, N_q, D]) that a second
+ * launch sums in a fixed order (deterministic). No counterpart in the
+ * reference, whose backward is one launch per (key block, head) with dQ
+ * inside (attention.py:754-770, 507-573). */
+int64_t fa_bwd_dq_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                                  int64_t D, int causal);
+int fa_bwd_dq_delta_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                       const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                       float* delta, fa_half_t* dq,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                       float scale, int causal, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+int fa_bwd_dq_delta_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                            const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                            float* delta, fa_half_t* dq,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                            int64_t D, float scale, int causal, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 /* Thread-local description of the last failure on the calling thread
  * ("" if none). The pointer stays valid until the next call on the thread. */

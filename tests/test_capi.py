@@ -244,3 +244,18 @@ def test_split_forward_workspace_sizing_and_rejection(lib):
     assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()
     rc = lib.fa_fwd_ws_bf16(P, P, P, P, P, 1, 32, 8, 1, 32768, 128, 0.09, 0, P + 8, ws, None)
     assert rc == _lib.FA_ERR_MISALIGNED
+
+
+def test_split_dq_workspace_sizing_and_rejection(lib):
+    assert lib.fa_bwd_dq_workspace_bytes(4, 16, 16, 4096, 4096, 64, 1) == 0
+    assert lib.fa_bwd_dq_workspace_bytes(1, 32, 8, 128, 700, 128, 0) == 0  # too few keys
+    ws = lib.fa_bwd_dq_workspace_bytes(1, 32, 8, 128, 32768, 128, 0)
+    per_split = 1 * 32 * 128 * 128 * 4  # [nsplit, B, Hq, N_q, D] fp32
+    assert ws > 0 and ws % per_split == 0 and 2 <= ws // per_split <= 32
+    assert lib.fa_bwd_dq_workspace_bytes(1, 32, 8, 128, 32768, 80, 0) == _lib.FA_ERR_HEAD_DIM
+    rc = lib.fa_bwd_dq_delta_ws(P, P, P, P, P, P, P, P, 1, 32, 8, 128, 32768, 128, 0.09, 0,
+                                P, ws - 16, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()
+    rc = lib.fa_bwd_dq_delta_ws_bf16(P, P, P, P, P, P, P, P, 1, 32, 8, 128, 32768, 128, 0.09, 0,
+                                     P + 4, ws, None)
+    assert rc == _lib.FA_ERR_MISALIGNED

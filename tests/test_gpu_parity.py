@@ -881,3 +881,57 @@ def test_packed_gqa_every_forward_tiling(head_dim):
             assert_close(tag + " o", o.double().cpu().numpy(), o_ref)
             lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - lse_ref)))
             assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# Split dQ (few work-groups: short queries against many keys, few heads)
+# ---------------------------------------------------------------------------
+SPLIT_DQ_CASES = [
+    # (B, Hq, Hkv, N_q, N_kv, D, causal, dtype)
+    (1, 32, 8, 128, 5000, 128, False, torch.float16),
+    (2, 4, 4, 64, 3000, 64, True, torch.float16),      # causal: later ranges empty
+    (1, 2, 2, 2048, 2048, 32, True, torch.float16),    # self-attention with few heads
+    (1, 6, 3, 40, 4100, 64, False, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_DQ_CASES,
+                         ids=lambda c: f"Nq{c[3]}Nkv{c[4]}D{c[5]}{'c' if c[6] else 'b'}-{str(c[7])[6:]}")
+def test_split_dq_matches_unsplit_and_oracle(case):
+    """fa_bwd_dq_delta_ws (taken by the op layer when the workspace query
+    asks for a split) agrees with the one-pass fa_bwd_dq_delta_kv up to fp32
+    summation order, writes the same Delta, and the whole backward matches
+    the oracle."""
+    B, Hq, Hkv, N, Nkv, D, causal, dtype = case
+    tag = f"split dq B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} causal={causal} {dtype}"
+    _note(tag)
+    lib = _lib.load()
+    assert lib.fa_bwd_dq_workspace_bytes(B, Hq, Hkv, N, Nkv, D, int(causal)) > 0
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + 2 * Nkv + D, mult=0.5, n_kv=Nkv,
+                              dtype=dtype)
+    bf16 = dtype == torch.bfloat16
+    got = run_kernel(q, k, v, do, causal)  # the op layer's backward takes the split dQ
+    if bf16:
+        check_bf16_against_oracle(got, q, k, v, do, causal, tag=tag)
+    else:
+        check_against_oracle(got, q, k, v, do, causal, tag=tag)
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    scale = D ** -0.5
+    o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
+    delta_s, dq_s = torch.empty_like(lse), torch.empty_like(qd)
+    delta_1, dq_1 = torch.empty_like(lse), torch.empty_like(qd)
+    ws_bytes = lib.fa_bwd_dq_workspace_bytes(B, Hq, Hkv, N, Nkv, D, int(causal))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), o.data_ptr(), dod.data_ptr(),
+            lse.data_ptr())
+    split_fn = lib.fa_bwd_dq_delta_ws_bf16 if bf16 else lib.fa_bwd_dq_delta_ws
+    one_fn = lib.fa_bwd_dq_delta_kv_bf16 if bf16 else lib.fa_bwd_dq_delta_kv
+    _lib.check(split_fn(*args, delta_s.data_ptr(), dq_s.data_ptr(), B, Hq, Hkv, N, Nkv, D, scale,
+                        int(causal), ws.data_ptr(), ws_bytes, stream))
+    _lib.check(one_fn(*args, delta_1.data_ptr(), dq_1.data_ptr(), B, Hq, Hkv, N, Nkv, D, scale,
+                      int(causal), stream))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(delta_s, delta_1, rtol=0, atol=0)
+    assert_close(f"{tag} dq split vs one pass", dq_s.float(), dq_1.float(),
+                 max_abs=4e-3 if not bf16 else 3e-2, rel_l2=1e-3 if not bf16 else 8e-3)

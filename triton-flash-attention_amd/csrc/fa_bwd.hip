@@ -122,6 +122,63 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   *reinterpret_cast<half4*>((is_v ? dv : dk) + 4 * j) = h;
 }
 
+template <class E>
+__global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part,
+                                                        half_t* __restrict__ out, int64_t elems4,
+                                                        int nsplit) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index
+  if (i >= elems4) return;
+  const float4v* src = reinterpret_cast<const float4v*>(part) + i;
+  float4v acc = src[0];
+  for (int sp = 1; sp < nsplit; ++sp) acc += src[(int64_t)sp * elems4];
+  half4 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) h[e] = to_elem<E>(acc[e]);
+  *reinterpret_cast<half4*>(out + 4 * i) = h;
+}
+
+hipError_t launch_split_sum(const float* part, half_t* out, int64_t elems, int nsplit, int dtype,
+                            hipStream_t stream) {
+  const int64_t elems4 = elems / 4;
+  const int64_t blocks = (elems4 + 255) / 256;
+  if (elems % 4 != 0 || nsplit < 2 || blocks <= 0 || blocks > 0x7fffffff)
+    return hipErrorInvalidValue;
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(split_sum_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, stream, part,
+                       out, elems4, nsplit);
+  else
+    hipLaunchKernelGGL(split_sum_kernel<F16>, dim3((unsigned)blocks), dim3(256), 0, stream, part,
+                       out, elems4, nsplit);
+  return hipGetLastError();
+}
+
+// dQ epilogue: lane (query qrow, half g) holds d = 32*db + 8*(j/4) + 4*g + j%4
+// of dQ / mul: 16-bit through rdq, or in split mode the fp32 partial of split
+// `split` (part[split][B*Hq][N][D]).
+template <int D, class E>
+__device__ __forceinline__ void store_dq(const BwdArgs& a, const rsrc_t& rdq, int split, int head,
+                                         int qrow, const float16v (&dq)[D / 32], float mul) {
+  const bool split_mode = a.nsplit > 1;
+  // The lane's half, recomputed (mbcnt needs no live register).
+  const int g = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 5);
+  const int64_t prow = ((int64_t)split * a.BH + head) * a.N + qrow;
+  float* po = split_mode ? a.part + prow * D : nullptr;  // part is null in one-pass mode
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      float4v v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = dq[db][4 * jq + e] * mul;
+      if (split_mode) {
+        if (qrow < a.N) *reinterpret_cast<float4v*>(po + 32 * db + 8 * jq + 4 * g) = v;
+      } else {
+        buf_store_b64(rdq, (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u,
+                      pack4<E>(v[0], v[1], v[2], v[3]));
+      }
+    }
+}
+
 hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_t plane_elems,
                                int nsplit, int dtype, hipStream_t stream) {
   const int64_t plane4 = plane_elems / 4;
@@ -994,7 +1051,10 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  const TileHead th = decode_block_grouped(blockIdx.x, a.BH, a.group);
+  // Split mode: the split index is the slowest-varying part of the block index.
+  const int split = blockIdx.x / (a.num_tiles * a.BH);
+  const TileHead th =
+      decode_block_grouped(blockIdx.x - split * a.num_tiles * a.BH, a.BH, a.group);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
@@ -1035,14 +1095,17 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   }
 
   const int kv_end = CAUSAL ? min(Nkv, q0 + T::BQ) : Nkv;
-  const int ntiles = (kv_end + KT - 1) / KT;
+  // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
+  const int kv_lo = split * a.split_keys;
+  const int kv_hi = min(kv_end, kv_lo + a.split_keys);
+  const int ntiles = kv_hi > kv_lo ? (kv_hi - kv_lo + KT - 1) / KT : 0;
 
   Dma dma;
   dma.init(wave, lane);
   auto issue_tile = [&](int t, int slot) {
     const half_t* base = lds + slot * T::STAGE;
-    dma.issue(rk, t * KT, base, wave);
-    dma.issue(rv, t * KT, base + T::TILE, wave);
+    dma.issue(rk, kv_lo + t * KT, base, wave);
+    dma.issue(rv, kv_lo + t * KT, base + T::TILE, wave);
   };
 #pragma unroll
   for (int t = 0; t < T::AHEAD; ++t) issue_tile(t, t);
@@ -1089,7 +1152,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   auto step = [&](auto slot_c, int t) {
     constexpr int SLOT = decltype(slot_c)::value;
     issue_tile(t + T::AHEAD, (SLOT + T::AHEAD) % T::NSTAGE);
-    const int kt0 = t * KT;
+    const int kt0 = kv_lo + t * KT;
     const half_t* Ks = lds + SLOT * T::STAGE;
     const half_t* Vs = Ks + T::TILE;
     bool act[NB];
@@ -1097,7 +1160,7 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int kb = 0; kb < NB; ++kb) {
       const int ka = kt0 + 32 * kb;
-      act[kb] = q0w < N && ka < Nkv && !(CAUSAL && ka > q0w + 31);
+      act[kb] = q0w < N && ka < kv_hi && !(CAUSAL && ka > q0w + 31);
       if (act[kb]) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -1121,14 +1184,14 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) kt_f[h][db] = tr8(Ks + (32 * kb + 16 * h) * D, db);
-      const bool need_mask = (CAUSAL && ka + 31 > q0w) || (ka + 32 > Nkv);
+      const bool need_mask = (CAUSAL && ka + 31 > q0w) || (ka + 32 > kv_hi);
       half8 sa[2];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         float pj = exp2_fast(s[kb][j] + nl);
         if (need_mask) {
           const int key = ka + result_row(j, g);
-          if (key >= Nkv || (CAUSAL && key > qrow)) pj = 0.f;
+          if (key >= kv_hi || (CAUSAL && key > qrow)) pj = 0.f;
         }
         sa[j >> 3][j & 7] = to_elem<E>(pj * (dp[kb][j] - delta));
       }
@@ -1150,17 +1213,8 @@ __global__ __launch_bounds__(64 * NW) void dq_kernel(BwdArgs a) {
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const float scale = a.scale;
   const rsrc_t rdq = make_rsrc(a.dq + (int64_t)head * N * D, slab);
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const uint32_t off = (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u;
-      buf_store_b64(rdq, off,
-                    pack4<E>(dq[db][4 * jq] * scale, dq[db][4 * jq + 1] * scale,
-                               dq[db][4 * jq + 2] * scale, dq[db][4 * jq + 3] * scale));
-    }
+  store_dq<D, E>(a, rdq, split, head, qrow, dq, a.scale);
 }
 
 template <int D, bool CAUSAL, int NW, int KT, class E = F16>
@@ -1168,7 +1222,10 @@ hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DqTile<D, NW, KT>;
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BH;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
+      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((dq_kernel<D, CAUSAL, NW, KT, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);
@@ -1236,7 +1293,10 @@ void dq_pipe_kernel(BwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  const TileHead th = decode_block_grouped(blockIdx.x, a.BH, a.group);
+  // Split mode: the split index is the slowest-varying part of the block index.
+  const int split = blockIdx.x / (a.num_tiles * a.BH);
+  const TileHead th =
+      decode_block_grouped(blockIdx.x - split * a.num_tiles * a.BH, a.BH, a.group);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
   const int head = th.head;
   const int b = head / a.Hq;
@@ -1282,7 +1342,7 @@ void dq_pipe_kernel(BwdArgs a) {
       for (int e = 0; e < 8; ++e) part = fmaf(elem_to_f32<E>(ov[e]), -elem_to_f32<E>(don[kk][e]), part);
     }
     delta = halves_sum(part);
-    if (g == 0 && qrow < N) a.delta_out[(int64_t)head * N + qrow] = delta;
+    if (g == 0 && qrow < N && split == 0) a.delta_out[(int64_t)head * N + qrow] = delta;
   } else {
     delta = buf_load_f32(rd, (uint32_t)qrow * 4u);
   }
@@ -1295,15 +1355,18 @@ void dq_pipe_kernel(BwdArgs a) {
   for (int kk = 0; kk < D / 16; ++kk) asm volatile("" : "+v"(qf[kk]), "+v"(don[kk]));
 
   const int kv_end = CAUSAL ? min(Nkv, q0 + T::BQ) : Nkv;
-  const int nunits = (kv_end + T::KT - 1) / T::KT;
+  // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
+  const int kv_lo = split * a.split_keys;
+  const int kv_hi = min(kv_end, kv_lo + a.split_keys);
+  const int nunits = kv_hi > kv_lo ? (kv_hi - kv_lo + T::KT - 1) / T::KT : 0;
   const int npad = (nunits + NS - 1) / NS * NS;
 
   Dma dma;
   dma.init(wave, lane);
   const uint32_t lds0 = lds_addr(lds);
-  int i_row = 0;  // first key row of the next unit to fetch
+  int i_row = kv_lo;  // first key row of the next unit to fetch
   auto issue = [&](int slot) {
-    const int row0 = i_row < kv_end ? i_row : Nkv;  // past the end: zeros
+    const int row0 = i_row < kv_hi ? i_row : Nkv;  // past the range: zeros
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;
@@ -1420,7 +1483,7 @@ void dq_pipe_kernel(BwdArgs a) {
       for (int db = 0; db < D / 32; ++db) acc_mfma(dq[db], tr8(slot + 16 * h * D, db), sa_prev[h]);
   };
 
-  int c_key = 0;  // first key of the unit the body works on
+  int c_key = kv_lo;  // first key of the unit the body works on
 
   auto body = [&](auto slot_c) {
     constexpr int SLOT = decltype(slot_c)::value;
@@ -1533,17 +1596,8 @@ void dq_pipe_kernel(BwdArgs a) {
   if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const float nscale = -a.scale;  // accumulated -dS
   const rsrc_t rdq = make_rsrc(a.dq + (int64_t)head * N * D, slab);
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-    for (int jq = 0; jq < 4; ++jq) {
-      const uint32_t off = (uint32_t)(qrow * D + 32 * db + 8 * jq + 4 * g) * 2u;
-      buf_store_b64(rdq, off,
-                    pack4<E>(dq[db][4 * jq] * nscale, dq[db][4 * jq + 1] * nscale,
-                               dq[db][4 * jq + 2] * nscale, dq[db][4 * jq + 3] * nscale));
-    }
+  store_dq<D, E>(a, rdq, split, head, qrow, dq, -a.scale);  // accumulated -dS
 }
 
 template <int D, bool CAUSAL, int NW, class E = F16>
@@ -1551,7 +1605,10 @@ hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   using T = DqPipeTile<D, NW>;
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
-  const int64_t blocks = (int64_t)b.num_tiles * a.BH;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
+      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
                      stream, b);

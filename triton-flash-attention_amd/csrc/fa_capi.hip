@@ -170,6 +170,7 @@ fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
   a.scale = scale;
   a.nsplit = 1;
   a.part = nullptr;
+  a.split_keys = (int)((Nkv + 127) / 128 * 128);
   a.o = nullptr;
   a.delta_out = nullptr;
   return a;
@@ -218,18 +219,31 @@ int fwd_pack(const fa::Variant& var, int64_t group, int64_t N) {
   return (int)std::gcd<int64_t>(group, var.waves);
 }
 
-FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv,
-                   int pack) {
-  const int64_t rows = var.rows / pack;  // query rows per head and work-group
-  const int64_t wgs = (N + rows - 1) / rows * B * Hq / pack;
+// Key split of a launch of `wgs` work-groups over Nkv keys (forward and dQ).
+FwdSplit key_split(int64_t wgs, int64_t Nkv, bool can_split) {
   const int whole = (int)((Nkv + 127) / 128 * 128);
-  if (wgs >= kFwdSplitBelowWorkgroups || !(var.flags & fa::kSplitsKv)) return {1, whole};
+  if (wgs >= kFwdSplitBelowWorkgroups || !can_split) return {1, whole};
   int64_t s = (kFwdSplitTargetWorkgroups + wgs - 1) / wgs;
   s = std::min<int64_t>(s, std::max<int64_t>(1, Nkv / kFwdMinSplitKeys));
   s = std::min<int64_t>(s, kMaxFwdSplit);
   if (s <= 1) return {1, whole};
   const int64_t keys = ((Nkv + s - 1) / s + 127) / 128 * 128;
   return {(int)((Nkv + keys - 1) / keys), (int)keys};
+}
+
+FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv,
+                   int pack) {
+  const int64_t rows = var.rows / pack;  // query rows per head and work-group
+  return key_split((N + rows - 1) / rows * B * Hq / pack, Nkv, var.flags & fa::kSplitsKv);
+}
+
+// dQ: the same split of its key loop; the partials (fp32 dQ) are summed.
+FwdSplit dq_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv) {
+  return key_split((N + var.rows - 1) / var.rows * B * Hq, Nkv, true);
+}
+
+int64_t dq_workspace_bytes(const FwdSplit& sp, int64_t B, int64_t Hq, int64_t N, int64_t D) {
+  return sp.nsplit > 1 ? (int64_t)sp.nsplit * B * Hq * N * D * 4 : 0;
 }
 
 int64_t fwd_workspace_bytes(const FwdSplit& sp, int64_t B, int64_t Hq, int64_t N, int64_t D) {
@@ -416,7 +430,7 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
                          const fa_half_t* v, const fa_half_t* o, const fa_half_t* dO,
                          const float* lse, float* delta, fa_half_t* dq, int64_t B, int64_t Hq,
                          int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
-                         void* stream) {
+                         void* stream, void* workspace = nullptr, int64_t workspace_bytes = 0) {
   if (!q || !k || !v || !o || !dO || !lse || !delta || !dq)
     return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
@@ -429,6 +443,20 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
   hipStream_t s = static_cast<hipStream_t>(stream);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
+  // Split mode (few work-groups, a workspace given): fp32 partial dQ per key range, then summed.
+  const FwdSplit sp = dq_split(*var, B, Hq, N, Nkv);
+  const int64_t need = dq_workspace_bytes(sp, B, Hq, N, D);
+  const bool split = need > 0 && workspace != nullptr;
+  if (split) {
+    if (workspace_bytes < need)
+      return fail(FA_ERR_BAD_SHAPE, "%s: workspace of %lld bytes is smaller than the %lld bytes "
+                  "fa_bwd_dq_workspace_bytes reports", name, (long long)workspace_bytes,
+                  (long long)need);
+    if ((rc = check_aligned(name, {workspace}))) return rc;
+    a.nsplit = sp.nsplit;
+    a.split_keys = sp.split_keys;
+    a.part = static_cast<float*>(workspace);
+  }
   if (var->flags & fa::kFusesDelta) {
     a.o = reinterpret_cast<const fa::half_t*>(o);
     a.delta_out = delta;
@@ -439,7 +467,40 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
     if (e != hipSuccess) return launch_result(e, name);
   }
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
-  return launch_result(fn(a, s), name);
+  hipError_t e = fn(a, s);
+  if (e != hipSuccess || !split) return launch_result(e, name);
+  return launch_result(fa::launch_split_sum(a.part, a.dq, B * Hq * N * D, sp.nsplit, dt, s), name);
+}
+
+int64_t fa_bwd_dq_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                                  int64_t D, int causal) {
+  int rc = check_common(B, Hq, Hkv, N_q, D);
+  if (rc) return rc;
+  if ((rc = check_kv_length(N_kv, D))) return rc;
+  int64_t bytes = 0;  // enough for either element type
+  for (int dt : {fa::kF16, fa::kBF16}) {
+    const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
+    if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq_workspace_bytes: no kernel for the selected tiling");
+    bytes = std::max(bytes, dq_workspace_bytes(dq_split(*var, B, Hq, N_q, N_kv), B, Hq, N_q, D));
+  }
+  return bytes;
+}
+
+int fa_bwd_dq_delta_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                       const fa_half_t* o, const fa_half_t* dO, const float* lse, float* delta,
+                       fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q,
+                       int64_t N_kv, int64_t D, float scale, int causal, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  return dq_delta_impl(fa::kF16, "fa_bwd_dq_delta_ws", q, k, v, o, dO, lse, delta, dq, B, Hq, Hkv,
+                       N_q, N_kv, D, scale, causal, stream, workspace, workspace_bytes);
+}
+int fa_bwd_dq_delta_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                            const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                            float* delta, fa_half_t* dq, int64_t B, int64_t Hq, int64_t Hkv,
+                            int64_t N_q, int64_t N_kv, int64_t D, float scale, int causal,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+  return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_ws_bf16", q, k, v, o, dO, lse, delta, dq, B,
+                       Hq, Hkv, N_q, N_kv, D, scale, causal, stream, workspace, workspace_bytes);
 }
 
 // ---- exported launches: fp16 (the reference's dtype) and bf16 twins ------

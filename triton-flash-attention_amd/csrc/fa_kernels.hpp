@@ -67,6 +67,11 @@ struct BwdArgs {
   // writes fp32 partials part[split][B*Hkv][N][D] (dK then dV planes).
   int nsplit;
   float* part;
+  // dQ split mode (nsplit > 1 in a dQ launch): work-group split s covers keys
+  // [s * split_keys, (s + 1) * split_keys) and writes its fp32 partial dQ
+  // (scaled) to part[split][B*Hq][N][D]; launch_split_sum adds them. With
+  // nsplit = 1, split_keys >= Nkv. Unused by the dK/dV launches.
+  int split_keys;
   // Fused Delta (dQ kernels whose variant has kFusesDelta): when o is set the
   // kernel computes Delta = rowsum(O * dO) itself and writes it to delta_out
   // instead of reading delta.
@@ -118,6 +123,10 @@ hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_
 
 hipError_t launch_preprocess(const half_t* o, const half_t* dO, float* delta, int64_t rows,
                              int D, int dtype, hipStream_t stream);
+
+// Sum of nsplit fp32 partial planes of `elems` values into 16-bit `out`.
+hipError_t launch_split_sum(const float* part, half_t* out, int64_t elems, int nsplit, int dtype,
+                            hipStream_t stream);
 
 // Merge of the forward's nsplit partials (FwdArgs::part) into O (16-bit) and
 // base-2 LSE, rows = B * Hq * N: O = sum_s w_s O_s / sum_s w_s with

@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 FA_OK = 0
 FA_ERR_NULL_POINTER = -1
@@ -79,6 +79,10 @@ del _name, _n_ptr, _res, _args, _kv
 SIGNATURES["fa_fwd_workspace_bytes"] = (_I64, (_I64, _I64, _I64, _I64, _I64, _I64, _INT))
 SIGNATURES["fa_fwd_ws"] = (_INT, SIGNATURES["fa_fwd_kv"][1][:-1] + (_P, _I64, _P))
 SIGNATURES["fa_fwd_ws_bf16"] = SIGNATURES["fa_fwd_ws"]
+# dQ with Delta and a split-KV workspace: fa_bwd_dq_delta_kv's arguments, then workspace, size, stream.
+SIGNATURES["fa_bwd_dq_workspace_bytes"] = SIGNATURES["fa_fwd_workspace_bytes"]
+SIGNATURES["fa_bwd_dq_delta_ws"] = (_INT, SIGNATURES["fa_bwd_dq_delta_kv"][1][:-1] + (_P, _I64, _P))
+SIGNATURES["fa_bwd_dq_delta_ws_bf16"] = SIGNATURES["fa_bwd_dq_delta_ws"]
 
 
 class FlashAttentionError(RuntimeError):

@@ -275,7 +275,8 @@ def flash_bwd_dq(q, k, v, do, lse, delta, causal: bool, scale: float) -> torch.T
 
 def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
     """Delta [B,H,N] fp32 = rowsum(O * dO) and dQ [B,Hq,N,D] (q's dtype) in one
-    call (one launch when the dQ tiling computes Delta itself)."""
+    call (one launch when the dQ tiling computes Delta itself). Launches with
+    few work-groups get a workspace for the library's split-KV dQ."""
     B, Hq, Hkv, N, Nkv, D = _qkv_dims(q, k, v)
     _require(o, "o", _elem_dtype(q, "q"), q.device)
     if o.shape != q.shape:
@@ -284,14 +285,24 @@ def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
     _check_bwd_inputs(q, k, v, do, lse, delta)
     q, k, v, o, do, lse = _aligned_all(q, k, v, o, do, lse)
     lib = _lib.load()
-    fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", q.dtype, N, Nkv)
+    c = int(bool(causal))
+    ws_bytes = lib.fa_bwd_dq_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c)
+    if ws_bytes < 0:
+        _lib.check(ws_bytes)
+    extra = ()
+    if ws_bytes > 0:  # few work-groups: dQ splits its keys over a workspace
+        fn, lengths = _entry(lib, "fa_bwd_dq_delta_ws", q.dtype), (N, Nkv)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        extra = (ws.data_ptr(), ws_bytes)
+    else:
+        fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", q.dtype, N, Nkv)
     dq = torch.empty_like(q)
     with _device_guard(q.device):
         rc = _launch(
             "dq", fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
             lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
-            B, Hq, Hkv, *lengths, D, float(scale), int(bool(causal)), _stream(q),
+            B, Hq, Hkv, *lengths, D, float(scale), c, *extra, _stream(q),
         )
     _lib.check(rc)
     return delta, dq
@@ -315,9 +326,15 @@ def flash_bwd(
         raise ValueError("lse must have shape [B, Hq, N]")
     q, k, v, o, do, lse = _aligned_all(q, k, v, o, do, lse)
     lib = _lib.load()
-    dq_fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", dt, N, Nkv)
-    dkdv_fn, _ = _entry_lengths(lib, "fa_bwd_dkdv_ws", dt, N, Nkv)
     c = int(bool(causal))
+    dq_ws_bytes = lib.fa_bwd_dq_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c)
+    if dq_ws_bytes < 0:
+        _lib.check(dq_ws_bytes)
+    if dq_ws_bytes > 0:  # few work-groups: dQ splits its keys over a workspace
+        dq_fn, lengths = _entry(lib, "fa_bwd_dq_delta_ws", dt), (N, Nkv)
+    else:
+        dq_fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", dt, N, Nkv)
+    dkdv_fn, dkdv_lengths = _entry_lengths(lib, "fa_bwd_dkdv_ws", dt, N, Nkv)
     if N == Nkv:
         ws_bytes = lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, c)
     else:
@@ -329,6 +346,10 @@ def flash_bwd(
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
+    dq_extra = ()
+    if dq_ws_bytes > 0:
+        dq_ws = torch.empty(dq_ws_bytes, dtype=torch.uint8, device=q.device)
+        dq_extra = (dq_ws.data_ptr(), dq_ws_bytes)
     scale = float(scale)
     with _device_guard(q.device):
         stream = _stream(q)
@@ -336,13 +357,13 @@ def flash_bwd(
             "dq", dq_fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
             lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
-            B, Hq, Hkv, *lengths, D, scale, c, stream,
+            B, Hq, Hkv, *lengths, D, scale, c, *dq_extra, stream,
         ))
         _lib.check(_launch(
             "dkdv", dkdv_fn,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
             delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-            B, Hq, Hkv, *lengths, D, scale, c,
+            B, Hq, Hkv, *dkdv_lengths, D, scale, c,
             ws.data_ptr() if ws is not None else None, ws_bytes, stream,
         ))
     return dq, dk, dv
