@@ -935,3 +935,29 @@ def test_split_dq_matches_unsplit_and_oracle(case):
     torch.testing.assert_close(delta_s, delta_1, rtol=0, atol=0)
     assert_close(f"{tag} dq split vs one pass", dq_s.float(), dq_1.float(),
                  max_abs=4e-3 if not bf16 else 3e-2, rel_l2=1e-3 if not bf16 else 8e-3)
+
+
+def _random_decode_cases(count=16, seed=4096):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(count):
+        Hkv = int(rng.choice([1, 2, 4]))
+        Hq = Hkv * int(rng.choice([1, 2, 3, 4, 6, 8]))
+        D = int(rng.choice([16, 32, 64, 96, 128]))
+        cases.append(dict(
+            B=int(rng.choice([1, 2])), Hq=Hq, Hkv=Hkv, N=int(rng.integers(1, 41)),
+            Nkv=int(rng.integers(1024, 6000)), D=D,
+            Dv=D if rng.random() < 0.8 else int(rng.choice([32, 64, 128])),
+            causal=bool(rng.random() < 0.3),
+            dtype=torch.bfloat16 if rng.random() < 0.25 else torch.float16,
+            scale=None if rng.random() < 0.7 else float(rng.uniform(0.05, 0.5)),
+            seed=seed + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_decode_cases(), ids=lambda c: f"seed{c['seed']}")
+def test_random_decode_envelope_matches_oracle(case):
+    """Seeded random decoding shapes (few queries, long keys): packed GQA,
+    split-KV forward and split dQ in combination with padded head sizes,
+    bf16 and custom scales, through the public API against the oracle."""
+    test_random_envelope_matches_oracle(case)
