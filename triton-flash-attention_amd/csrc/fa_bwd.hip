@@ -206,6 +206,14 @@ hipError_t launch_split_reduce(const float* part, half_t* dk, half_t* dv, int64_
 // S and dP of every block of the tile are issued before the first block's
 // vector work, so matrix and vector work overlap.
 // --------------------------------------------------------------------------
+template <int I, int N, typename F>
+__device__ __forceinline__ void bwd_static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    bwd_static_for<I + 1, N>(f);
+  }
+}
+
 template <int D, int NW, int QT>
 struct DkdvTile {
   static constexpr int BKV = 32 * NW;  // keys per work-group
@@ -946,15 +954,23 @@ void dkdv_pipe_kernel(BwdArgs a) {
     wait_vm_and_barrier<2 * IPU>();
   };
 
+  // Whole steps until the work-group's units are done (the unrolled ring turn
+  // may end early: padding to the turn would run masked units for nothing).
+  // `last` is the ring slot of the last unit run, the zeroed slot if none.
   static_assert(NS == 8, "the loop below is unrolled for 8 slots");
-  for (int u = 0; u < npad; u += NS) {
-    step(ic<0>{});
-    step(ic<1>{});
-    step(ic<2>{});
-    step(ic<3>{});
+  int left = nunits;
+  int last = NS - 1;
+  for (int u = 0; u < npad && left > 0; u += NS) {
+    bwd_static_for<0, 4>([&](auto p_c) {
+      if (left > 0) {
+        step(p_c);
+        last = 2 * decltype(p_c)::value + 1;
+        left -= 2;
+      }
+    });
   }
-  // dV/dK of the last unit (slot 7; zeros if it was a padding unit).
-  dvdk(lds + (NS - 1) * T::STAGE);
+  // dV/dK of the last unit run (zeros if it was a padding unit).
+  dvdk(lds + last * T::STAGE);
   if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -1585,14 +1601,20 @@ void dq_pipe_kernel(BwdArgs a) {
     wait_vm_and_barrier<2 * IPU>();
   };
 
+  // Whole steps until the work-group's units are done (as in dK/dV above).
   static_assert(NS == 8, "the loop below is unrolled for 8 slots");
-  for (int u = 0; u < npad; u += NS) {
-    step(ic<0>{});
-    step(ic<1>{});
-    step(ic<2>{});
-    step(ic<3>{});
+  int left = nunits;
+  int last = NS - 1;
+  for (int u = 0; u < npad && left > 0; u += NS) {
+    bwd_static_for<0, 4>([&](auto p_c) {
+      if (left > 0) {
+        step(p_c);
+        last = 2 * decltype(p_c)::value + 1;
+        left -= 2;
+      }
+    });
   }
-  dq_mm(lds + (NS - 1) * T::STAGE);  // dQ of the last unit (slot 7)
+  dq_mm(lds + last * T::STAGE);  // dQ of the last unit run
   if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
