@@ -66,3 +66,31 @@ def test_bench_refuses_more_than_one_gpu(capsys) -> None:
     spec.loader.exec_module(bench)
     assert bench.main(["--gpus", "8"]) == 2
     assert "one GPU" in capsys.readouterr().err
+
+
+def test_tiling_sweep_counts_executed_matmuls() -> None:
+    """The sweep's executed FLOP: the forward equals the harness's forward count;
+    dK/dV and dQ recompute S and dP, so the three kernels execute 9 matmuls
+    where the harness's 3.5 x forward convention counts 7."""
+    from benchmarks.tiling_sweep import executed_flops
+
+    kw = dict(batch=2, query_heads=3, seq_len=17, head_dim=32)
+    for causal in (False, True):
+        fwd = executed_flops("fwd", causal=causal, **kw)
+        assert fwd == attention_flops(batch=2, query_heads=3, sequence=17, head_dim=32,
+                                      causal=causal, mode="forward")
+        assert executed_flops("dkdv", causal=causal, **kw) == 2 * fwd
+        assert 2 * executed_flops("dq", causal=causal, **kw) == 3 * fwd
+    assert executed_flops("fwd", batch=1, query_heads=1, seq_len=4, head_dim=8,
+                          causal=True) == 2 * 2 * 10 * 8
+
+
+def test_tiling_sweep_rejects_bad_arguments() -> None:
+    import pytest
+
+    from benchmarks.tiling_sweep import main
+
+    with pytest.raises(SystemExit):
+        main(["--kernels", "fwd,bogus"])
+    with pytest.raises(SystemExit):
+        main(["--query-heads", "6", "--kv-heads", "4"])

@@ -52,9 +52,9 @@ def test_fallback_names_for_undemangled_kernels():
 def test_default_kernel_list_follows_the_tiling_table():
     ok, why = _lib.available()
     assert ok, why
-    for (kind, D), variant in compile_check.DEFAULT_VARIANTS.items():
-        for causal in (False, True):
-            assert _lib.get_tiling(kind, D, causal)["variant"] == variant, (kind, D, causal)
+    for (kind, D, causal), variant in compile_check.DEFAULT_VARIANTS.items():
+        assert _lib.get_tiling(kind, D, causal)["variant"] == variant, (kind, D, causal)
+    assert len(compile_check.DEFAULT_VARIANTS) == 3 * 3 * 2
 
 
 def test_unsupported_arch_is_rejected():

@@ -220,6 +220,23 @@ def test_split_dkdv_matches_single_pass():
         assert_close("split dv", dv1.float(), dv2.float(), max_abs=2e-3, rel_l2=1e-3)
 
 
+def test_tiling_sweep_times_every_variant_and_restores_the_table():
+    """benchmarks.tiling_sweep times each compiled tiling of each kernel once,
+    marks the table's choice, and leaves the table selected afterwards."""
+    from benchmarks.tiling_sweep import sweep
+
+    before = {k: _lib.get_tiling(k, 64, True)["variant"]
+              for k in (_lib.KERNEL_FWD, _lib.KERNEL_DKDV, _lib.KERNEL_DQ)}
+    rows = sweep(batch=1, query_heads=4, kv_heads=2, seq_len=300, head_dim=64, causal=True,
+                 kernels=["fwd", "dkdv", "dq"], reps=2)
+    for name, kind in (("fwd", _lib.KERNEL_FWD), ("dkdv", _lib.KERNEL_DKDV), ("dq", _lib.KERNEL_DQ)):
+        mine = [r for r in rows if r["kernel"] == name]
+        assert [r["variant"] for r in mine] == [t["variant"] for t in _lib.tiling_variants(kind, 64, True)]
+        assert sum(r["table"] for r in mine) == 1
+        assert all(r["us"] > 0 and r["tflops_executed"] > 0 for r in mine)
+        assert _lib.get_tiling(kind, 64, True)["variant"] == before[kind]
+
+
 @pytest.mark.parametrize("head_dim", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_every_tiling_variant_matches_oracle(head_dim, causal):

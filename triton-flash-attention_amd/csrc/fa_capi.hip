@@ -59,12 +59,13 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //         D = 128 runs one work-group per CU with dK, dV in AGPRs)
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-key units, software-pipelined (all D;
-//         at D = 128 the classic 4 waves x 32 stays faster)
+//         at D = 128 the classic 4 waves x 32 with its separate Delta pass stays
+//         faster under the causal mask)
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
     {{6, 6}, {6, 6}, {2, 2}},  // fwd
     {{4, 4}, {4, 4}, {4, 4}},  // dkdv
-    {{4, 4}, {4, 4}, {1, 1}},  // dq
+    {{4, 4}, {4, 4}, {4, 1}},  // dq
 };
 
 const fa::Variant* registry(int kind, int* count) {

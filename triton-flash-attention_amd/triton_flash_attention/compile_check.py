@@ -40,19 +40,24 @@ def _defaults() -> tuple[str, ...]:
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
                       f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
                       f"fa::dq_pipe_kernel<32, {c}, 4, {e}>", f"fa::dq_pipe_kernel<64, {c}, 4, {e}>",
-                      f"fa::dq_kernel<128, {c}, 4, 32, {e}>"]
+                      f"fa::dq_pipe_kernel<128, false, 4, {e}>" if c == "false"
+                      else f"fa::dq_kernel<128, true, 4, 32, {e}>"]
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
     return tuple(names)
 
 
 DEFAULT_KERNELS = _defaults()
-# The same table as (kernel kind, head_dim) -> default variant index, for the
-# test that keeps this list in step with kDefault (kinds: 0 fwd, 1 dK/dV, 2 dQ).
+# The same table as (kernel kind, head_dim, causal) -> default variant index,
+# for the test that keeps this list in step with kDefault (kinds: 0 fwd,
+# 1 dK/dV, 2 dQ).
 DEFAULT_VARIANTS = {
-    (0, 32): 6, (0, 64): 6, (0, 128): 2,
-    (1, 32): 4, (1, 64): 4, (1, 128): 4,
-    (2, 32): 4, (2, 64): 4, (2, 128): 1,
+    (0, 32, False): 6, (0, 32, True): 6, (0, 64, False): 6, (0, 64, True): 6,
+    (0, 128, False): 2, (0, 128, True): 2,
+    (1, 32, False): 4, (1, 32, True): 4, (1, 64, False): 4, (1, 64, True): 4,
+    (1, 128, False): 4, (1, 128, True): 4,
+    (2, 32, False): 4, (2, 32, True): 4, (2, 64, False): 4, (2, 64, True): 4,
+    (2, 128, False): 4, (2, 128, True): 1,
 }
 
 
