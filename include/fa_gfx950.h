@@ -275,7 +275,10 @@ int fa_abi_version(void);
  * fa_num_tiling_variants / fa_describe_tiling_variant enumerate the
  * variants of a kernel (describe returns FA_ERR_BAD_TILING for one that is
  * not compiled for this head_dim); fa_set_tiling selects one for the
- * process (variant < 0 restores the default). Used by tuning sweeps. */
+ * process (variant < 0 restores the default). Used by tuning sweeps. One
+ * shape rule refines the table: dQ at D = 128 without the mask runs the
+ * classic 4 x 32 tiling (variant 1) for fewer than 128 queries, unless a
+ * tiling was set. */
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);
 int fa_num_tiling_variants(int kernel, int64_t D, int causal);
 int fa_describe_tiling_variant(int kernel, int64_t D, int causal, int variant, int* out4);

@@ -220,6 +220,32 @@ def test_split_dkdv_matches_single_pass():
         assert_close("split dv", dv1.float(), dv2.float(), max_abs=2e-3, rel_l2=1e-3)
 
 
+def test_short_query_dq_rule_matches_oracle_and_the_pipelined_tiling():
+    """dQ at D = 128 without the mask runs the classic tiling for fewer than
+    128 queries (a shape rule over the table): results agree with the oracle
+    and, to fp32 summation order, with the table's pipelined tiling forced by
+    fa_set_tiling, in one pass and with the split dQ."""
+    for (B, Hq, Hkv, N, Nkv) in [(2, 8, 2, 16, 700), (1, 32, 8, 40, 6000)]:
+        tag = f"short-query dq B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D=128"
+        print(tag, flush=True)
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, 128, seed=N + Nkv, mult=0.5, n_kv=Nkv)
+        got = run_kernel(q, k, v, do, False)
+        check_against_oracle(got, q, k, v, do, False, tag=tag)
+        qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+        o, lse = _ops.flash_fwd(qd, kd, vd, False, 128 ** -0.5)
+        delta_rule, dq_rule = _ops.flash_bwd_dq_delta(qd, kd, vd, o, dod, lse, False, 128 ** -0.5)
+        _lib.set_tiling(_lib.KERNEL_DQ, 128, False, 4)
+        try:
+            delta_pipe, dq_pipe = _ops.flash_bwd_dq_delta(qd, kd, vd, o, dod, lse, False,
+                                                          128 ** -0.5)
+        finally:
+            _lib.set_tiling(_lib.KERNEL_DQ, 128, False, -1)
+        torch.cuda.synchronize()
+        assert_close(tag + " dq rule vs pipelined", dq_rule.float(), dq_pipe.float(),
+                     max_abs=2e-3, rel_l2=1e-3)
+        torch.testing.assert_close(delta_rule, delta_pipe, rtol=1e-5, atol=1e-5, msg=tag)
+
+
 def test_tiling_sweep_times_every_variant_and_restores_the_table():
     """benchmarks.tiling_sweep times each compiled tiling of each kernel once,
     marks the table's choice, and leaves the table selected afterwards."""

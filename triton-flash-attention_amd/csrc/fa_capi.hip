@@ -102,6 +102,26 @@ const fa::Variant* select(int kind, int di, int causal, int* index, int dt = fa:
   return &vs[v];
 }
 
+// dQ tiling for a launch of N queries. Without the mask at D = 128 the table's
+// pipelined kernel (one work-group per CU) is faster once the queries fill its
+// 128-row tiles; with fewer (a short-query backward) the classic 4 waves x 32
+// tiling, at two work-groups per CU, is (MI355X, B8 Hq32 Hkv8 against 8192
+// keys: 16 queries 147 vs 177 us, 128 queries 251 vs 239 us). A tiling set
+// with fa_set_tiling is used as set.
+constexpr int kDqShortQueryVariant = 1;
+
+const fa::Variant* select_dq(int di, int causal, int64_t N, int dt) {
+  const fa::Variant* var = select(fa::kDq, di, causal, nullptr, dt);
+  if (!var || di != fa::head_dim_index(128) || causal || N >= 128 ||
+      g_override[fa::kDq][di][0] >= 0)
+    return var;
+  int count = 0;
+  const fa::Variant* vs = registry(fa::kDq, &count);
+  if (kDqShortQueryVariant < count && usable(vs[kDqShortQueryVariant], di, causal, dt))
+    return &vs[kDqShortQueryVariant];
+  return var;
+}
+
 int check_common(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || N <= 0)
     return fail(FA_ERR_BAD_SHAPE, "B, Hq, Hkv and N must be positive (got %lld, %lld, %lld, %lld)",
@@ -419,7 +439,7 @@ static int dq_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
+  const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
@@ -439,7 +459,7 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
+  const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   hipStream_t s = static_cast<hipStream_t>(stream);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
@@ -480,7 +500,7 @@ int64_t fa_bwd_dq_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_
   if ((rc = check_kv_length(N_kv, D))) return rc;
   int64_t bytes = 0;  // enough for either element type
   for (int dt : {fa::kF16, fa::kBF16}) {
-    const fa::Variant* var = select(fa::kDq, fa::head_dim_index(D), causal, nullptr, dt);
+    const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N_q, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq_workspace_bytes: no kernel for the selected tiling");
     bytes = std::max(bytes, dq_workspace_bytes(dq_split(*var, B, Hq, N_q, N_kv), B, Hq, N_q, D));
   }
