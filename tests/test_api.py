@@ -217,11 +217,11 @@ def test_missing_library_raises_in_auto_mode(monkeypatch) -> None:
     mode raises instead of silently running PyTorch."""
     calls = {}
 
-    def fake_explain(q, k, v, *, enable_gqa=False):
+    def fake_dispatch(q, k, v):
         calls["n"] = calls.get("n", 0) + 1
         return DispatchDecision("torch", f"{attn._REASON_LIBRARY}: not built")
 
-    monkeypatch.setattr(attn, "explain_dispatch", fake_explain)
+    monkeypatch.setattr(attn, "_dispatch", fake_dispatch)
     t = torch.randn(1, 1, 4, 32)
     with pytest.raises(RuntimeError, match="kernel library is not available"):
         attn.scaled_dot_product_attention(t, t, t)

@@ -246,6 +246,31 @@ def test_short_query_dq_rule_matches_oracle_and_the_pipelined_tiling():
         torch.testing.assert_close(delta_rule, delta_pipe, rtol=1e-5, atol=1e-5, msg=tag)
 
 
+def test_forward_without_grad_matches_the_autograd_path():
+    """Inputs that need no gradient (or calls under torch.no_grad()) take the
+    forward launch without the autograd Function: bit-identical output, no
+    graph, for native and zero-padded head sizes, fp16 and bf16, GQA."""
+    for (B, Hq, Hkv, N, Nkv, D, Dv, dtype) in [(2, 8, 2, 300, 300, 64, 64, torch.float16),
+                                               (1, 4, 4, 77, 500, 40, 40, torch.bfloat16),
+                                               (1, 6, 3, 129, 129, 64, 32, torch.float16)]:
+        q, k, v, _ = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + D, n_kv=Nkv,
+                                                      d_v=Dv, dtype=dtype))
+        gqa = Hq != Hkv
+        with_grad = scaled_dot_product_attention(
+            q.clone().requires_grad_(), k.clone().requires_grad_(), v.clone().requires_grad_(),
+            is_causal=True, enable_gqa=gqa, backend="triton")
+        plain = scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=gqa,
+                                             backend="triton")
+        with torch.no_grad():
+            no_grad = scaled_dot_product_attention(q.clone().requires_grad_(), k, v,
+                                                   is_causal=True, enable_gqa=gqa,
+                                                   backend="triton")
+        assert with_grad.grad_fn is not None
+        assert plain.grad_fn is None and no_grad.grad_fn is None
+        assert plain.shape == no_grad.shape == with_grad.shape == (B, Hq, N, Dv)
+        assert torch.equal(plain, with_grad.detach()) and torch.equal(no_grad, plain)
+
+
 def test_tiling_sweep_times_every_variant_and_restores_the_table():
     """benchmarks.tiling_sweep times each compiled tiling of each kernel once,
     marks the table's choice, and leaves the table selected afterwards."""

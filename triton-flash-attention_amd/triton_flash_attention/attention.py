@@ -40,7 +40,7 @@ raises instead of silently falling back (rule 8), unless ``backend="torch"``.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, replace
+from dataclasses import dataclass
 from numbers import Real
 from typing import Literal
 
@@ -203,19 +203,26 @@ def explain_dispatch(
 ) -> DispatchDecision:
     """Explain whether the custom gfx950 kernel can serve these inputs."""
     _validate_inputs(query, key, value, enable_gqa=enable_gqa)
-    facts = _DispatchFacts(
+    return _dispatch(query, key, value)
+
+
+def _dispatch(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> DispatchDecision:
+    """The dispatch decision for inputs that already passed ``_validate_inputs``
+    (the public API validates once, then decides)."""
+    arch = library_error = None
+    if query.device.type == "cuda":
+        ok, why = _lib.available()
+        arch, library_error = _device_arch(query.device), None if ok else why
+    return _decide(_DispatchFacts(
         q_len=query.shape[2],
         kv_len=key.shape[2],
         head_dim=query.shape[3],
         value_head_dim=value.shape[3],
         device_type=query.device.type,
         dtype=query.dtype,
-    )
-    if facts.device_type == "cuda":
-        ok, why = _lib.available()
-        facts = replace(facts, arch=_device_arch(query.device),
-                        library_error=None if ok else why)
-    return _decide(facts)
+        arch=arch,
+        library_error=library_error,
+    ))
 
 
 class TritonAttention(torch.autograd.Function):
@@ -234,19 +241,12 @@ class TritonAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, key, value, causal, softmax_scale):
         head_dim, value_head_dim = query.shape[-1], value.shape[-1]
-        width = _kernel_width(head_dim, value_head_dim)
-        if width is None:
-            raise ValueError(
-                f"head sizes {head_dim} / {value_head_dim}: the gfx950 kernels serve at most "
-                f"{_SUPPORTED_HEAD_DIMS[-1]}"
-            )
-        query, key, value = (_pad_head(t, width) for t in (query, key, value))
-        output, lse = _ops.flash_fwd(query, key, value, bool(causal), float(softmax_scale))
+        query, key, value, output, lse = _padded_forward(query, key, value, causal, softmax_scale)
         ctx.save_for_backward(query, key, value, output, lse)
         ctx.head_dims = (head_dim, value_head_dim)
         ctx.softmax_scale = float(softmax_scale)
         ctx.causal = bool(causal)
-        return output if value_head_dim == width else output[..., :value_head_dim].contiguous()
+        return _unpad_output(output, value_head_dim)
 
     @staticmethod
     def backward(ctx, grad_output):
@@ -261,6 +261,24 @@ class TritonAttention(torch.autograd.Function):
         if value_head_dim != query.shape[-1]:
             grad_value = grad_value[..., :value_head_dim]
         return grad_query, grad_key, grad_value, None, None
+
+
+def _padded_forward(query, key, value, causal, softmax_scale):
+    """The forward launch at the kernel width: (padded q, k, v, O, LSE)."""
+    width = _kernel_width(query.shape[-1], value.shape[-1])
+    if width is None:
+        raise ValueError(
+            f"head sizes {query.shape[-1]} / {value.shape[-1]}: the gfx950 kernels serve at "
+            f"most {_SUPPORTED_HEAD_DIMS[-1]}"
+        )
+    query, key, value = (_pad_head(t, width) for t in (query, key, value))
+    output, lse = _ops.flash_fwd(query, key, value, bool(causal), float(softmax_scale))
+    return query, key, value, output, lse
+
+
+def _unpad_output(output: torch.Tensor, value_head_dim: int) -> torch.Tensor:
+    return (output if output.shape[-1] == value_head_dim
+            else output[..., :value_head_dim].contiguous())
 
 
 def _pad_head(t: torch.Tensor, width: int) -> torch.Tensor:
@@ -321,7 +339,7 @@ def scaled_dot_product_attention(
             query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
         )
 
-    decision = explain_dispatch(query, key, value, enable_gqa=enable_gqa)
+    decision = _dispatch(query, key, value)
     if decision.backend == "torch":
         if backend == "triton" or decision.reason.startswith(_REASON_LIBRARY):
             raise RuntimeError(f"Triton backend is unavailable: {decision.reason}")
@@ -339,6 +357,11 @@ def scaled_dot_product_attention(
         return _torch_sdpa(
             query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
         )
-    return TritonAttention.apply(
-        query.contiguous(), key.contiguous(), value.contiguous(), is_causal, softmax_scale
-    )
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    if torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
+                                    or value.requires_grad):
+        return TritonAttention.apply(query, key, value, is_causal, softmax_scale)
+    # No gradient can flow (inference, or under torch.no_grad()): the same
+    # forward launch without the autograd Function's bookkeeping.
+    output = _padded_forward(query, key, value, is_causal, softmax_scale)[3]
+    return _unpad_output(output, value.shape[-1])
