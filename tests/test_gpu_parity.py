@@ -14,6 +14,7 @@ relative L2 <= 5e-3; base-2 LSE max-abs <= 1e-4.
 
 from __future__ import annotations
 
+import math
 import sys
 
 import numpy as np
@@ -900,6 +901,100 @@ def test_long_sequences():
     o_ref, lse_ref = oracle.fwd(q.numpy(), k.numpy(), v.numpy(), False)
     assert_close("long decode o", o.double().cpu().numpy(), o_ref)
     assert float(np.max(np.abs(lse.double().cpu().numpy() - lse_ref))) <= LSE_TOL
+
+
+def _chunked_reference(q, k, v, do, o16, scale, chunk=1 << 21):
+    """fp64 forward and backward of one key/value head on the GPU, keys in
+    chunks: q, do [G, n, D] (the group's query heads), k, v [N_kv, D], o16 the
+    kernel's stored O. The backward's scores use the fp16-rounded scaled
+    operands the kernels use, fp16(c k) for dK/dV and fp16(c q) for dQ with
+    c = scale / ln 2, as the oracle's fold mode does. Returns O, LSE2, dQ and
+    a generator of (key slice, dK, dV) chunks, computed as it is consumed."""
+    G, n, D = q.shape
+    c = scale / math.log(2.0)
+    qf = q.double().reshape(G * n, D)
+    dof = do.double().reshape(G * n, D)
+    m = torch.full((G * n,), -math.inf, dtype=torch.float64, device=q.device)
+    l = torch.zeros_like(m)
+    acc = torch.zeros_like(qf)
+    for c0 in range(0, k.shape[0], chunk):
+        s2 = (qf @ k[c0:c0 + chunk].double().t().contiguous()) * c
+        m_new = torch.maximum(m, s2.max(dim=1).values)
+        alpha = torch.exp2(m - m_new)
+        p = torch.exp2(s2 - m_new[:, None])
+        l = l * alpha + p.sum(dim=1)
+        acc = acc * alpha[:, None] + p @ v[c0:c0 + chunk].double()
+        m = m_new
+    o = acc / l[:, None]
+    lse2 = m + torch.log2(l)
+    delta = (o16.double().reshape(G * n, D) * dof).sum(dim=1)
+    q16 = (q.double() * c).half().double().reshape(G * n, D)
+    dq = torch.zeros_like(qf)
+    for c0 in range(0, k.shape[0], chunk):
+        kc, vc = k[c0:c0 + chunk].double(), v[c0:c0 + chunk].double()
+        p_q = torch.exp2(q16 @ kc.t().contiguous() - lse2[:, None])
+        dq += (p_q * (dof @ vc.t().contiguous() - delta[:, None])) @ kc * scale
+
+    def kv_chunks():
+        for c0 in range(0, k.shape[0], chunk):
+            kc, vc = k[c0:c0 + chunk].double(), v[c0:c0 + chunk].double()
+            p_kv = torch.exp2(qf @ (kc * c).half().double().t().contiguous() - lse2[:, None])
+            ds_kv = p_kv * (dof @ vc.t().contiguous() - delta[:, None])
+            yield (slice(c0, c0 + chunk), (ds_kv.t().contiguous() @ qf) * scale,
+                   p_kv.t().contiguous() @ dof)
+
+    return o.reshape(G, n, D), lse2.reshape(G, n), dq.reshape(G, n, D), kv_chunks()
+
+
+def test_longest_key_sequence_the_library_accepts():
+    """The largest N_kv the C ABI accepts at D = 32 (2 GiB key and value slabs:
+    N_kv D 2 + 4096 D 2 < 2^31): forward (split-KV, packed GQA) and backward
+    (dK/dV over 262 k key tiles, split dQ) through the op layer against an fp64
+    reference. Each query row has its own dominant key among the last six
+    (the last key is row 0's), so a lost or misaddressed final row shows in
+    O, LSE and dK/dV. Also checks that the API's own limit stays within the
+    library's."""
+    D, G, n = 32, 2, 3
+    Nkv = (1 << 31) // (2 * D) - 4096 - 1
+    lib = _lib.load()
+    assert lib.fa_fwd_workspace_bytes(1, G, 1, n, Nkv, D, 0) > 0
+    assert lib.fa_fwd_workspace_bytes(1, G, 1, n, Nkv + 1, D, 0) == _lib.FA_ERR_TOO_LARGE
+    from triton_flash_attention import attention as attn
+    assert (attn._MAX_SLAB_BYTES // (2 * D)) <= Nkv
+    _note(f"longest key sequence B=1 Hq={G} Hkv=1 N_q={n} N_kv={Nkv} D={D}")
+    gen = torch.Generator(device=DEV).manual_seed(71)
+    q = (torch.randn((1, G, n, D), generator=gen, device=DEV) * 0.5).half()
+    k = (torch.randn((1, 1, Nkv, D), generator=gen, device=DEV) * 0.5).half()
+    v = (torch.randn((1, 1, Nkv, D), generator=gen, device=DEV) * 0.5).half()
+    do = (torch.randn((1, G, n, D), generator=gen, device=DEV) * 0.5).half()
+    scale = D ** -0.5
+    # Key N_kv-1-r is query row r's own: score 24 with it (e^24 >> N_kv), value 3 - r.
+    for r in range(G * n):
+        qr = q[0, r // n, r % n].float()
+        k[0, 0, Nkv - 1 - r] = (qr * (24.0 / scale / float(qr @ qr))).half()
+        v[0, 0, Nkv - 1 - r] = 3.0 - r
+    o, lse = _ops.flash_fwd(q, k, v, False, scale)
+    dq, dk, dv = _ops.flash_bwd(q, k, v, o, lse, do, False, scale)
+    torch.cuda.synchronize()
+    o_ref, lse_ref, dq_ref, grads = _chunked_reference(q[0], k[0, 0], v[0, 0], do[0], o[0], scale)
+    for r in range(G * n):  # each row's planted key, the last row among them, dominates
+        assert abs(float(o[0, r // n, r % n].float().mean()) - (3.0 - r)) < 0.05, r
+    assert_close("longest o", o[0].double(), o_ref)
+    assert float((lse[0].double() - lse_ref).abs().max()) <= LSE_TOL
+    assert_close("longest dq", dq[0].double(), dq_ref)
+    num = {"dk": 0.0, "dv": 0.0}
+    den = {"dk": 0.0, "dv": 0.0}
+    worst = {"dk": 0.0, "dv": 0.0}
+    for sl, dk_ref, dv_ref in grads:
+        for name, got, ref in (("dk", dk[0, 0, sl], dk_ref), ("dv", dv[0, 0, sl], dv_ref)):
+            diff = got.double() - ref
+            num[name] += float((diff * diff).sum())
+            den[name] += float((ref * ref).sum())
+            worst[name] = max(worst[name], float(diff.abs().max()))
+    for name in ("dk", "dv"):
+        rel = math.sqrt(num[name]) / math.sqrt(den[name])
+        _note(f"  {name}: max-abs {worst[name]:.2e} rel-L2 {rel:.2e}")
+        assert worst[name] <= MAX_ABS_TOL and rel <= REL_L2_TOL, (name, worst[name], rel)
 
 
 # ---------------------------------------------------------------------------
