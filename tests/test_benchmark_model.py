@@ -94,3 +94,19 @@ def test_tiling_sweep_rejects_bad_arguments() -> None:
         main(["--kernels", "fwd,bogus"])
     with pytest.raises(SystemExit):
         main(["--query-heads", "6", "--kv-heads", "4"])
+
+
+def test_cross_attention_flops_count_top_left_visible_pairs() -> None:
+    """kv_sequence (the cross-attention extension): N_q * N_kv pairs without the
+    mask; under SDPA's top-left causal mask query i sees min(i+1, N_kv) keys
+    (brute-force count). kv_sequence = sequence is the reference's count."""
+    kw = dict(batch=1, query_heads=1, head_dim=1, mode="forward")
+    for n_q, n_kv in ((3, 7), (7, 3), (1, 32768), (5, 5)):
+        brute = sum(min(i + 1, n_kv) for i in range(n_q))
+        assert attention_flops(sequence=n_q, kv_sequence=n_kv, causal=True, **kw) == 4 * brute
+        assert attention_flops(sequence=n_q, kv_sequence=n_kv, causal=False, **kw) == 4 * n_q * n_kv
+    for causal in (False, True):
+        assert attention_flops(sequence=9, kv_sequence=9, causal=causal, **kw) == \
+            attention_flops(sequence=9, causal=causal, **kw)
+    cross = memory_model(batch=1, query_heads=1, sequence=4, kv_sequence=1024)
+    assert cross["naive_score_mib"] == memory_model(batch=1, query_heads=1, sequence=64)["naive_score_mib"]

@@ -52,11 +52,14 @@ def attention_flops(
     head_dim: int,
     causal: bool,
     mode: str,
+    kv_sequence: int | None = None,
 ) -> int:
     """Algorithmic FLOPs (reference convention, benchmark_attention.py:36-54):
     forward = 4 * B * Hq * pairs * D with pairs = N(N+1)/2 causal, N^2
-    otherwise; backward = 2.5x forward; forward-backward = 3.5x forward."""
-    pairs = sequence * (sequence + 1) // 2 if causal else sequence * sequence
+    otherwise; backward = 2.5x forward; forward-backward = 3.5x forward.
+    With ``kv_sequence`` (cross-attention, an extension) pairs = N_q * N_kv,
+    or under the causal mask the top-left visible pairs sum_i min(i+1, N_kv)."""
+    pairs = _visible_pairs(sequence, sequence if kv_sequence is None else kv_sequence, causal)
     forward = 4 * batch * query_heads * pairs * head_dim
     if mode == "forward":
         return forward
@@ -67,17 +70,29 @@ def attention_flops(
     raise ValueError(f"unknown mode: {mode}")
 
 
+def _visible_pairs(n_q: int, n_kv: int, causal: bool) -> int:
+    """(query, key) pairs a query sequence of n_q attends over n_kv keys;
+    causal: query i sees keys j <= i (SDPA's top-left mask)."""
+    if not causal:
+        return n_q * n_kv
+    full = min(n_q, n_kv)
+    return full * (full + 1) // 2 + (n_q - full) * n_kv
+
+
 def memory_model(
     *,
     batch: int,
     query_heads: int,
     sequence: int,
     element_size: int = 2,
+    kv_sequence: int | None = None,
 ) -> dict[str, float]:
-    """One materialized score matrix versus the saved fp32 LSE vector, MiB."""
+    """One materialized score matrix versus the saved fp32 LSE vector, MiB
+    (``kv_sequence``: the key length of cross-attention, an extension)."""
     mib = float(1 << 20)
+    n_kv = sequence if kv_sequence is None else kv_sequence
     return {
-        "naive_score_mib": batch * query_heads * sequence * sequence * element_size / mib,
+        "naive_score_mib": batch * query_heads * sequence * n_kv * element_size / mib,
         "saved_lse_mib": batch * query_heads * sequence * 4 / mib,
     }
 
@@ -166,10 +181,11 @@ def benchmark_case(
     causal: bool,
     warmup_ms: int,
     rep_ms: int,
+    kv_sequence: int | None = None,
 ) -> dict[str, Any]:
     requires_grad = mode != "forward"
     shape_q = (batch, query_heads, sequence, head_dim)
-    shape_kv = (batch, kv_heads, sequence, head_dim)
+    shape_kv = (batch, kv_heads, sequence if kv_sequence is None else kv_sequence, head_dim)
     kw = dict(device="cuda", dtype=torch.float16, requires_grad=requires_grad)
     query = torch.randn(shape_q, **kw)
     key = torch.randn(shape_kv, **kw)
@@ -181,9 +197,11 @@ def benchmark_case(
     )
     median, low, high = bench_gpu(runner, warmup_ms=warmup_ms, rep_ms=rep_ms)
     flops = attention_flops(batch=batch, query_heads=query_heads, sequence=sequence,
-                            head_dim=head_dim, causal=causal, mode=mode)
-    memory = memory_model(batch=batch, query_heads=query_heads, sequence=sequence)
+                            head_dim=head_dim, causal=causal, mode=mode, kv_sequence=kv_sequence)
+    memory = memory_model(batch=batch, query_heads=query_heads, sequence=sequence,
+                          kv_sequence=kv_sequence)
     tflops = flops / (median * 1e-3) / 1e12
+    cross = {} if kv_sequence is None else {"kv_sequence": kv_sequence}
     return {
         "provider": provider,
         "mode": mode,
@@ -192,6 +210,7 @@ def benchmark_case(
         "query_heads": query_heads,
         "kv_heads": kv_heads,
         "sequence": sequence,
+        **cross,
         "head_dim": head_dim,
         "median_ms": round(median, 5),
         "p20_ms": round(low, 5),
@@ -244,6 +263,9 @@ def build_parser() -> argparse.ArgumentParser:
     parser.add_argument("--query-heads", type=_positive_int, default=16)
     parser.add_argument("--kv-heads", type=_positive_int, default=None,
                         help="set below query-heads to benchmark GQA")
+    parser.add_argument("--kv-sequence-length", type=_positive_int, default=None,
+                        help="key/value length for cross-attention (an extension; the "
+                             "default is each query sequence length)")
     parser.add_argument("--mode", choices=("forward", "backward", "forward-backward"),
                         default="forward-backward")
     parser.add_argument("--mask", choices=("causal", "noncausal", "both"), default="causal")
@@ -280,7 +302,7 @@ def main(argv: list[str] | None = None) -> int:
                         provider=provider, mode=args.mode, batch=args.batch,
                         query_heads=args.query_heads, kv_heads=kv_heads, sequence=sequence,
                         head_dim=head_dim, causal=causal, warmup_ms=args.warmup_ms,
-                        rep_ms=args.rep_ms,
+                        rep_ms=args.rep_ms, kv_sequence=args.kv_sequence_length,
                     ))
     meta = metadata()
     write_results(rows, meta, args.output)

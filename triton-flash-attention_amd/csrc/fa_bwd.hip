@@ -115,6 +115,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
   const int64_t j = is_v ? i - plane4 : i;
   const float4v* src = reinterpret_cast<const float4v*>(part) + (is_v ? plane4 : 0) + j;
   float4v acc = src[0];
+#pragma unroll 8
   for (int sp = 1; sp < nsplit; ++sp) acc += src[(int64_t)sp * 2 * plane4];
   half4 h;
 #pragma unroll
@@ -130,6 +131,7 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
   if (i >= elems4) return;
   const float4v* src = reinterpret_cast<const float4v*>(part) + i;
   float4v acc = src[0];
+#pragma unroll 8
   for (int sp = 1; sp < nsplit; ++sp) acc += src[(int64_t)sp * elems4];
   half4 h;
 #pragma unroll

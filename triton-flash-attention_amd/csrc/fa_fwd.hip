@@ -766,10 +766,14 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   const int64_t row = i / CPR;
   const int c = (int)(i - row * CPR);
   const float* plse = part + (int64_t)nsplit * rows * D;
+  // Unrolled so that several splits' loads are in flight at once (the loop is
+  // a chain of dependent-latency loads otherwise); the summation order is fixed.
   float mx = -INFINITY;
+#pragma unroll 8
   for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, plse[(int64_t)sp * rows + row]);
   float wsum = 0.f;
   float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
   for (int sp = 0; sp < nsplit; ++sp) {
     const float ls = plse[(int64_t)sp * rows + row];
     const float w = ls == -INFINITY ? 0.f : exp2_fast(ls - mx);
