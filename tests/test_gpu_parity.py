@@ -272,6 +272,19 @@ def test_forward_without_grad_matches_the_autograd_path():
         assert torch.equal(plain, with_grad.detach()) and torch.equal(no_grad, plain)
 
 
+def test_forward_mode_ad_is_not_silently_dropped():
+    """Dual tensors carry tangents without requires_grad: the call goes through
+    the autograd Function, which defines no jvp (as the reference's), so it
+    raises rather than returning an output without a tangent."""
+    import torch.autograd.forward_ad as fwAD
+
+    q, k, v, _ = (t.to(DEV) for t in make_inputs(1, 2, 2, 64, 64, seed=5))
+    with fwAD.dual_level():
+        qd = fwAD.make_dual(q, torch.randn_like(q))
+        with pytest.raises(RuntimeError):
+            scaled_dot_product_attention(qd, k, v, is_causal=True, backend="triton")
+
+
 def test_tiling_sweep_times_every_variant_and_restores_the_table():
     """benchmarks.tiling_sweep times each compiled tiling of each kernel once,
     marks the table's choice, and leaves the table selected afterwards."""

@@ -263,6 +263,13 @@ class TritonAttention(torch.autograd.Function):
         return grad_query, grad_key, grad_value, None, None
 
 
+def _forward_ad_active() -> bool:
+    """Inside a forward-mode AD level, dual tensors carry tangents without
+    requires_grad; such calls go through the autograd Function, which (like
+    the reference's) defines no jvp and raises instead of dropping them."""
+    return getattr(torch.autograd.forward_ad, "_current_level", -1) >= 0
+
+
 def _padded_forward(query, key, value, causal, softmax_scale):
     """The forward launch at the kernel width: (padded q, k, v, O, LSE)."""
     width = _kernel_width(query.shape[-1], value.shape[-1])
@@ -358,8 +365,8 @@ def scaled_dot_product_attention(
             query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
         )
     query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
-    if torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
-                                    or value.requires_grad):
+    if (torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
+                                     or value.requires_grad)) or _forward_ad_active():
         return TritonAttention.apply(query, key, value, is_causal, softmax_scale)
     # No gradient can flow (inference, or under torch.no_grad()): the same
     # forward launch without the autograd Function's bookkeeping.
