@@ -773,7 +773,35 @@ def _random_cases(count=24, seed=2024):
     return cases
 
 
-@pytest.mark.parametrize("case", _random_cases(), ids=lambda c: f"seed{c['seed']}")
+def _wide_random_cases(count=96, seed=97):
+    """A wider envelope than _random_cases: GQA groups up to 8, head sizes that
+    pad (8 to 112), query lengths up to 2000 and key lengths up to 6000 (so the
+    split forward, split dQ and split dK/dV paths run), bounded so the CPU
+    oracle stays at about a second per case."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < count:
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        Hq = Hkv * int(rng.choice([1, 2, 3, 4, 8]))
+        B = int(rng.choice([1, 2, 3]))
+        N = int(rng.choice([int(rng.integers(1, 40)), int(rng.integers(1, 700)),
+                            int(rng.integers(700, 2000))]))
+        Nkv = N if rng.random() < 0.4 else int(rng.choice([int(rng.integers(1, 700)),
+                                                           int(rng.integers(700, 6000))]))
+        D = int(rng.choice([8, 16, 24, 32, 40, 64, 72, 96, 112, 128]))
+        Dv = D if rng.random() < 0.7 else int(rng.choice([16, 32, 64, 100, 128]))
+        if B * Hq * N * Nkv * max(D, Dv) > 6e8:
+            continue
+        cases.append(dict(
+            B=B, Hq=Hq, Hkv=Hkv, N=N, Nkv=Nkv, D=D, Dv=Dv, causal=bool(rng.random() < 0.5),
+            dtype=torch.bfloat16 if rng.random() < 0.3 else torch.float16,
+            scale=None if rng.random() < 0.6 else float(rng.uniform(0.03, 0.6)),
+            seed=seed * 1000 + len(cases)))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases() + _wide_random_cases(),
+                         ids=lambda c: f"seed{c['seed']}")
 def test_random_envelope_matches_oracle(case):
     c = case
     tag = (f"random seed={c['seed']} B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} N_q={c['N']} "
