@@ -285,6 +285,52 @@ def test_forward_mode_ad_is_not_silently_dropped():
             scaled_dot_product_attention(qd, k, v, is_causal=True, backend="triton")
 
 
+def test_two_threads_on_their_own_streams_match_sequential_results():
+    """The op layer launches on the calling thread's current stream and the
+    library keeps no per-call global state: two threads, each on its own
+    stream (default priority), running fwd + bwd concurrently on different
+    inputs (one taking the split paths) reproduce the sequential results
+    bit for bit."""
+    import threading
+
+    shapes = [(2, 8, 2, 333, 333, 64, True), (1, 32, 8, 16, 5000, 128, False)]
+    inputs = []
+    for i, (B, Hq, Hkv, N, Nkv, D, causal) in enumerate(shapes):
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=80 + i, n_kv=Nkv))
+        inputs.append((q, k, v, do, causal, D ** -0.5))
+
+    def step(q, k, v, do, causal, scale):
+        o, lse = _ops.flash_fwd(q, k, v, causal, scale)
+        return (o, lse) + tuple(_ops.flash_bwd(q, k, v, o, lse, do, causal, scale))
+
+    want = [step(*args) for args in inputs]
+    torch.cuda.synchronize()
+    got = [None, None]
+    errors = []
+
+    def worker(i):
+        try:
+            stream = torch.cuda.Stream()
+            with torch.cuda.stream(stream):
+                for _ in range(5):
+                    out = step(*inputs[i])
+                stream.synchronize()
+            got[i] = out
+        except Exception as exc:  # reported on the main thread
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not errors, errors
+    assert all(not th.is_alive() for th in threads)
+    for i in range(2):
+        for name, a, b in zip(("o", "lse", "dq", "dk", "dv"), got[i], want[i]):
+            assert torch.equal(a, b), f"thread {i} {name} differs from the sequential result"
+
+
 def test_tiling_sweep_times_every_variant_and_restores_the_table():
     """benchmarks.tiling_sweep times each compiled tiling of each kernel once,
     marks the table's choice, and leaves the table selected afterwards."""
