@@ -14,14 +14,20 @@ Prints ONE JSON line with the driver's fields plus
   cpu_baseline: the reference's CPU path (its public API on CPU tensors
                 dispatches to torch SDPA, attention.py:647-648 -> 774-786)
                 timed on this host over the same workload;
-  parity:       after the timed regions, the measured path's O, LSE, dQ, dK,
-                dV on the bench inputs against a plain PyTorch fp32 attention
-                on the GPU, with the north-star tolerances;
+  parity:       the measured path's O, LSE, dQ, dK, dV on the bench inputs
+                against a plain PyTorch fp32 attention on the GPU, with the
+                north-star tolerances;
   reference_protocol: the same step timed the way the reference's harness
                 does (benchmark_attention.py:153-158 via triton.testing.do_bench:
                 a 512 MiB L2/MALL flush before every repetition, median and
                 p20/p80 of HIP-event times) — the number comparable with the
                 reference's published table; `value` is the back-to-back rate.
+
+Order of a run: inputs to HBM, the parity check, the reference-protocol timing,
+then the W warmup steps and the K timed steps back to back, then the per-launch
+kernel pass and the CPU baseline. Validating before timing also means the timed
+steps start on a GPU whose clocks have left idle (from a cold start the first
+~50 steps of this workload run up to ~10 % slower).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -110,16 +116,34 @@ def kernel_flops(kernel: str, B: int, Hq: int, N: int, D: int, causal: bool) -> 
     return {"fwd": 2, "dkdv": 4, "dq": 1}[kernel] * per_matmul
 
 
+# The GPU box's CPU share for one GPU: worker threads beyond it are not ours,
+# whatever the affinity mask shows.
+CPU_SHARE_PER_GPU = 16
+
+
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (platform.processor() is
+    empty on this image)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(inputs, causal: bool, budget_s: float):
     """The reference's CPU path on the same workload: the public API with CPU
     tensors falls back to torch SDPA. Median of repetitions after one warmup,
-    repeated until ``budget_s`` of CPU work has been spent."""
+    repeated until ``budget_s`` of CPU work has been spent. Threads: every CPU
+    in the affinity mask, capped at the box's CPU share for one GPU."""
     import torch
 
     from triton_flash_attention import scaled_dot_product_attention
 
-    threads = len(os.sched_getaffinity(0))
-    threads = min(threads, 16)  # the GPU box's CPU share
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(affinity, CPU_SHARE_PER_GPU)
     torch.set_num_threads(threads)
     q, k, v, do = (t.clone() for t in inputs)
     gqa = q.shape[1] != k.shape[1]
@@ -143,7 +167,7 @@ def cpu_baseline(inputs, causal: bool, budget_s: float):
         print(f"[bench] cpu baseline rep {len(times)}: {times[-1]:.3f} s", file=sys.stderr,
               flush=True)
     times.sort()
-    return times[len(times) // 2], threads, len(times)
+    return times[len(times) // 2], threads, affinity, len(times)
 
 
 def load_traffic(workload: str, kernel: str):
@@ -187,7 +211,8 @@ def main(argv=None) -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every "
-              "(batch, head) is independent; see DESIGN.md for how it would shard). "
+              "(batch, KV-head group) is independent, so the path would shard by whole "
+              "groups with no exchange). "
               f"Requested --gpus {args.gpus} / WORLD_SIZE {world}.", file=sys.stderr)
         return 2
     if args.steps <= 0 or args.warmup < 0:
@@ -221,6 +246,24 @@ def main(argv=None) -> int:
 
     print(f"[bench] {args.workload}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal}; "
           f"warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
+    flops = attention_flops(batch=B, query_heads=Hq, sequence=N, head_dim=D, causal=causal,
+                            mode="forward-backward")
+    # Validation and the reference-protocol timing come first (see the module
+    # docstring); the headline region below is W warmup + K timed steps.
+    parity = None
+    if not args.no_parity:
+        parity = parity_check(q, k, v, do, causal)
+        print(f"[bench] parity vs fp32 reference: {'pass' if parity['pass'] else 'FAIL'}",
+              file=sys.stderr, flush=True)
+    reference_protocol = None
+    if not args.no_reference_protocol:
+        median, p20, p80 = bench_gpu(step, warmup_ms=100.0, rep_ms=300.0)
+        reference_protocol = {
+            "median_ms": round(median, 5), "p20_ms": round(p20, 5), "p80_ms": round(p80, 5),
+            "value": round(flops / (median * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+            "flush_bytes": 512 << 20,
+        }
+        print(f"[bench] reference protocol: median {median:.4f} ms", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -249,8 +292,6 @@ def main(argv=None) -> int:
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step (wall {wall_s:.3f} s)",
           file=sys.stderr, flush=True)
 
-    flops = attention_flops(batch=B, query_heads=Hq, sequence=N, head_dim=D, causal=causal,
-                            mode="forward-backward")
     value = flops / (ms_per_step * 1e-3) / 1e12
 
     kernels = {}
@@ -301,24 +342,21 @@ def main(argv=None) -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": load_traffic(args.workload, dominant),
+            "traffic_source": "profiles/traffic.json (FETCH_SIZE + WRITE_SIZE from separate "
+                              "rocprofv3 --pmc runs of this command, calibrated by a copy)",
+            "duration_source": "HIP events around each launch on its stream, kernel pass",
         },
         "baseline_note": "vs_baseline divides by the reference's published 13.283 TFLOP/s "
                          "(Triton path, RTX 5050 Laptop GPU, README.md:159)",
         "device": torch.cuda.get_device_name(),
     }
 
-    if not args.no_reference_protocol:
-        median, p20, p80 = bench_gpu(step, warmup_ms=100.0, rep_ms=300.0)
-        record["reference_protocol"] = {
-            "median_ms": round(median, 5), "p20_ms": round(p20, 5), "p80_ms": round(p80, 5),
-            "value": round(flops / (median * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-            "flush_bytes": 512 << 20,
-        }
-
-    if not args.no_parity:
-        record["parity"] = parity_check(q, k, v, do, causal)
-        print(f"[bench] parity vs fp32 reference: {'pass' if record['parity']['pass'] else 'FAIL'}",
-              file=sys.stderr, flush=True)
+    if reference_protocol is not None:
+        record["reference_protocol"] = reference_protocol
+    if parity is not None:
+        record["parity"] = parity
+    record["order"] = ("parity check and reference-protocol timing ran before the warmup "
+                       "and timed steps; per-launch kernel pass and CPU baseline after")
 
     if args.calibrate_copy_mib > 0:
         src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device="cuda")
@@ -330,16 +368,21 @@ def main(argv=None) -> int:
         del src, dst
 
     if args.cpu_seconds > 0:
-        median_s, threads, reps = cpu_baseline(cpu_inputs, causal, args.cpu_seconds)
+        median_s, threads, affinity, reps = cpu_baseline(cpu_inputs, causal, args.cpu_seconds)
         record["cpu_baseline"] = {
             "value": round(flops / median_s / 1e12, 4),
             "unit": "TFLOP/s",
             "cores": threads,
+            "affinity_cpus": affinity,
+            "thread_cap": CPU_SHARE_PER_GPU,
+            "cpu_model": cpu_model(),
             "kind": "reference",
             "sample": (f"full {args.workload} workload (fwd+bwd, {flops / 1e9:.1f} GFLOP) through "
                        "the public API on CPU fp16 tensors, which is the reference's CPU path "
                        f"(torch SDPA); median of {reps} reps after 1 warmup, "
-                       f"{median_s:.3f} s/rep, host {platform.processor() or platform.machine()}"),
+                       f"{median_s:.3f} s/rep, {threads} threads "
+                       f"(min of {affinity} CPUs in the affinity mask and the box's "
+                       f"{CPU_SHARE_PER_GPU}-CPU share per GPU)"),
         }
     else:
         record["cpu_baseline"] = None

@@ -9,6 +9,8 @@ the facts a gfx950 device would report.
 
 from __future__ import annotations
 
+import warnings
+
 import pytest
 import torch
 
@@ -88,22 +90,31 @@ def test_explicit_torch_backend_honors_custom_scale() -> None:
 
 
 def test_cross_attention_fallback_matches_reference() -> None:
-    # The reference's cross-attention test inputs (N_q 3, N_kv 5, value head
-    # size 16 != 32): on the CPU the device rule sends them to SDPA; neither the
-    # lengths nor the head sizes decide any more.
+    # The reference's test, verbatim (tests/test_api.py:100-109): on the CPU
+    # cross-attention inputs fall back with the reference's first-rule reason.
     query = torch.randn(1, 2, 3, 32)
     key = torch.randn(1, 2, 5, 32)
     value = torch.randn(1, 2, 5, 16)
     decision = explain_dispatch(query, key, value)
     assert decision.backend == "torch"
-    assert "CUDA tensor" in decision.reason
+    assert "self-attention" in decision.reason
     actual = scaled_dot_product_attention(query, key, value)
     expected = torch.nn.functional.scaled_dot_product_attention(query, key, value)
     torch.testing.assert_close(actual, expected)
+
+
+def test_cross_attention_fallback_reason_names_the_deciding_rule() -> None:
+    query = torch.randn(1, 2, 3, 32)
+    key = torch.randn(1, 2, 5, 32)
+    d = explain_dispatch(query, key, torch.randn(1, 2, 5, 16))
+    assert d.reason.startswith("the custom kernel currently specializes in self-attention")
+    assert "requires a CUDA tensor" in d.reason
     # a value head size the kernels cannot hold is rejected before the device rule
-    value = torch.randn(1, 2, 5, 160)
-    decision = explain_dispatch(query, key, value)
-    assert decision.backend == "torch" and "equal query/key and value head sizes" in decision.reason
+    d = explain_dispatch(query, key, torch.randn(1, 2, 5, 160))
+    assert d.backend == "torch" and "self-attention" in d.reason
+    assert "equal query/key and value head sizes" in d.reason
+    with pytest.raises(RuntimeError, match="self-attention"):
+        scaled_dot_product_attention(query, key, key, backend="triton")
 
 
 # --- remaining validation and argument checks (ref attention.py:584-626, 806-815)
@@ -178,6 +189,12 @@ def test_rule_eligible_gfx950_selects_custom_kernel() -> None:
         d = attn._decide(_facts(q_len=q_len, kv_len=kv_len))
         assert d.backend == "triton" and "cross-attention" in d.reason
     assert "self-attention" in attn._decide(_facts()).reason
+    # ... and where it falls back, the reason starts with the reference's first rule
+    for overrides in (dict(device_type="cpu"), dict(dtype=torch.float32), dict(arch="gfx942"),
+                      dict(library_error="missing"), dict(value_head_dim=160)):
+        d = attn._decide(_facts(q_len=3, kv_len=5, **overrides))
+        assert d.backend == "torch"
+        assert d.reason.startswith("the custom kernel currently specializes in self-attention")
 
 
 @pytest.mark.parametrize(
@@ -212,9 +229,10 @@ def test_rule_order_is_first_match() -> None:
     assert "float16" in d.reason
 
 
-def test_missing_library_raises_in_auto_mode(monkeypatch) -> None:
-    """A gfx950 device without its kernel library is a broken install: auto
-    mode raises instead of silently running PyTorch."""
+def test_missing_library_falls_back_in_auto_mode(monkeypatch) -> None:
+    """As in the reference (attention.py:829-839), auto mode never raises for
+    an unavailable backend: a gfx950 device without its kernel library runs
+    SDPA, with one RuntimeWarning per process; strict mode raises."""
     calls = {}
 
     def fake_dispatch(q, k, v):
@@ -222,10 +240,162 @@ def test_missing_library_raises_in_auto_mode(monkeypatch) -> None:
         return DispatchDecision("torch", f"{attn._REASON_LIBRARY}: not built")
 
     monkeypatch.setattr(attn, "_dispatch", fake_dispatch)
+    monkeypatch.setattr(attn, "_library_warned", False)
     t = torch.randn(1, 1, 4, 32)
-    with pytest.raises(RuntimeError, match="kernel library is not available"):
+    with pytest.warns(RuntimeWarning, match="kernel library is not available"):
+        out = attn.scaled_dot_product_attention(t, t, t)
+    torch.testing.assert_close(out, torch.nn.functional.scaled_dot_product_attention(t, t, t))
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # once per process
         attn.scaled_dot_product_attention(t, t, t)
+    with pytest.raises(RuntimeError, match="kernel library is not available"):
+        attn.scaled_dot_product_attention(t, t, t, backend="triton")
     # backend="torch" never consults the library
     out = attn.scaled_dot_product_attention(t, t, t, backend="torch")
     torch.testing.assert_close(out, torch.nn.functional.scaled_dot_product_attention(t, t, t))
-    assert calls["n"] == 1
+    assert calls["n"] == 3
+
+
+# --- every finite scale is served (ref attention.py:812-815, 844-845) ----------
+def test_kernel_scale_modes() -> None:
+    assert attn._kernel_scale(0.125) == (0.125, "plain")
+    assert attn._kernel_scale(-0.5) == (0.5, "negate")
+    for tiny in (0.0, -0.0, 1e-40, -1e-40, 1e-50):  # zero or subnormal in float32
+        assert attn._kernel_scale(tiny) == (1.0, "zero"), tiny
+    assert attn._kernel_scale(2.0 ** -126) == (2.0 ** -126, "plain")
+    assert attn._kernel_scale(1e39) is None  # float32 overflow
+    assert attn._kernel_scale(3e38) is None  # scale * log2(e) overflows float32
+
+
+def test_kernel_scale_served_scales_pass_the_library_check() -> None:
+    """Every kernel scale the Python layer sends passes the C ABI's scale check,
+    and the library rejects what _kernel_scale maps away. A call that passes
+    every check reaches the launch, which fails on a host without a GPU (the
+    fake pointers are never touched); on a GPU host only the rejections run."""
+    from triton_flash_attention import _lib
+
+    ok, why = _lib.available()
+    assert ok, why
+    lib = _lib.load()
+    P = 0x10000
+
+    def rc(scale):
+        return lib.fa_fwd(P, P, P, P, P, 1, 1, 1, 16, 32, scale, 0, None)
+
+    for s in (0.0, -1.0, 1e-40, -1e-40, float("inf"), float("nan")):
+        assert rc(s) == _lib.FA_ERR_BAD_SCALE, s
+    if torch.cuda.is_available():
+        return
+    for s in (0.125, -0.5, 0.0, 1e-40, 2.0 ** -126, 1e30, -7.0):
+        served = attn._kernel_scale(s)
+        assert served is not None and served[0] > 0
+        assert rc(served[0]) > 0, s  # reached the launch: a HIP error, not FA_ERR_BAD_SCALE
+
+
+def test_scale_transforms_are_exact_in_fp64() -> None:
+    """The score identity the negate and zero modes rest on, with the
+    reference's rounding of the backward's scaled operands (attention.py:435,
+    515: fp16(k * c), c = float32(scale / ln 2)), on fp16 inputs."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(3, 40, 64, generator=g).half()
+    k = torch.randn(3, 50, 64, generator=g).half()
+    for scale in (-0.125, -1.7, -3e-5):
+        c = torch.tensor(scale * attn._LOG2E, dtype=torch.float32)
+        cn = torch.tensor(-scale * attn._LOG2E, dtype=torch.float32)
+        assert float(cn) == -float(c)
+        s_ref = (q.double() @ k.double().transpose(1, 2)) * float(c)
+        s_neg = ((-q).double() @ k.double().transpose(1, 2)) * float(cn)
+        assert torch.equal(s_ref, s_neg)
+        k_ref = (k.float() * c).half()
+        k_neg = (k.float() * cn).half()
+        assert torch.equal(k_ref, -k_neg)
+    # with a subnormal scale every exp2 argument s * c - m rounds to -m in float32
+    s = (q.float() @ k.float().transpose(1, 2))
+    c = torch.tensor(1e-40 * attn._LOG2E, dtype=torch.float32)
+    m = (s * c).amax(-1, keepdim=True)
+    assert torch.equal(torch.exp2(s * c - m), torch.ones_like(s))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [-0.3, 0.0])
+def test_cpu_fallback_honors_nonpositive_scales(scale, causal) -> None:
+    # The CPU path is SDPA itself, as in the reference; this torch build's CPU
+    # SDPA returns NaN for causal inputs with a scale <= 0 (it scales after
+    # masking), and the fallback reproduces that bit for bit. The gfx950
+    # kernels mask after scaling, like the reference's kernel (attention.py:61-66).
+    q = torch.randn(1, 2, 9, 32)
+    out = scaled_dot_product_attention(q, q, q, scale=scale, is_causal=causal)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, q, q, scale=scale, is_causal=causal)
+    torch.testing.assert_close(out, ref, equal_nan=True, rtol=0, atol=0)
+
+
+# --- the Python eligibility bounds are the library's own ----------------------
+@pytest.mark.parametrize("width", [32, 64, 128])
+def test_length_bound_matches_library_workspace_query(width) -> None:
+    """_decide sends exactly the lengths the C ABI accepts (fa_capi.hip
+    check_common / check_kv_length) to the kernel, at the boundary for each
+    kernel width; the workspace queries check before any HIP call."""
+    from triton_flash_attention import _lib
+
+    lib = _lib.load()
+    n_max = attn._max_sequence(width)
+    for n in (n_max - 1, n_max, n_max + 1):
+        fits = attn._sequence_fits(n, width)
+        assert fits == (n <= n_max)
+        d_q = attn._decide(_facts(q_len=n, kv_len=64, head_dim=width, value_head_dim=width))
+        d_kv = attn._decide(_facts(q_len=64, kv_len=n, head_dim=width, value_head_dim=width))
+        rc_q = lib.fa_fwd_workspace_bytes(1, 1, 1, n, 64, width, 0)
+        rc_kv = lib.fa_fwd_workspace_bytes(1, 1, 1, 64, n, width, 0)
+        rc_dkdv = lib.fa_bwd_dkdv_workspace_bytes_kv(1, 1, 1, 64, n, width, 0)
+        assert (rc_q >= 0) == fits == (d_q.backend == "triton"), (n, rc_q, d_q)
+        assert (rc_kv >= 0) == fits == (d_kv.backend == "triton"), (n, rc_kv, d_kv)
+        assert (rc_dkdv >= 0) == fits
+        if not fits:
+            assert rc_q == rc_kv == _lib.FA_ERR_TOO_LARGE
+    # a smaller head size is checked at the kernel width it is padded to
+    d = attn._decide(_facts(q_len=attn._max_sequence(128), kv_len=64, head_dim=96,
+                            value_head_dim=96))
+    assert d.backend == "triton"
+    d = attn._decide(_facts(q_len=attn._max_sequence(128) + 1, kv_len=64, head_dim=96,
+                            value_head_dim=96))
+    assert d.backend == "torch" and "too long" in d.reason
+
+
+def test_batch_heads_bound_matches_library() -> None:
+    from triton_flash_attention import _lib
+
+    lib = _lib.load()
+    limit = attn._MAX_BATCH_HEADS
+    assert lib.fa_fwd_workspace_bytes(1, limit - 1, 1, 16, 16, 64, 0) >= 0
+    assert lib.fa_fwd_workspace_bytes(1, limit, 1, 16, 16, 64, 0) == _lib.FA_ERR_TOO_LARGE
+    assert attn._decide(_facts(batch_heads=limit - 1)).backend == "triton"
+    d = attn._decide(_facts(batch_heads=limit))
+    assert d.backend == "torch" and "batch * heads" in d.reason
+
+
+# --- BASELINE configuration 1 through the package on the CPU -----------------
+def test_config1_runs_the_reference_cpu_path_through_the_package() -> None:
+    """configs[0] (B1 H4 N257 D64 bidirectional, fp16 on the CPU) through the
+    public API: the CPU input takes the reference's SDPA fallback
+    (attention.py:647-648 -> 774-786), so the output is bit for bit a direct
+    F.scaled_dot_product_attention call on this host, and within fp16 accuracy
+    of the committed fp64 golden O (tests/golden/make_golden.py)."""
+    from pathlib import Path
+
+    import numpy as np
+
+    data = np.load(Path(__file__).resolve().parent / "golden" / "attention_fp64.npz")
+    name = "config1_b1_h4_n257_d64_bidir"
+    q, k, v = (torch.from_numpy(data[f"{name}/{t}"]) for t in ("q", "k", "v"))
+    assert q.dtype == torch.float16 and tuple(q.shape) == (1, 4, 257, 64)
+    decision = explain_dispatch(q, k, v)
+    assert decision == DispatchDecision("torch", "the Triton kernel requires a CUDA tensor")
+    out = scaled_dot_product_attention(q, k, v)
+    direct = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+    assert out.dtype == torch.float16 and torch.equal(out, direct)
+    golden = torch.from_numpy(data[f"{name}/o"]).double()
+    assert float((out.double() - golden).abs().max()) <= 2e-3
+    rel = float(torch.linalg.vector_norm(out.double() - golden) / torch.linalg.vector_norm(golden))
+    assert rel <= 5e-3
+    with pytest.raises(RuntimeError, match="requires a CUDA tensor"):
+        scaled_dot_product_attention(q, k, v, backend="triton")

@@ -494,20 +494,143 @@ def test_full_config_matches_fp32_reference(name, causal):
     _note(f"  lse: max-abs {lse_err:.3e}")
     assert lse_err <= LSE_TOL
 
-    # fp64 oracle on one key/value head's group of query heads (full N).
+    _check_oracle_slices(name, q, k, v, do, out.detach(), lse, dq, dk, dv, causal, ref["lse"])
+    # The whole key/value head 0 group of batch 0 where the oracle finishes in
+    # seconds (c2, c3): every row and key, full N.
     G = Hq // Hkv
-    sl = slice(0, G)
-    qs, ks, vs, dos = q[:1, sl], k[:1, :1], v[:1, :1], do[:1, sl]
-    got = {
-        "o16": out.detach()[:1, sl].cpu(),
-        "o": out.detach()[:1, sl].double().cpu().numpy(),
-        "lse": lse[:1, sl].double().cpu().numpy(),
-        "dq": dq[:1, sl].double().cpu().numpy(),
-        "dk": dk[:1, :1].double().cpu().numpy(),
-        "dv": dv[:1, :1].double().cpu().numpy(),
-    }
     if N * N * D * G <= 2 ** 32:
-        check_against_oracle(got, qs, ks, vs, dos, causal, tag=f"{name} oracle slice")
+        sl = slice(0, G)
+        got = {
+            "o16": out.detach()[:1, sl].cpu(),
+            "o": out.detach()[:1, sl].double().cpu().numpy(),
+            "lse": lse[:1, sl].double().cpu().numpy(),
+            "dq": dq[:1, sl].double().cpu().numpy(),
+            "dk": dk[:1, :1].double().cpu().numpy(),
+            "dv": dv[:1, :1].double().cpu().numpy(),
+        }
+        check_against_oracle(got, q[:1, sl], k[:1, :1], v[:1, :1], do[:1, sl], causal,
+                             tag=f"{name} oracle head group")
+
+
+# Rows and keys of the fp64-oracle slices of the full configurations.
+SLICE_FIRST_ROWS = 16
+SLICE_LAST_ROWS = 64
+SLICE_KEYS = 64
+
+
+def _check_oracle_slices(name, q, k, v, do, out, lse, dq, dk, dv, causal, lse_fp32):
+    """fp64-oracle checks on slices of a full configuration, for every GQA
+    query head of batch 0's key/value head 0:
+      * O, LSE and dQ of the first 16 and the last 64 query rows (the tail
+        tile included). Under the causal mask row r sees keys 0..r, so each
+        row is its own oracle call on those keys (unmasked); bidirectional
+        rows take one call against every key.
+      * dK and dV of the last 64 keys. Under the causal mask only the last 64
+        queries see them, so the oracle's backward on the last 64 queries and
+        keys (the top-left mask at equal offsets) is exact; bidirectional keys
+        take every query. P comes from the independent fp32 PyTorch LSE and
+        Delta from the kernel's stored O, as in the reference backward
+        (attention.py:252-254).
+    The backward uses the reference's fp16-rounded score operands (fold)."""
+    B, Hq, N, D = q.shape
+    G = Hq // k.shape[1]
+    hs = slice(0, G)
+    f64 = lambda t: t.double().cpu().numpy()
+    qh, kh, vh, doh = q[:1, hs], k[:1, :1], v[:1, :1], do[:1, hs]
+    o16 = out[:1, hs].cpu()
+    rows = sorted(set(range(min(SLICE_FIRST_ROWS, N))) | set(range(max(0, N - SLICE_LAST_ROWS), N)))
+    got_o, got_lse, got_dq = f64(out[:1, hs, rows]), f64(lse[:1, hs, rows]), f64(dq[:1, hs, rows])
+    if causal:
+        parts = [oracle.attention(qh[:, :, r:r + 1].numpy(), kh[:, :, :r + 1].numpy(),
+                                  vh[:, :, :r + 1].numpy(), doh[:, :, r:r + 1].numpy(), False,
+                                  o16=o16[:, :, r:r + 1].numpy(), fold_bwd=True) for r in rows]
+        ref = {t: np.concatenate([p[t] for p in parts], axis=2) for t in ("o", "lse", "dq")}
+    else:
+        ref = oracle.attention(qh[:, :, rows].numpy(), kh.numpy(), vh.numpy(),
+                               doh[:, :, rows].numpy(), False, o16=o16[:, :, rows].numpy(),
+                               fold_bwd=True)
+    report = {}
+    for t, got in (("o", got_o), ("dq", got_dq)):
+        report[t] = assert_close(f"{name} oracle rows {t}", got, ref[t])
+    lse_err = float(np.max(np.abs(got_lse - ref["lse"])))
+    assert lse_err <= LSE_TOL, f"{name} oracle rows lse: {lse_err:.3e}"
+    # dK, dV of the last SLICE_KEYS keys
+    k0 = max(0, N - SLICE_KEYS)
+    qrows = slice(k0, N) if causal else slice(0, N)
+    delta = oracle.bwd_preprocess(o16[:, :, qrows].numpy(), doh[:, :, qrows].numpy())
+    _, rdk, rdv = oracle.bwd(qh[:, :, qrows].numpy(), kh[:, :, k0:].numpy(), vh[:, :, k0:].numpy(),
+                             doh[:, :, qrows].numpy(), f64(lse_fp32[:1, hs, qrows]), delta,
+                             causal, fold=True)
+    report["dk"] = assert_close(f"{name} oracle keys dk", f64(dk[:1, :1, k0:]), rdk)
+    report["dv"] = assert_close(f"{name} oracle keys dv", f64(dv[:1, :1, k0:]), rdv)
+    _note(f"  {name} fp64 oracle slices ({len(rows)} rows x {G} heads, {N - k0} keys): "
+          + ", ".join(f"{t}={e[0]:.2e}/{e[1]:.2e}" for t, e in report.items())
+          + f", lse={lse_err:.2e}")
+
+
+# ---------------------------------------------------------------------------
+# Committed golden vectors (tests/golden/attention_fp64.npz: torch fp64 SDPA,
+# autograd and logsumexp, made without the oracle) against the HIP path.
+# ---------------------------------------------------------------------------
+def _golden():
+    from pathlib import Path
+
+    data = np.load(Path(__file__).resolve().parent / "golden" / "attention_fp64.npz")
+    names = sorted({key.split("/")[0] for key in data.files if "/" in key})
+    return data, names
+
+
+def _golden_case(data, name):
+    return {key.split("/")[1]: data[key] for key in data.files if key.startswith(name + "/")}
+
+
+def test_config1_hip_path_matches_golden():
+    """BASELINE configs[0] (B1 H4 N257 D64 bidirectional, seeded fp16 inputs)
+    on the HIP path: the committed golden inputs, O against the golden fp64
+    O and LSE against the golden base-2 LSE at the north-star tolerances."""
+    data, _ = _golden()
+    g = _golden_case(data, "config1_b1_h4_n257_d64_bidir")
+    q, k, v = (torch.from_numpy(g[t]).to(DEV) for t in ("q", "k", "v"))
+    assert tuple(q.shape) == (1, 4, 257, 64) and q.dtype == torch.float16
+    assert explain_dispatch(q, k, v).backend == "triton"
+    out = scaled_dot_product_attention(q, k, v, backend="triton")
+    o2, lse = _ops.flash_fwd(q, k, v, False, 64 ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o2)
+    ma, rl = assert_close("c1 o", out.double().cpu().numpy(), g["o"])
+    lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - g["lse2"])))
+    assert lse_err <= LSE_TOL, f"c1 lse {lse_err:.3e}"
+    # and the reference's own CPU path (fp16 SDPA on the CPU) on the same inputs
+    cpu = torch.nn.functional.scaled_dot_product_attention(*(t.cpu() for t in (q, k, v)))
+    assert_close("c1 o vs CPU SDPA", out.double().cpu(), cpu.double())
+    _note(f"c1 HIP vs golden: o {ma:.2e}/{rl:.2e}, lse {lse_err:.2e}")
+
+
+def test_every_golden_case_matches_on_the_hip_path():
+    """Every committed golden case through the public API on the GPU: O, LSE,
+    and (where the case has dO) dQ, dK, dV against the fp64 golden values."""
+    data, names = _golden()
+    assert len(names) >= 15
+    for name in names:
+        g = _golden_case(data, name)
+        B, Hq, Hkv, N, D, causal = (int(x) for x in g["meta"])
+        q, k, v = (torch.from_numpy(g[t]) for t in ("q", "k", "v"))
+        qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+        o2, lse = _ops.flash_fwd(qd, kd, vd, bool(causal), D ** -0.5)
+        report = {}
+        if "do" in g:
+            got = run_kernel(q, k, v, torch.from_numpy(g["do"]), bool(causal))
+            for t in ("o", "dq", "dk", "dv"):
+                report[t] = assert_close(f"golden {name} {t}", got[t], g[t])
+        else:
+            out = scaled_dot_product_attention(qd, kd, vd, is_causal=bool(causal),
+                                               enable_gqa=Hq != Hkv, backend="triton")
+            report["o"] = assert_close(f"golden {name} o", out.double().cpu().numpy(), g["o"])
+        torch.cuda.synchronize()
+        lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - g["lse2"])))
+        assert lse_err <= LSE_TOL, f"golden {name} lse: {lse_err:.3e}"
+        _note(f"golden {name}: " + ", ".join(f"{t}={e[0]:.1e}/{e[1]:.1e}" for t, e in report.items())
+              + f", lse={lse_err:.1e}")
 
 
 # ---------------------------------------------------------------------------
@@ -1047,7 +1170,7 @@ def test_longest_key_sequence_the_library_accepts():
     assert lib.fa_fwd_workspace_bytes(1, G, 1, n, Nkv, D, 0) > 0
     assert lib.fa_fwd_workspace_bytes(1, G, 1, n, Nkv + 1, D, 0) == _lib.FA_ERR_TOO_LARGE
     from triton_flash_attention import attention as attn
-    assert (attn._MAX_SLAB_BYTES // (2 * D)) <= Nkv
+    assert attn._max_sequence(D) == Nkv
     _note(f"longest key sequence B=1 Hq={G} Hkv=1 N_q={n} N_kv={Nkv} D={D}")
     gen = torch.Generator(device=DEV).manual_seed(71)
     q = (torch.randn((1, G, n, D), generator=gen, device=DEV) * 0.5).half()

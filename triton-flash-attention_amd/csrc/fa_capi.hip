@@ -2,6 +2,7 @@
 // include/fa_gfx950.h). Argument checks happen here, before any HIP call, so
 // an unsupported request never reaches the device; a rejected call returns a
 // negative FA_ERR_* code and records a message for fa_last_error().
+#include <float.h>
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -160,9 +161,17 @@ int check_aligned(const char* fn, std::initializer_list<const void*> ptrs) {
   return FA_OK;
 }
 
+// The kernels fold c = scale * log2(e) into base-2 exponents and mask by
+// setting scores to -inf before multiplying by c, so c must be a positive
+// normal float32. Callers serve other finite scales exactly on top of this:
+// a negative scale as -q at |scale| (dQ negated back), a zero (or subnormal)
+// one as a zero q at scale 1 (dQ = 0).
 int check_scale(float scale) {
-  if (!isfinite(scale) || !(scale > 0.f))
-    return fail(FA_ERR_BAD_SCALE, "scale must be finite and > 0 (got %g)", (double)scale);
+  const float c = scale * fa::kLog2e;
+  if (!isfinite(scale) || !isfinite(c) || !(c >= FLT_MIN))
+    return fail(FA_ERR_BAD_SCALE,
+                "scale must be finite and > 0 with scale * log2(e) a normal float32 (got %g)",
+                (double)scale);
   return FA_OK;
 }
 
@@ -381,9 +390,15 @@ static int64_t dkdv_workspace_impl(const char* name, int64_t B, int64_t Hq, int6
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
   if ((rc = check_kv_length(Nkv, D))) return rc;
-  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr);
-  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-  return split_workspace_bytes(dkdv_split(*var, B, Hkv, Nkv), B, Hkv, Nkv, D);
+  // Enough for either element type (an overridden fp16-only tiling leaves
+  // bf16 calls on the default tiling, whose split can be larger).
+  int64_t bytes = 0;
+  for (int dt : {fa::kF16, fa::kBF16}) {
+    const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+    if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
+    bytes = std::max(bytes, split_workspace_bytes(dkdv_split(*var, B, Hkv, Nkv), B, Hkv, Nkv, D));
+  }
+  return bytes;
 }
 
 int64_t fa_bwd_dkdv_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,

@@ -15,31 +15,44 @@ Dispatch rules (first match wins; reference rules at attention.py:629-670):
                                                         dtype of the gfx950 kernels)
   4. head_dim above 128                     -> torch   (ref 657-661 also rejects every
                                                         size other than 32, 64, 128)
-  5. sequence too long for 32-bit offsets   -> torch   (no reference counterpart)
+  5. sequence or batch*heads too large for  -> torch   (no reference counterpart; the
+     the library's 32-bit addressing                    exact bounds of fa_capi.hip)
   6. device is not gfx950                   -> torch   (replaces ref 662-666, SM >= 8)
   7. libfa_gfx950.so not loadable           -> torch   (replaces ref 649-652, the ROCm
-                                                        reject); see below
+                                                        reject)
   8. otherwise                              -> "triton" (the custom kernel backend)
 
-The reference's first rule, cross-attention (N_q != N_kv) -> torch (ref 639-642),
-is gone: the gfx950 kernels take separate query and key/value lengths and
-compute what that SDPA fallback does, top-left causal mask included (query i
-sees keys j <= i). Head sizes other than the kernels' 32, 64 and 128, and a
-value head size other than the query/key one, are served up to 128:
-:class:`TritonAttention` zero-pads the operands to the smallest kernel width
-that holds both sizes (zero columns add exact zeros to every dot product) and
-slices the results back.
+Cross-attention (N_q != N_kv) is served by the gfx950 kernels, which take
+separate query and key/value lengths and compute what the reference's SDPA
+fallback computes, top-left causal mask included (query i sees keys j <= i).
+Where rules 1-7 send cross-attention inputs to torch, the reason starts with
+the reference's first-rule reason (ref 639-642, "the custom kernel currently
+specializes in self-attention") so that callers matching on it keep working,
+followed by the rule that decided here. Head sizes other than the kernels'
+32, 64 and 128, and a value head size other than the query/key one, are served
+up to 128: :class:`TritonAttention` zero-pads the operands to the smallest
+kernel width that holds both sizes (zero columns add exact zeros to every dot
+product) and slices the results back.
 
 The backend keeps the reference's name "triton" so existing call sites
 (``backend="triton"``) run unchanged; it now means "the custom fused kernel".
-On a gfx950 device an eligible input whose kernel library is missing is a
-broken install, not an unsupported input: ``scaled_dot_product_attention``
-raises instead of silently falling back (rule 8), unless ``backend="torch"``.
+As in the reference, ``backend="auto"`` never raises for an unavailable
+backend: a missing or unloadable kernel library on a gfx950 device falls back
+to SDPA with the library's error as the reason (and one RuntimeWarning per
+process, since that is a broken install), while ``backend="triton"`` raises.
+
+Every finite scale is served, as the reference's kernel serves it
+(ref 812-815, 844-845): the kernels take a positive scale, so a negative one
+runs on the negated query (q.k scale = (-q).k |scale| exactly, dQ negated
+back) and a zero one (also a scale that rounds to zero in float32) runs on a
+zero query at scale 1 (every score is exactly 0, as with scale 0; dQ = 0).
 """
 
 from __future__ import annotations
 
+import ctypes
 import math
+import warnings
 from dataclasses import dataclass
 from numbers import Real
 from typing import Literal
@@ -51,11 +64,28 @@ from . import _lib, _ops
 _SUPPORTED_HEAD_DIMS = (32, 64, 128)  # the kernels' widths; smaller sizes are zero-padded
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
 _SUPPORTED_ARCH = "gfx950"
-# Per-head slabs are addressed with 32-bit byte offsets (include/fa_gfx950.h).
-_MAX_SLAB_BYTES = (1 << 31) - 4096 * 128 * 2
 Backend = Literal["auto", "triton", "torch"]
 
 _REASON_LIBRARY = "the gfx950 kernel library is not available"
+# The reference's first rule (attention.py:639-642), kept as the start of the
+# reason whenever cross-attention inputs fall back.
+_REASON_CROSS = "the custom kernel currently specializes in self-attention"
+
+
+def _sequence_fits(length: int, width: int) -> bool:
+    """The library's per-head slab bound for a sequence of ``length`` rows at
+    kernel width ``width`` (fa_capi.hip check_common / check_kv_length:
+    rows are addressed with 32-bit byte offsets, a 4096-row margin included)."""
+    return length * width * 2 + 4096 * width * 2 < (1 << 31)
+
+
+def _max_sequence(width: int) -> int:
+    """The longest sequence :func:`_sequence_fits` accepts at ``width``."""
+    return ((1 << 31) - 1 - 4096 * width * 2) // (width * 2)
+
+
+# fa_capi.hip check_common: batch * query heads < 2^30.
+_MAX_BATCH_HEADS = 1 << 30
 
 
 @dataclass(frozen=True)
@@ -134,6 +164,7 @@ class _DispatchFacts:
     value_head_dim: int
     device_type: str
     dtype: torch.dtype
+    batch_heads: int = 1             # batch * query heads
     arch: str | None = None          # filled in only for GPU tensors
     library_error: str | None = None  # None when libfa_gfx950.so loaded
 
@@ -145,7 +176,19 @@ def _kernel_width(head_dim: int, value_head_dim: int) -> int | None:
 
 
 def _decide(facts: _DispatchFacts) -> DispatchDecision:
-    """First-match dispatch rules (ref attention.py:639-670, module docstring)."""
+    """First-match dispatch rules (ref attention.py:639-670, module docstring).
+
+    Cross-attention inputs that fall back keep the reference's first-rule
+    reason in front (ref 639-642), then the rule that decided here."""
+    decision = _decide_rules(facts)
+    if decision.backend == "torch" and facts.q_len != facts.kv_len:
+        return DispatchDecision(
+            "torch", f"{_REASON_CROSS} (cross-attention runs on gfx950 only; here {decision.reason})"
+        )
+    return decision
+
+
+def _decide_rules(facts: _DispatchFacts) -> DispatchDecision:
     if facts.value_head_dim != facts.head_dim and (
         _kernel_width(facts.head_dim, facts.value_head_dim) is None
     ):
@@ -168,9 +211,13 @@ def _decide(facts: _DispatchFacts) -> DispatchDecision:
             f"head_dim must be one of ({supported}) for the Triton path, or a smaller size "
             "that is zero-padded to one of them",
         )
-    if max(facts.q_len, facts.kv_len) * width * 2 > _MAX_SLAB_BYTES:
+    if not (_sequence_fits(facts.q_len, width) and _sequence_fits(facts.kv_len, width)):
         return DispatchDecision(
             "torch", "the sequence is too long for the 32-bit addressed gfx950 kernel"
+        )
+    if facts.batch_heads >= _MAX_BATCH_HEADS:
+        return DispatchDecision(
+            "torch", "batch * heads is too large for the 32-bit addressed gfx950 kernel"
         )
     arch = facts.arch or ""
     if not arch.startswith(_SUPPORTED_ARCH):
@@ -220,6 +267,7 @@ def _dispatch(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> Di
         value_head_dim=value.shape[3],
         device_type=query.device.type,
         dtype=query.dtype,
+        batch_heads=query.shape[0] * query.shape[1],
         arch=arch,
         library_error=library_error,
     ))
@@ -235,16 +283,19 @@ class TritonAttention(torch.autograd.Function):
     Unless D and D_v are the same kernel size (32, 64 or 128), the kernels run
     at the smallest kernel size that holds both, on zero-padded copies of the
     operands (and of dO), and the outputs are sliced back: zero columns change
-    no dot product, and their gradients are exactly zero.
+    no dot product, and their gradients are exactly zero. A scale that is not
+    positive in float32 runs as :func:`_kernel_scale` describes.
     """
 
     @staticmethod
     def forward(ctx, query, key, value, causal, softmax_scale):
         head_dim, value_head_dim = query.shape[-1], value.shape[-1]
-        query, key, value, output, lse = _padded_forward(query, key, value, causal, softmax_scale)
+        query, key, value, output, lse, kscale, mode = _padded_forward(
+            query, key, value, causal, softmax_scale)
         ctx.save_for_backward(query, key, value, output, lse)
         ctx.head_dims = (head_dim, value_head_dim)
-        ctx.softmax_scale = float(softmax_scale)
+        ctx.softmax_scale = kscale
+        ctx.scale_mode = mode
         ctx.causal = bool(causal)
         return _unpad_output(output, value_head_dim)
 
@@ -256,6 +307,10 @@ class TritonAttention(torch.autograd.Function):
         grad_query, grad_key, grad_value = _ops.flash_bwd(
             query, key, value, output, lse, grad_output, ctx.causal, ctx.softmax_scale
         )
+        if ctx.scale_mode == "negate":
+            grad_query = -grad_query  # d/dq of (-q).k |scale|
+        elif ctx.scale_mode == "zero":
+            grad_query = torch.zeros_like(grad_query)  # the scores do not depend on q
         if head_dim != query.shape[-1]:
             grad_query, grad_key = grad_query[..., :head_dim], grad_key[..., :head_dim]
         if value_head_dim != query.shape[-1]:
@@ -270,17 +325,61 @@ def _forward_ad_active() -> bool:
     return getattr(torch.autograd.forward_ad, "_current_level", -1) >= 0
 
 
+_LOG2E = 1.4426950408889634  # the kernels' fp32 constant scale * log2(e) (fa_kernels.hpp)
+
+
+def _float32(x: float) -> float:
+    return ctypes.c_float(x).value
+
+
+def _kernel_scale(softmax_scale: float) -> tuple[float, str] | None:
+    """(positive kernel scale, query transform) serving ``softmax_scale``, or
+    None when float32 cannot hold it.
+
+    The library takes a scale whose float32 value c = scale * log2(e) is
+    positive and normal (fa_capi.hip check_scale). The reference's kernel takes
+    any finite scale (attention.py:812-815, 844-845), so:
+      * "plain":  scale as given;
+      * "negate": scale < 0 runs on -q at |scale|; every score (-q).k |scale|
+        equals q.k scale exactly (fp16 negation and round-to-nearest are
+        sign-symmetric, also for the backward's fp16(c q) and fp16(c k)
+        operands), and dQ is negated back;
+      * "zero":   |scale| below the float32 normal range (0 included) runs on
+        a zero query at scale 1: every score is exactly 0 either way (with a
+        subnormal scale every exp2 argument rounds to 0 in float32), so P, O,
+        LSE, dV and dK (= scale dS^T Q, which is 0) agree, and dQ (= scale dS K)
+        is 0.
+    """
+    s32 = _float32(softmax_scale)
+    if not math.isfinite(s32) or not math.isfinite(_float32(abs(s32) * _LOG2E)):
+        return None
+    if abs(s32) < 2.0 ** -126:
+        return 1.0, "zero"
+    if s32 < 0.0:
+        return -float(softmax_scale), "negate"
+    return float(softmax_scale), "plain"
+
+
 def _padded_forward(query, key, value, causal, softmax_scale):
-    """The forward launch at the kernel width: (padded q, k, v, O, LSE)."""
+    """The forward launch at the kernel width: (padded q, k, v, O, LSE, kernel
+    scale, scale mode), q as the kernels saw it (see :func:`_kernel_scale`)."""
     width = _kernel_width(query.shape[-1], value.shape[-1])
     if width is None:
         raise ValueError(
             f"head sizes {query.shape[-1]} / {value.shape[-1]}: the gfx950 kernels serve at "
             f"most {_SUPPORTED_HEAD_DIMS[-1]}"
         )
+    served = _kernel_scale(float(softmax_scale))
+    if served is None:
+        raise ValueError(f"scale {softmax_scale!r} overflows the kernels' float32 arithmetic")
+    kscale, mode = served
+    if mode == "negate":
+        query = -query
+    elif mode == "zero":
+        query = torch.zeros_like(query)
     query, key, value = (_pad_head(t, width) for t in (query, key, value))
-    output, lse = _ops.flash_fwd(query, key, value, bool(causal), float(softmax_scale))
-    return query, key, value, output, lse
+    output, lse = _ops.flash_fwd(query, key, value, bool(causal), kscale)
+    return query, key, value, output, lse, kscale, mode
 
 
 def _unpad_output(output: torch.Tensor, value_head_dim: int) -> torch.Tensor:
@@ -322,12 +421,12 @@ def scaled_dot_product_attention(
     """Compute scaled dot-product attention with safe backend selection.
 
     The custom gfx950 path supports forward/backward, causal and bidirectional
-    attention, arbitrary positive sequence lengths, and GQA, for float16 or
-    bfloat16 self- or cross-attention with head_dim and value head_dim up to 128
-    (32, 64 and 128 natively, other sizes zero-padded). Other inputs
-    fall back to PyTorch when ``backend="auto"``; ``backend="triton"`` requires
-    the custom kernel and raises RuntimeError otherwise; ``backend="torch"``
-    always uses PyTorch SDPA.
+    attention, arbitrary positive sequence lengths, GQA and any finite scale,
+    for float16 or bfloat16 self- or cross-attention with head_dim and value
+    head_dim up to 128 (32, 64 and 128 natively, other sizes zero-padded).
+    Other inputs fall back to PyTorch when ``backend="auto"``;
+    ``backend="triton"`` requires the custom kernel and raises RuntimeError
+    otherwise; ``backend="torch"`` always uses PyTorch SDPA.
     """
     if backend not in ("auto", "triton", "torch"):
         raise ValueError("backend must be one of: 'auto', 'triton', 'torch'")
@@ -347,23 +446,19 @@ def scaled_dot_product_attention(
         )
 
     decision = _dispatch(query, key, value)
+    softmax_scale = float(scale) if scale is not None else query.shape[-1] ** -0.5
+    if decision.backend == "triton" and _kernel_scale(softmax_scale) is None:
+        decision = DispatchDecision(
+            "torch", f"scale {softmax_scale!r} overflows the gfx950 kernel's float32 arithmetic")
     if decision.backend == "torch":
-        if backend == "triton" or decision.reason.startswith(_REASON_LIBRARY):
+        if backend == "triton":
             raise RuntimeError(f"Triton backend is unavailable: {decision.reason}")
+        if _REASON_LIBRARY in decision.reason:
+            _warn_library_once(decision.reason)
         return _torch_sdpa(
             query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
         )
 
-    softmax_scale = float(scale) if scale is not None else query.shape[-1] ** -0.5
-    if not softmax_scale > 0.0:
-        # The kernels fold the scale into a base-2 exponent and require scale > 0.
-        if backend == "triton":
-            raise RuntimeError(
-                "Triton backend is unavailable: the gfx950 kernel requires scale > 0"
-            )
-        return _torch_sdpa(
-            query, key, value, is_causal=is_causal, scale=scale, enable_gqa=enable_gqa
-        )
     query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
     if (torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
                                      or value.requires_grad)) or _forward_ad_active():
@@ -372,3 +467,15 @@ def scaled_dot_product_attention(
     # forward launch without the autograd Function's bookkeeping.
     output = _padded_forward(query, key, value, is_causal, softmax_scale)[3]
     return _unpad_output(output, value.shape[-1])
+
+
+_library_warned = False
+
+
+def _warn_library_once(reason: str) -> None:
+    """One RuntimeWarning per process when an eligible gfx950 input falls back
+    because the kernel library did not load (a broken install)."""
+    global _library_warned
+    if not _library_warned:
+        _library_warned = True
+        warnings.warn(f"falling back to torch SDPA: {reason}", RuntimeWarning, stacklevel=3)
