@@ -64,13 +64,19 @@ def build_command(output: Path = LIB_PATH, extra: tuple[str, ...] = ()) -> list[
     ]
 
 
-def build(output: Path = LIB_PATH, verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 into ``output`` (always recompiles)."""
-    tmp = output.with_name(output.name + ".tmp")
-    cmd = build_command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+def object_commands(obj_dir: Path, extra: tuple[str, ...] = ()) -> list[tuple[Path, list[str]]]:
+    """One ``hipcc -c`` per source (each object carries its own gfx950 code
+    object), so the translation units compile in parallel."""
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    out = []
+    for s in SOURCES:
+        obj = obj_dir / (Path(s).stem + ".o")
+        out.append((obj, [hipcc(), *flags, *extra, f"-I{INCLUDE_DIR}", "-c", "-o", str(obj),
+                          str(CSRC_DIR / s)]))
+    return out
+
+
+def _check(proc: subprocess.CompletedProcess) -> None:
     if proc.returncode != 0:
         # hipcc's host pass warns that it does not know the packed-fp32 feature;
         # only real diagnostics are worth showing.
@@ -80,6 +86,30 @@ def build(output: Path = LIB_PATH, verbose: bool = False) -> Path:
             if "packed-fp32-ops" not in ln
         ]
         raise RuntimeError("hipcc failed:\n" + "\n".join(lines[-60:]))
+
+
+def build(output: Path = LIB_PATH, verbose: bool = False) -> Path:
+    """Compile every HIP source for gfx950 into ``output`` (always recompiles).
+    The sources compile as separate objects in parallel and are then linked."""
+    import tempfile
+
+    tmp = output.with_name(output.name + ".tmp")
+    with tempfile.TemporaryDirectory(prefix="fa_build_") as d:
+        jobs = object_commands(Path(d))
+        procs = []
+        for _, cmd in jobs:
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                          text=True))
+        for (_, cmd), p in zip(jobs, procs):
+            out, err = p.communicate()
+            _check(subprocess.CompletedProcess(cmd, p.returncode, out, err))
+        link = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp),
+                *(str(o) for o, _ in jobs)]
+        if verbose:
+            print(" ".join(link), flush=True)
+        _check(subprocess.run(link, capture_output=True, text=True))
     os.replace(tmp, output)
     return output
 

@@ -142,14 +142,17 @@ def compile_library(arch: str = "gfx950") -> tuple[list[KernelUsage], str]:
     if arch not in SUPPORTED_ARCHS:
         raise ValueError(f"unsupported arch {arch!r}: the kernels are written for {SUPPORTED_ARCHS}")
     with tempfile.TemporaryDirectory() as tmp:
-        cmd = _build.build_command(Path(tmp) / "libfa_check.so",
-                                   extra=("-Rpass-analysis=kernel-resource-usage",))
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-    diag = "\n".join(ln for ln in (proc.stderr or "").splitlines()
+        jobs = _build.object_commands(Path(tmp),
+                                      extra=("-Rpass-analysis=kernel-resource-usage",))
+        procs = [subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+                 for _, cmd in jobs]
+        results = [(p.returncode, err) for p in procs for _, err in [p.communicate()]]
+    stderr = "\n".join(err or "" for _, err in results)
+    diag = "\n".join(ln for ln in stderr.splitlines()
                      if "packed-fp32-ops" not in ln and "remark:" not in ln)
-    if proc.returncode != 0:
+    if any(rc != 0 for rc, _ in results):
         raise RuntimeError("hipcc failed:\n" + diag[-6000:])
-    return parse_resource_usage(proc.stderr or ""), diag
+    return parse_resource_usage(stderr), diag
 
 
 def spilling_defaults(kernels: list[KernelUsage]) -> tuple[list[KernelUsage], list[str]]:
