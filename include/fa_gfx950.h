@@ -259,6 +259,27 @@ int fa_bwd_dq_delta_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_hal
                             int64_t D, float scale, int causal, void* workspace,
                             int64_t workspace_bytes, void* stream);
 
+/* Forward that allocates nothing: fa_fwd_ws's computation with the split-KV
+ * partials kept in a device array inside the library (64 MiB per GPU, held
+ * until the process ends) instead of a caller workspace. No counterpart in
+ * the reference; it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight decoding loops, harnesses that forbid
+ * hipMalloc). Same arguments, checks and results as fa_fwd_ws with a large
+ * enough workspace; shapes that do not split run as fa_fwd_kv. A shape whose
+ * partials need more than fa_fwd_noalloc_max_workspace_bytes() (as reported
+ * by fa_fwd_workspace_bytes) is rejected with FA_ERR_TOO_LARGE before any HIP
+ * call. The array's device address is looked up once per device, on the
+ * first call with that device current; `stream` must belong to the current
+ * device. All calls on one GPU share its array: calls that overlap in time on
+ * one GPU (different streams or threads) race and must be serialised by the
+ * caller. fp16 only. */
+int fa_fwd_noalloc(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                   fa_half_t* o, float* lse,
+                   int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                   float scale, int causal, void* stream);
+/* Bytes of the device array fa_fwd_noalloc uses (the largest workspace it serves). */
+int64_t fa_fwd_noalloc_max_workspace_bytes(void);
+
 /* Thread-local description of the last failure on the calling thread
  * ("" if none). The pointer stays valid until the next call on the thread. */
 const char* fa_last_error(void);

@@ -1,0 +1,87 @@
+"""fa_fwd_noalloc: the forward that allocates nothing (split-KV partials in a
+device array inside the library) against fa_fwd_ws with a caller workspace,
+called through the C ABI.
+
+The GPU test runs two decoding shapes that take the split path, the second
+smaller than the first, so the second call runs on the array the first left
+behind; each result must equal fa_fwd_ws's bit for bit (same kernels, same
+split, same summation order) and match the fp64 oracle at the north-star
+tolerances. The CPU test checks the size limit, which is enforced before any
+HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from fa_testutil import LSE_TOL, assert_close, make_inputs
+from oracle import oracle
+from triton_flash_attention import _lib
+
+# (B, Hq, Hkv, N_q, N_kv, D, causal); both take the split-KV forward.
+NOALLOC_CASES = [
+    (2, 8, 2, 3, 6000, 128, False),
+    (1, 4, 1, 2, 3000, 64, True),
+]
+
+
+def _note(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_noalloc_rejects_partials_beyond_the_scratch():
+    lib = _lib.load()
+    limit = lib.fa_fwd_noalloc_max_workspace_bytes()
+    assert limit == 64 << 20
+    # 511 query heads x one 128-query tile: 511 work-groups, split in two ranges.
+    shape = (1, 511, 1, 128, 4096, 128)
+    need = lib.fa_fwd_workspace_bytes(*shape, 0)
+    assert need > limit
+    fake = ctypes.c_void_p(0x10000)  # never dereferenced: rejected before any HIP call
+    rc = lib.fa_fwd_noalloc(fake, fake, fake, fake, fake, *shape, 128 ** -0.5, 0, None)
+    assert rc == _lib.FA_ERR_TOO_LARGE
+    msg = _lib.last_error()
+    assert "fa_fwd_noalloc" in msg and str(need) in msg and str(limit) in msg
+    # A bad argument is rejected the same way as by fa_fwd_ws.
+    assert lib.fa_fwd_noalloc(fake, fake, fake, fake, fake, 1, 4, 1, 2, 3000, 64, -1.0, 1,
+                              None) == _lib.FA_ERR_BAD_SCALE
+
+
+@pytest.mark.gpu
+def test_noalloc_forward_matches_workspace_forward_twice():
+    lib = _lib.load()
+    dev = torch.device("cuda")
+    for B, Hq, Hkv, N, Nkv, D, causal in NOALLOC_CASES:
+        tag = f"noalloc fwd B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} causal={causal}"
+        _note(tag)
+        need = lib.fa_fwd_workspace_bytes(B, Hq, Hkv, N, Nkv, D, int(causal))
+        assert 0 < need <= lib.fa_fwd_noalloc_max_workspace_bytes(), tag
+        q, k, v, _ = make_inputs(B, Hq, Hkv, N, D, seed=7 * N + Nkv + D, n_kv=Nkv)
+        qd, kd, vd = (t.to(dev) for t in (q, k, v))
+        scale = D ** -0.5
+        stream = torch.cuda.current_stream().cuda_stream
+        o_ws, o_na = torch.empty_like(qd), torch.empty_like(qd)
+        lse_ws = torch.empty((B, Hq, N), device=dev, dtype=torch.float32)
+        lse_na = torch.empty_like(lse_ws)
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        _lib.check(lib.fa_fwd_ws(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), o_ws.data_ptr(),
+                                 lse_ws.data_ptr(), B, Hq, Hkv, N, Nkv, D, scale, int(causal),
+                                 ws.data_ptr(), need, stream))
+        _lib.check(lib.fa_fwd_noalloc(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                      o_na.data_ptr(), lse_na.data_ptr(), B, Hq, Hkv, N, Nkv, D,
+                                      scale, int(causal), stream))
+        torch.cuda.synchronize()
+        assert torch.equal(o_na, o_ws), f"{tag}: O differs from fa_fwd_ws"
+        assert torch.equal(lse_na, lse_ws), f"{tag}: LSE differs from fa_fwd_ws"
+        o_ref, lse_ref = oracle.fwd(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                    causal, scale)
+        assert_close(f"{tag} o", o_na.double().cpu().numpy(), o_ref)
+        lse_err = float(np.max(np.abs(lse_na.double().cpu().numpy() - lse_ref)))
+        assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"
+        _note(f"{tag}: equal to fa_fwd_ws, lse err {lse_err:.2e}, partials {need} bytes")

@@ -10,10 +10,19 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <mutex>
 #include <numeric>
 
 #include "../../include/fa_gfx950.h"
 #include "fa_kernels.hpp"
+
+// Device-resident scratch of fa_fwd_noalloc: the split-KV forward's fp32
+// partials ([nsplit, B, Hq, N_q, D + 1]) for callers that cannot allocate.
+// Every GPU the library runs on holds its own copy for the life of the
+// process. In host code `scratch` only names the symbol; its device address
+// comes from hipGetSymbolAddress (scratch_address below), once per device.
+constexpr int64_t kNoallocScratchBytes = (int64_t)64 << 20;
+static __device__ __align__(256) float scratch[kNoallocScratchBytes / 4];
 
 namespace {
 
@@ -280,6 +289,38 @@ int64_t fwd_workspace_bytes(const FwdSplit& sp, int64_t B, int64_t Hq, int64_t N
   return sp.nsplit > 1 ? (int64_t)sp.nsplit * B * Hq * N * (D + 1) * 4 : 0;
 }
 
+
+constexpr int kMaxScratchDevices = 256;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first
+// call on that device (with it current) and kept. The launch stream must
+// belong to the current device, whose copy of the array the kernels get.
+int scratch_address(const char* name, hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_result(e, name);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if ((e = hipStreamGetDevice(stream, &sdev)) != hipSuccess) return hip_result(e, name);
+    if ((int)sdev != dev)
+      return fail(FA_ERR_BAD_SHAPE, "%s: the stream belongs to device %d but device %d is "
+                  "current; make the stream's device current", name, (int)sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(FA_ERR_BAD_SHAPE, "%s: device index %d out of range", name, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess)
+      return hip_result(e, name);
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -288,18 +329,33 @@ int fa_abi_version(void) { return FA_ABI_VERSION; }
 
 const char* fa_last_error(void) { return g_last_error; }
 
-static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
-                    const fa_half_t* v, fa_half_t* o, float* lse, int64_t B, int64_t Hq,
-                    int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
-                    void* stream, void* workspace = nullptr, int64_t workspace_bytes = 0) {
+// Argument checks of the forward entry points (no HIP call); on success *var
+// is the selected tiling and *need the split workspace bytes (0: one pass).
+static int fwd_check(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                     const fa_half_t* v, fa_half_t* o, float* lse, int64_t B, int64_t Hq,
+                     int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
+                     const fa::Variant** var, int64_t* need) {
   if (!q || !k || !v || !o || !lse) return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
   int rc = check_common(B, Hq, Hkv, N, D);
   if (rc) return rc;
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, lse}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
-  if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
+  *var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
+  if (!*var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
+  const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, fwd_pack(**var, Hq / Hkv, N));
+  *need = fwd_workspace_bytes(sp, B, Hq, N, D);
+  return FA_OK;
+}
+
+static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                    const fa_half_t* v, fa_half_t* o, float* lse, int64_t B, int64_t Hq,
+                    int64_t Hkv, int64_t N, int64_t Nkv, int64_t D, float scale, int causal,
+                    void* stream, void* workspace = nullptr, int64_t workspace_bytes = 0) {
+  const fa::Variant* var = nullptr;
+  int64_t need = 0;
+  int rc = fwd_check(dt, name, q, k, v, o, lse, B, Hq, Hkv, N, Nkv, D, scale, causal, &var, &need);
+  if (rc) return rc;
   fa::FwdArgs a;
   a.q = reinterpret_cast<const fa::half_t*>(q);
   a.k = reinterpret_cast<const fa::half_t*>(k);
@@ -318,7 +374,6 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   hipStream_t s = static_cast<hipStream_t>(stream);
   a.pack = fwd_pack(*var, Hq / Hkv, N);
   const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv, a.pack);
-  const int64_t need = fwd_workspace_bytes(sp, B, Hq, N, D);
   a.nsplit = 1;
   a.split_keys = (int)((Nkv + 127) / 128 * 128);
   a.part = nullptr;
@@ -616,6 +671,31 @@ int fa_bwd_dq_delta_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t
                          float scale, int causal, void* stream) {
   return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_bf16", q, k, v, o, dO, lse, delta, dq, B, Hq,
                        Hkv, N, N, D, scale, causal, stream);
+}
+
+// ---- forward without allocation: the split workspace is `scratch` --------
+int64_t fa_fwd_noalloc_max_workspace_bytes(void) { return kNoallocScratchBytes; }
+
+int fa_fwd_noalloc(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,
+                   float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                   int64_t D, float scale, int causal, void* stream) {
+  const char* name = "fa_fwd_noalloc";
+  const fa::Variant* var = nullptr;
+  int64_t need = 0;
+  int rc = fwd_check(fa::kF16, name, q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale, causal,
+                     &var, &need);
+  if (rc) return rc;
+  if (need > kNoallocScratchBytes)
+    return fail(FA_ERR_TOO_LARGE, "%s: this shape's split-KV partials need %lld bytes, more than "
+                "the %lld-byte device scratch; use fa_fwd_ws with a workspace of "
+                "fa_fwd_workspace_bytes", name, (long long)need, (long long)kNoallocScratchBytes);
+  if (need == 0)
+    return fwd_impl(fa::kF16, name, q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale, causal,
+                    stream);
+  void* ws = nullptr;
+  if ((rc = scratch_address(name, static_cast<hipStream_t>(stream), &ws))) return rc;
+  return fwd_impl(fa::kF16, name, q, k, v, o, lse, B, Hq, Hkv, N_q, N_kv, D, scale, causal,
+                  stream, ws, kNoallocScratchBytes);
 }
 
 int fa_fwd_ws(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, fa_half_t* o,

@@ -83,6 +83,9 @@ SIGNATURES["fa_fwd_ws_bf16"] = SIGNATURES["fa_fwd_ws"]
 SIGNATURES["fa_bwd_dq_workspace_bytes"] = SIGNATURES["fa_fwd_workspace_bytes"]
 SIGNATURES["fa_bwd_dq_delta_ws"] = (_INT, SIGNATURES["fa_bwd_dq_delta_kv"][1][:-1] + (_P, _I64, _P))
 SIGNATURES["fa_bwd_dq_delta_ws_bf16"] = SIGNATURES["fa_bwd_dq_delta_ws"]
+# Forward without allocation (device-resident scratch): fa_fwd_kv's arguments.
+SIGNATURES["fa_fwd_noalloc"] = SIGNATURES["fa_fwd_kv"]
+SIGNATURES["fa_fwd_noalloc_max_workspace_bytes"] = (_I64, ())
 
 
 class FlashAttentionError(RuntimeError):
