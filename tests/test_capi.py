@@ -182,7 +182,10 @@ def test_dkdv_workspace_sizing_and_rejection(lib):
     # GQA with 2 KV heads: split into partials; size = nsplit * 2 planes * B*Hkv*N*D * 4 bytes
     plane = 1 * 2 * 16381 * 32
     ws = lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 16381, 32, 1)
-    assert ws > 0 and ws % (2 * plane * 4) == 0 and ws // (2 * plane * 4) <= 8
+    assert ws > 0 and ws % (2 * plane * 4) == 0 and ws // (2 * plane * 4) <= 16
+    # causal launches this poorly filled split further than bidirectional ones
+    ws_bidir = lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 16381, 32, 0)
+    assert 0 < ws_bidir < ws and ws_bidir % (2 * plane * 4) == 0
     assert lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 16381, 48, 1) == _lib.FA_ERR_HEAD_DIM
     # a workspace smaller than required is rejected before any launch
     rc = lib.fa_bwd_dkdv_ws(P, P, P, P, P, P, P, P, 1, 8, 2, 16381, 32, 0.17, 1, P, ws - 16, None)
@@ -217,11 +220,12 @@ def test_cross_attention_workspace_follows_the_key_length(lib):
         B, Hq, Hkv, N, D, causal = args
         assert lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, N, D, causal) == \
             lib.fa_bwd_dkdv_workspace_bytes(*args)
-    # the split partials are [nsplit, 2, B, Hkv, N_kv, D] fp32: N_q does not enter
+    # the split partials are [nsplit, 2, B, Hkv, N_kv, D] fp32; N_q only sets how
+    # much work each key tile has, and too little (300 queries) is not split
     ws = lib.fa_bwd_dkdv_workspace_bytes_kv(1, 8, 2, 5000, 300, 64, 1)
     plane = 1 * 2 * 300 * 64 * 4
-    assert ws > 0 and ws % (2 * plane) == 0 and ws // (2 * plane) <= 8
-    assert lib.fa_bwd_dkdv_workspace_bytes_kv(1, 8, 2, 300, 300, 64, 1) == ws
+    assert ws > 0 and ws % (2 * plane) == 0 and ws // (2 * plane) <= 16
+    assert lib.fa_bwd_dkdv_workspace_bytes_kv(1, 8, 2, 300, 300, 64, 1) == 0
     rc = lib.fa_bwd_dkdv_ws_kv(P, P, P, P, P, P, P, P, 1, 8, 2, 5000, 300, 64, 0.125, 1,
                                P, ws - 16, None)
     assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()

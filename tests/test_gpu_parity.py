@@ -203,17 +203,17 @@ def test_constant_value_rows_give_zero_qk_gradients():
 def test_split_dkdv_matches_single_pass():
     """The split-and-reduce dK/dV (few key tiles per KV head) agrees with the
     single-pass kernel up to fp32 summation order."""
-    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 8, 2, 700, 64, seed=12))
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 8, 2, 1500, 64, seed=12))
     for causal in (False, True):
         o, lse = _ops.flash_fwd(q, k, v, causal, 0.125)
         delta = _ops.flash_bwd_preprocess(o, do)
         lib = _lib.load()
-        assert lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 700, 64, int(causal)) > 0
+        assert lib.fa_bwd_dkdv_workspace_bytes(1, 8, 2, 1500, 64, int(causal)) > 0
         dk1, dv1 = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, 0.125)  # split
         dk2, dv2 = torch.empty_like(k), torch.empty_like(v)
         rc = lib.fa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
                              lse.data_ptr(), delta.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
-                             1, 8, 2, 700, 64, 0.125, int(causal),
+                             1, 8, 2, 1500, 64, 0.125, int(causal),
                              torch.cuda.current_stream().cuda_stream)
         _lib.check(rc)
         torch.cuda.synchronize()
@@ -353,11 +353,13 @@ def test_tiling_sweep_times_every_variant_and_restores_the_table():
 def test_every_tiling_variant_matches_oracle(head_dim, causal):
     """Each compiled tiling of each kernel (fwd, dK/dV single-pass and split,
     dQ) against the oracle on a ragged GQA shape, not only the defaults."""
-    B, Hq, Hkv, N, D = 1, 4, 2, 300, head_dim
+    B, Hq, Hkv, N, D = 1, 8, 1, 520, head_dim
     q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=77, mult=0.5)
     qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
     scale = D ** -0.5
     lib = _lib.load()
+    # the op layer's dK/dV (dk1, dv1 below) takes the split path on this shape
+    assert lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, int(causal)) > 0
     stream = torch.cuda.current_stream().cuda_stream
     o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
     delta = _ops.flash_bwd_preprocess(o, dod)
@@ -714,7 +716,7 @@ def test_bf16_full_c2_matches_fp32_reference():
 CROSS_CASES = [
     # (B, Hq, Hkv, N_q, N_kv): fewer queries than keys (GQA, split dK/dV),
     # more queries than keys, one query, one key
-    (1, 4, 2, 300, 700),
+    (1, 8, 1, 600, 700),
     (2, 4, 4, 777, 129),
     (1, 2, 1, 1, 513),
     (1, 2, 2, 1000, 1),
@@ -877,7 +879,7 @@ def test_hip_graph_capture_replays_match_eager():
     to the eager result (the kernels are deterministic). The shape takes the
     split dK/dV path, so its workspace is allocated inside the capture; the
     launches record no memset."""
-    B, Hq, Hkv, N, D = 1, 8, 2, 700, 64
+    B, Hq, Hkv, N, D = 1, 8, 2, 1500, 64
     causal, scale = True, D ** -0.5
     q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=41))
     assert _lib.load().fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, 1) > 0

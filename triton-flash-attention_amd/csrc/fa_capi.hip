@@ -217,17 +217,33 @@ fa::BwdArgs bwd_args(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
 
 // dK/dV split factor: key tiles x KV heads below ~3 work-groups per CU (GQA
 // with few KV heads, or long causal sequences with few heads) split each key
-// tile's step sequence into up to 8 chunks that run as separate work-groups.
+// tile's step sequence (query head of the group x 32-query unit) into up to 16
+// chunks that run as separate work-groups. Under the causal mask the first key
+// tile carries about twice the mean work, and every tile is split into the
+// same number of chunks, so its chunks set the end of the launch: causal
+// launches with fewer than 384 work-groups aim at 4x as many (measured on
+// MI355X, B1 Hq8 Hkv2 N16381 D32: 471 us at 768, 374 at 1536, 352 at 3072).
+// Chunks keep at least 32 units on average, below which the partials and their
+// sum cost more than the balance returns (B2 Hq16 Hkv4 N2049 D64: 64 us at 4
+// chunks, 83 at 12).
 constexpr int64_t kSplitTargetWorkgroups = 768;
-constexpr int kMaxSplit = 8;
+constexpr int64_t kSplitTargetWorkgroupsCausal = 3072;
+constexpr int64_t kMinSplitUnits = 32;
+constexpr int kMaxSplit = 16;
 
-int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hkv, int64_t Nkv) {
+int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
+               int64_t Nkv, int causal) {
   const int64_t tiles = (Nkv + var.rows - 1) / var.rows;
   const int64_t wgs = tiles * B * Hkv;
   if (wgs >= kSplitTargetWorkgroups) return 1;
-  int64_t s = (kSplitTargetWorkgroups + wgs - 1) / wgs;
-  if (s > kMaxSplit) s = kMaxSplit;
-  return (int)s;
+  const int64_t target =
+      causal && 2 * wgs < kSplitTargetWorkgroups ? kSplitTargetWorkgroupsCausal : kSplitTargetWorkgroups;
+  int64_t s = (target + wgs - 1) / wgs;
+  // mean units per key tile: every query unit of the group (about half under the mask)
+  const int64_t units = (Hq / Hkv) * ((N + 31) / 32) / (causal ? 2 : 1);
+  s = std::min<int64_t>(s, std::max<int64_t>(1, units / kMinSplitUnits));
+  s = std::min<int64_t>(s, kMaxSplit);
+  return (int)std::max<int64_t>(s, 1);
 }
 
 int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D) {
@@ -451,7 +467,8 @@ static int64_t dkdv_workspace_impl(const char* name, int64_t B, int64_t Hq, int6
   for (int dt : {fa::kF16, fa::kBF16}) {
     const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-    bytes = std::max(bytes, split_workspace_bytes(dkdv_split(*var, B, Hkv, Nkv), B, Hkv, Nkv, D));
+    bytes = std::max(bytes, split_workspace_bytes(dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal),
+                                                  B, Hkv, Nkv, D));
   }
   return bytes;
 }
@@ -478,7 +495,7 @@ static int dkdv_ws_impl(int dt, const char* name, const fa_half_t* q, const fa_h
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
   a.dv = reinterpret_cast<fa::half_t*>(dv);
-  const int nsplit = dkdv_split(*var, B, Hkv, Nkv);
+  const int nsplit = dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal);
   const int64_t need = split_workspace_bytes(nsplit, B, Hkv, Nkv, D);
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto fn = reinterpret_cast<fa::bwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
