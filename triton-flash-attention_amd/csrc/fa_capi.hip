@@ -62,7 +62,8 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //   fwd : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 8 waves, 64; 2 = 4 waves, 32;
 //         3 = 2 waves, 64; 4 = 4 waves, 128; 5 = 4 waves, 32-key units, software-
 //         pipelined, 2 units per barrier (D <= 64); 6 = the same, 1 unit per
-//         barrier and a 6-slot ring (three work-groups per CU)
+//         barrier and a 6-slot ring (three work-groups per CU); 7 = 8 waves, 32-key
+//         units, pipelined, one work-group per CU (D = 128)
 //         (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;
@@ -73,7 +74,7 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //         faster under the causal mask)
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
-    {{6, 6}, {6, 6}, {2, 2}},  // fwd
+    {{6, 6}, {6, 6}, {7, 7}},  // fwd
     {{4, 4}, {4, 4}, {4, 4}},  // dkdv
     {{4, 4}, {4, 4}, {4, 1}},  // dq
 };
@@ -129,6 +130,30 @@ const fa::Variant* select_dq(int di, int causal, int64_t N, int dt) {
   const fa::Variant* vs = registry(fa::kDq, &count);
   if (kDqShortQueryVariant < count && usable(vs[kDqShortQueryVariant], di, causal, dt))
     return &vs[kDqShortQueryVariant];
+  return var;
+}
+
+// Forward tiling for a launch of N queries over BH query heads. At D = 128 the
+// table's 8-wave pipelined kernel (256 queries per work-group, one per CU) is
+// faster once the launch has long query sequences and enough work-groups; for
+// short queries or small launches the 4-wave tiling is (MI355X, one box:
+// B2 H32 N8192 causal 1091 vs 1181 us, bidirectional 1941 vs 2316 us; 512
+// queries x 64 heads against 8192 keys 204 vs 218 us; 128 queries x 256 heads
+// 270 vs 223 us; B1 H16 N1024 36 vs 33 us; decoding 2-6 % slower). A tiling
+// set with fa_set_tiling is used as set.
+constexpr int kFwdWideVariant = 7;
+constexpr int kFwdNarrowVariant = 2;
+
+const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt) {
+  int index = -1;
+  const fa::Variant* var = select(fa::kFwd, di, causal, &index, dt);
+  if (!var || index != kFwdWideVariant || g_override[fa::kFwd][di][causal ? 1 : 0] >= 0)
+    return var;
+  if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
+  int count = 0;
+  const fa::Variant* vs = registry(fa::kFwd, &count);
+  if (kFwdNarrowVariant < count && usable(vs[kFwdNarrowVariant], di, causal, dt))
+    return &vs[kFwdNarrowVariant];
   return var;
 }
 
@@ -357,7 +382,7 @@ static int fwd_check(int dt, const char* name, const fa_half_t* q, const fa_half
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, lse}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  *var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
+  *var = select_fwd(fa::head_dim_index(D), causal, N, B * Hq, dt);
   if (!*var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, fwd_pack(**var, Hq / Hkv, N));
   *need = fwd_workspace_bytes(sp, B, Hq, N, D);
@@ -415,7 +440,7 @@ int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, 
   // Enough for either element type (their tilings can differ when overridden).
   int64_t bytes = 0;
   for (int dt : {fa::kF16, fa::kBF16}) {
-    const fa::Variant* var = select(fa::kFwd, fa::head_dim_index(D), causal, nullptr, dt);
+    const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_workspace_bytes: no kernel for the selected tiling");
     const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, fwd_pack(*var, Hq / Hkv, N_q));
     bytes = std::max(bytes, fwd_workspace_bytes(sp, B, Hq, N_q, D));

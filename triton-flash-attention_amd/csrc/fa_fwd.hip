@@ -388,7 +388,10 @@ struct FwdPipeTile {
   static constexpr int STAGE = 2 * TILE;
   static constexpr int NSTAGE = UPS == 2 ? 8 : 6;
   static constexpr int AHEAD = UPS == 2 ? 5 : 4;  // units issued before step 0
-  static constexpr int WGS_PER_CU = UPS == 2 ? 2 : 3;
+  // Work-groups per CU: three 4-wave work-groups with one unit per barrier,
+  // two with two; an 8-wave work-group (D = 128: 16 KiB units) takes a CU alone.
+  static constexpr int WGS_PER_CU = NW == 8 ? 1 : (UPS == 2 ? 2 : 3);
+  static constexpr int WAVES_PER_SIMD = WGS_PER_CU * NW / 4;
   static_assert(UPS == 1 || UPS == 2, "units per step");
 };
 
@@ -397,7 +400,7 @@ constexpr bool fwd_pipe_tiling_ok() {
   using T = FwdPipeTile<D, NW, UPS>;
   constexpr int instr = T::TILE * 2 / 1024;
   return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
-         T::WGS_PER_CU * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && D <= 64;
+         T::WGS_PER_CU * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && (D <= 64 || NW == 8);
 }
 
 #ifndef FA_FWD_LEAD
@@ -423,7 +426,7 @@ __device__ __forceinline__ void static_for_fwd_issue(F&& f) {
 
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 __global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS>::WGS_PER_CU)))
+__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS>::WAVES_PER_SIMD)))
 void fwd_pipe_kernel(FwdArgs a) {
   using T = FwdPipeTile<D, NW, UPS>;
   using Dma = DmaStager<D, T::KT, NW>;
@@ -848,6 +851,8 @@ static const Variant kFwdVariants[] = {
     FA_FWD_VARIANT(4, 128),
     {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 2), FA_NO_ENTRIES}, kSplitsKv},
     {4, 128, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe_entry, BF16, 4, 1)},
+     kSplitsKv},
+    {8, 256, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 8, 1), FA_ENTRIES(fwd_pipe_entry, BF16, 8, 1)},
      kSplitsKv},
 };
 

@@ -28,15 +28,16 @@ from . import _build
 
 SUPPORTED_ARCHS = ("gfx950",)
 
-# Kernel instances the default tiling table (kDefault in csrc/fa_capi.hip)
-# selects, as demangled name prefixes, for D = 32, 64, 128, both mask modes
-# and both element types.
+# Kernel instances the default tiling table (kDefault in csrc/fa_capi.hip) and
+# its shape rules select, as demangled name prefixes, for D = 32, 64, 128, both
+# mask modes and both element types (at D = 128 the forward takes the 8-wave
+# pipelined kernel, and the 4-wave one for short queries).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
         for c in ("false", "true"):
             names += [f"fa::fwd_pipe_kernel<32, {c}, 4, 1, {e}>", f"fa::fwd_pipe_kernel<64, {c}, 4, 1, {e}>",
-                      f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
+                      f"fa::fwd_pipe_kernel<128, {c}, 8, 1, {e}>", f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
                       f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
                       f"fa::dq_pipe_kernel<32, {c}, 4, {e}>", f"fa::dq_pipe_kernel<64, {c}, 4, {e}>",
@@ -53,7 +54,7 @@ DEFAULT_KERNELS = _defaults()
 # 1 dK/dV, 2 dQ).
 DEFAULT_VARIANTS = {
     (0, 32, False): 6, (0, 32, True): 6, (0, 64, False): 6, (0, 64, True): 6,
-    (0, 128, False): 2, (0, 128, True): 2,
+    (0, 128, False): 7, (0, 128, True): 7,
     (1, 32, False): 4, (1, 32, True): 4, (1, 64, False): 4, (1, 64, True): 4,
     (1, 128, False): 4, (1, 128, True): 4,
     (2, 32, False): 4, (2, 32, True): 4, (2, 64, False): 4, (2, 64, True): 4,
