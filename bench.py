@@ -280,11 +280,18 @@ def main(argv=None) -> int:
         ends[i].record()
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
-    # Kernel pass: the same K steps again with HIP events around each launch on
-    # its own stream; the per-kernel durations and the roofline come from here.
+    # Kernel pass: the kernels of the same K steps again, each launched through
+    # its own entry point (forward; dQ with Delta; dK/dV reading that Delta: the
+    # launches fa_bwd makes, in this order, for shapes whose dK/dV launch does
+    # not split, c2 among them) with HIP events around each launch on its
+    # stream; the per-kernel durations and the roofline come from here.
+    qd, kd, vd = q.detach(), k.detach(), v.detach()
+    kscale = D ** -0.5
     with _ops.LaunchTimer() as timer:
         for _ in range(args.steps):
-            step()
+            o_k, lse_k = _ops.flash_fwd(qd, kd, vd, causal, kscale)
+            delta_k, _ = _ops.flash_bwd_dq_delta(qd, kd, vd, o_k, do, lse_k, causal, kscale)
+            _ops.flash_bwd_dkdv(qd, kd, vd, do, lse_k, delta_k, causal, kscale)
     torch.cuda.synchronize()
     step_ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
     total_ms = starts[0].elapsed_time(ends[-1])

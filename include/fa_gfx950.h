@@ -13,6 +13,8 @@
  *   fa_bwd_dkdv        replaces  _attn_bwd[grid](...) phase 1     attention.py:754-770 (kernel 428-505)
  *   fa_bwd_dq          replaces  _attn_bwd[grid](...) phase 2     attention.py:754-770 (kernel 507-573)
  *   fa_bwd_dq_delta    replaces  _attn_bwd_preprocess + phase 2   attention.py:736-744, 754-770
+ *   fa_bwd             replaces  all of TritonAttention.backward's launches
+ *                                (preprocess, then both phases)   attention.py:720-770
  *
  * Conventions shared by every entry point
  *   - Tensors are caller-owned device memory, contiguous, row-major:
@@ -47,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 5
+#define FA_ABI_VERSION 6
 
 /* Error codes returned before any HIP call is made. */
 #define FA_OK 0
@@ -258,6 +260,37 @@ int fa_bwd_dq_delta_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_hal
                             int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
                             int64_t D, float scale, int causal, void* workspace,
                             int64_t workspace_bytes, void* stream);
+
+/* Whole backward in one call, as TritonAttention.backward launches it
+ * (attention.py:720-770: the Delta preprocess, then one _attn_bwd grid whose
+ * programs run phase 1, dK/dV, and phase 2, dQ). Writes Delta ([B, Hq, N_q]
+ * fp32, the reference's preprocess output), dq, dk and dv; shapes, element
+ * type and key/value length as for fa_bwd_dq_delta_ws and fa_bwd_dkdv_ws_kv
+ * (N_q == N_kv for self-attention). fa_bwd_workspace_bytes returns the bytes of
+ * device workspace a call with these sizes needs (0 when nothing splits, for
+ * either element type): the split partials of dQ and of dK/dV. With
+ * workspace == NULL every launch runs in one pass; a non-NULL workspace smaller
+ * than needed is rejected (FA_ERR_BAD_SHAPE). Launch plan: dQ with Delta fused,
+ * then dK/dV (each split when its launch has few work-groups); except when
+ * dK/dV splits and dQ does not (head_dim 32 or 64, the default tilings):
+ * then Delta runs as its own pass and the dK/dV and dQ work-groups run in one
+ * combined launch, each filling the other's tail, before the dK/dV partials
+ * are summed. Results are identical for a given plan on every call
+ * (deterministic); the two plans differ only in how Delta reaches the dQ
+ * kernel, within fp32 rounding. Concurrent calls need separate workspaces. */
+int64_t fa_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                               int64_t D, int causal);
+int fa_bwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+           const fa_half_t* o, const fa_half_t* dO, const float* lse,
+           float* delta, fa_half_t* dq, fa_half_t* dk, fa_half_t* dv,
+           int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+           float scale, int causal, void* workspace, int64_t workspace_bytes, void* stream);
+int fa_bwd_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
+                const fa_half_t* o, const fa_half_t* dO, const float* lse,
+                float* delta, fa_half_t* dq, fa_half_t* dk, fa_half_t* dv,
+                int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                float scale, int causal, void* workspace, int64_t workspace_bytes,
+                void* stream);
 
 /* Forward that allocates nothing: fa_fwd_ws's computation with the split-KV
  * partials kept in a device array inside the library (64 MiB per GPU, held

@@ -250,6 +250,50 @@ def test_split_forward_workspace_sizing_and_rejection(lib):
     assert rc == _lib.FA_ERR_MISALIGNED
 
 
+def test_whole_backward_workspace_is_both_splits_and_rejects_bad_arguments(lib):
+    """fa_bwd's workspace holds the dQ partials, then (at a 256-byte boundary)
+    the dK/dV partials: the sum of what the per-kernel queries report, except
+    that in the combined plan (dK/dV splits, dQ does not) the dK/dV launch
+    takes at most as many chunks, and at least two."""
+    for args in [(4, 16, 16, 4096, 4096, 64, 1), (2, 16, 4, 2049, 2049, 64, 1),
+                 (1, 8, 2, 16381, 16381, 32, 1), (1, 32, 8, 128, 32768, 128, 0),
+                 (1, 8, 2, 5000, 300, 64, 1), (1, 4, 1, 700, 900, 64, 0),
+                 (1, 8, 2, 16381, 16381, 128, 1)]:
+        dq = lib.fa_bwd_dq_workspace_bytes(*args)
+        dkdv = lib.fa_bwd_dkdv_workspace_bytes_kv(*args)
+        assert dq >= 0 and dkdv >= 0
+        got = lib.fa_bwd_workspace_bytes(*args)
+        B, Hq, Hkv, N, Nkv, D, causal = args
+        if dkdv == 0 or dq > 0 or D == 128:  # the per-kernel launches, one after the other
+            assert got == (((dq + 255) // 256 * 256 + dkdv) if dkdv else dq), args
+        else:  # combined launch
+            plane = 2 * B * Hkv * Nkv * D * 4
+            assert got % plane == 0 and 2 <= got // plane and got <= dkdv, args
+    assert lib.fa_bwd_workspace_bytes(4, 16, 16, 4096, 4096, 64, 1) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 8, 2, 16381, 16381, 48, 1) == _lib.FA_ERR_HEAD_DIM
+    assert lib.fa_bwd_workspace_bytes(1, 8, 2, 16381, 0, 32, 1) == _lib.FA_ERR_BAD_SHAPE
+    # fa_bwd(q, k, v, o, dO, lse, delta, dq, dk, dv, B, Hq, Hkv, N_q, N_kv, D, scale,
+    #        causal, workspace, workspace_bytes, stream)
+    ptrs = [P] * 10
+    shape = (2, 16, 4, 2049, 2049, 64)
+    ws = lib.fa_bwd_workspace_bytes(*shape, 1)
+    assert ws > 0
+    rc = lib.fa_bwd(*ptrs[:9], None, *shape, 0.125, 1, P, ws, None)
+    assert rc == _lib.FA_ERR_NULL_POINTER and "fa_bwd: null pointer" in _lib.last_error()
+    rc = lib.fa_bwd(*ptrs, 2, 16, 3, 2049, 2049, 64, 0.125, 1, P, ws, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE
+    rc = lib.fa_bwd_bf16(*ptrs, 2, 16, 4, 2049, 2049, 96, 0.125, 1, P, ws, None)
+    assert rc == _lib.FA_ERR_HEAD_DIM
+    rc = lib.fa_bwd(P, P, P, P, P, P + 8, P, P, P, P, *shape, 0.125, 1, P, ws, None)
+    assert rc == _lib.FA_ERR_MISALIGNED
+    rc = lib.fa_bwd(*ptrs, *shape, 0.0, 1, P, ws, None)
+    assert rc == _lib.FA_ERR_BAD_SCALE
+    rc = lib.fa_bwd(*ptrs, *shape, 0.125, 1, P, ws - 16, None)
+    assert rc == _lib.FA_ERR_BAD_SHAPE and "smaller than" in _lib.last_error()
+    rc = lib.fa_bwd_bf16(*ptrs, *shape, 0.125, 1, P + 4, ws, None)
+    assert rc == _lib.FA_ERR_MISALIGNED
+
+
 def test_split_dq_workspace_sizing_and_rejection(lib):
     assert lib.fa_bwd_dq_workspace_bytes(4, 16, 16, 4096, 4096, 64, 1) == 0
     assert lib.fa_bwd_dq_workspace_bytes(1, 32, 8, 128, 700, 128, 0) == 0  # too few keys

@@ -221,6 +221,105 @@ def test_split_dkdv_matches_single_pass():
         assert_close("split dv", dv1.float(), dv2.float(), max_abs=2e-3, rel_l2=1e-3)
 
 
+# (B, Hq, Hkv, N_q, N_kv, D, causal): the dK/dV launch splits and dQ does not,
+# so fa_bwd runs the Delta pass and the combined dK/dV + dQ launch.
+PAIR_CASES = [
+    (1, 8, 2, 1500, 1500, 64, True),
+    (1, 8, 2, 1500, 1500, 64, False),
+    (2, 16, 4, 2049, 2049, 64, True),
+    (2, 16, 4, 2049, 2049, 32, True),
+    (1, 8, 2, 1000, 1300, 64, True),
+    (1, 4, 1, 900, 700, 32, False),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("case", PAIR_CASES, ids=lambda c: "B{}Hq{}Hkv{}Nq{}Nkv{}D{}".format(
+    *c[:6]) + ("causal" if c[6] else "bidir"))
+def test_combined_backward_launch_matches_separate_launches_and_reference(case, dtype):
+    """The combined launch runs the very dK/dV and dQ work-groups of the
+    separate launches: with the same Delta its dQ is bitwise that of fa_bwd_dq
+    (self-attention), and its dK, dV those of the split fa_bwd_dkdv_ws when
+    both split the key tiles into as many chunks (else equal to fp32
+    summation order); two calls are
+    bitwise identical; and all three match the fp32 reference (the oracle for
+    cross-attention, through the public API)."""
+    B, Hq, Hkv, N, Nkv, D, causal = case
+    tag = f"combined backward {case} {str(dtype)[6:]}"
+    _note(tag)
+    lib = _lib.load()
+    c = int(causal)
+    assert lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, Nkv, D, c) > 0  # dK/dV splits
+    assert lib.fa_bwd_dq_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c) == 0  # dQ does not
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D,
+                                                    n_kv=Nkv, dtype=dtype))
+    scale = D ** -0.5
+    o, lse = _ops.flash_fwd(q, k, v, causal, scale)
+    dq, dk, dv = _ops.flash_bwd(q, k, v, o, lse, do, causal, scale)
+    again = _ops.flash_bwd(q, k, v, o, lse, do, causal, scale)
+    delta = _ops.flash_bwd_preprocess(o, do)
+    dk_s, dv_s = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, scale)
+    if N == Nkv:
+        dq_s = _ops.flash_bwd_dq(q, k, v, do, lse, delta, causal, scale)
+    else:  # no Delta-reading dQ entry for cross-attention: the fused one, to fp32 rounding
+        dq_s = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, causal, scale)[1]
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), again):
+        assert torch.equal(a, b), f"{tag}: {name} differs between two calls"
+    if lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c) == \
+            lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, Nkv, D, c):  # same chunking
+        assert torch.equal(dk, dk_s) and torch.equal(dv, dv_s), f"{tag}: dK/dV differ"
+    else:  # fewer chunks beside dQ: the same sums in another fp32 order
+        assert_close(f"{tag} dk vs split launch", dk.float(), dk_s.float(), max_abs=2e-3,
+                     rel_l2=1e-3)
+        assert_close(f"{tag} dv vs split launch", dv.float(), dv_s.float(), max_abs=2e-3,
+                     rel_l2=1e-3)
+    if N == Nkv:
+        assert torch.equal(dq, dq_s), f"{tag}: dQ differs from fa_bwd_dq"
+    else:
+        assert_close(f"{tag} dq vs fused-Delta dQ", dq.float(), dq_s.float(),
+                     max_abs=2e-3, rel_l2=1e-3)
+    if N != Nkv:  # the public API on the same inputs against the oracle's cross-attention
+        cpu = tuple(t.cpu() for t in (q, k, v, do))
+        check = check_bf16_against_oracle if dtype == torch.bfloat16 else check_against_oracle
+        check(run_kernel(*cpu, causal), *cpu, causal, tag=tag)
+        return
+    ref = torch_reference_fp32(q, k, v, do, causal, o16=o)
+    tols = (dict(max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL)
+            if dtype == torch.bfloat16 else {})
+    for name, a in (("dq", dq), ("dk", dk), ("dv", dv)):
+        ma, rl = assert_close(f"{tag} {name}", a.float(), ref[name], **tols)
+        _note(f"  {name}: max-abs {ma:.2e} rel-L2 {rl:.2e}")
+
+
+def test_whole_backward_without_a_workspace_runs_one_pass():
+    """fa_bwd with no workspace on a shape that would take the combined plan
+    runs every launch in one pass (fused-Delta dQ, unsplit dK/dV): the same
+    results as those launches, within tolerance of the combined plan."""
+    B, Hq, Hkv, N, D = 1, 8, 2, 1500, 64
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=77))
+    lib = _lib.load()
+    o, lse = _ops.flash_fwd(q, k, v, True, 0.125)
+    delta, dq, dk, dv = (torch.empty((B, Hq, N), device=DEV), torch.empty_like(q),
+                         torch.empty_like(k), torch.empty_like(v))
+    rc = lib.fa_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
+                    lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                    B, Hq, Hkv, N, N, D, 0.125, 1, None, 0, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc)
+    delta1, dq1 = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, True, 0.125)
+    dk1, dv1 = torch.empty_like(k), torch.empty_like(v)
+    _lib.check(lib.fa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                               lse.data_ptr(), delta1.data_ptr(), dk1.data_ptr(), dv1.data_ptr(),
+                               B, Hq, Hkv, N, D, 0.125, 1, torch.cuda.current_stream().cuda_stream))
+    dq2, dk2, dv2 = _ops.flash_bwd(q, k, v, o, lse, do, True, 0.125)  # combined plan
+    torch.cuda.synchronize()
+    assert torch.equal(delta, delta1) and torch.equal(dq, dq1)
+    assert torch.equal(dk, dk1) and torch.equal(dv, dv1)
+    for name, a, b in (("dq", dq, dq2), ("dk", dk, dk2), ("dv", dv, dv2)):
+        assert_close(f"one pass vs combined {name}", a.float(), b.float(), max_abs=2e-3,
+                     rel_l2=1e-3)
+
+
 def test_short_query_dq_rule_matches_oracle_and_the_pipelined_tiling():
     """dQ at D = 128 without the mask runs the classic tiling for fewer than
     128 queries (a shape rule over the table): results agree with the oracle

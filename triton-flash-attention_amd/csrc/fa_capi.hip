@@ -256,6 +256,22 @@ constexpr int64_t kSplitTargetWorkgroupsCausal = 3072;
 constexpr int64_t kMinSplitUnits = 32;
 constexpr int kMaxSplit = 16;
 
+// Chunks per key tile for a launch whose dK/dV work-groups, `wgs` unsplit,
+// should number about `target` (at most 16 chunks, each with at least
+// `min_units` 32-query units on average).
+int64_t chunks_for(int64_t target, int64_t wgs, int64_t units, int64_t min_units) {
+  int64_t s = (target + wgs - 1) / wgs;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, units / min_units));
+  s = std::min<int64_t>(s, kMaxSplit);
+  return std::max<int64_t>(s, 1);
+}
+
+// mean 32-query units per key tile: every query unit of the group (about
+// half under the mask)
+int64_t dkdv_tile_units(int64_t Hq, int64_t Hkv, int64_t N, int causal) {
+  return (Hq / Hkv) * ((N + 31) / 32) / (causal ? 2 : 1);
+}
+
 int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
                int64_t Nkv, int causal) {
   const int64_t tiles = (Nkv + var.rows - 1) / var.rows;
@@ -263,12 +279,7 @@ int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t Hkv, int64
   if (wgs >= kSplitTargetWorkgroups) return 1;
   const int64_t target =
       causal && 2 * wgs < kSplitTargetWorkgroups ? kSplitTargetWorkgroupsCausal : kSplitTargetWorkgroups;
-  int64_t s = (target + wgs - 1) / wgs;
-  // mean units per key tile: every query unit of the group (about half under the mask)
-  const int64_t units = (Hq / Hkv) * ((N + 31) / 32) / (causal ? 2 : 1);
-  s = std::min<int64_t>(s, std::max<int64_t>(1, units / kMinSplitUnits));
-  s = std::min<int64_t>(s, kMaxSplit);
-  return (int)std::max<int64_t>(s, 1);
+  return (int)chunks_for(target, wgs, dkdv_tile_units(Hq, Hkv, N, causal), kMinSplitUnits);
 }
 
 int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D) {
@@ -634,6 +645,143 @@ int fa_bwd_dq_delta_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_hal
                             void* workspace, int64_t workspace_bytes, void* stream) {
   return dq_delta_impl(fa::kBF16, "fa_bwd_dq_delta_ws_bf16", q, k, v, o, dO, lse, delta, dq, B,
                        Hq, Hkv, N_q, N_kv, D, scale, causal, stream, workspace, workspace_bytes);
+}
+
+// ---- whole backward ---------------------------------------------------------
+// Launch plan of one backward call: the dQ and dK/dV tilings, their splits,
+// whether they run as one combined launch, and the workspace layout
+// [dQ partials | dK/dV partials at a 256-byte boundary].
+struct BwdPlan {
+  const fa::Variant* dq;
+  const fa::Variant* dkdv;
+  FwdSplit dq_split;
+  int dkdv_nsplit;
+  bool pair;
+  int64_t dq_bytes;
+  int64_t dkdv_offset;
+  int64_t dkdv_bytes;
+  int64_t total;
+};
+
+// A dK/dV launch that splits (too few key tiles) next to a dQ launch that
+// does not runs best as one combined launch (fa_bwd_pair.hip): MI355X,
+// B2 Hq16 Hkv4 N2049 D64 causal, backward 106 -> 97 us already with the two
+// launches on two streams, while with launches that fill the GPU (B4 H16
+// N4096) running them together is slower (505 vs 478 us).
+// Work-groups (dK/dV chunks plus dQ) the combined launch aims at, and the
+// fewest 32-query units per dK/dV chunk on average.
+constexpr int64_t kPairTargetWorkgroups = 3072;
+constexpr int64_t kPairMinSplitUnits = 32;
+
+bool plan_bwd(int dt, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv, int64_t D,
+              int causal, BwdPlan* p) {
+  const int di = fa::head_dim_index(D);
+  p->dq = select_dq(di, causal, N, dt);
+  p->dkdv = select(fa::kDkdv, di, causal, nullptr, dt);
+  if (!p->dq || !p->dkdv) return false;
+  p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv);
+  p->dkdv_nsplit = dkdv_split(*p->dkdv, B, Hq, Hkv, N, Nkv, causal);
+  p->pair = p->dkdv_nsplit > 1 && p->dq_split.nsplit == 1 && (p->dq->flags & fa::kPairs) &&
+            (p->dkdv->flags & fa::kPairs) && p->dq->waves == fa::bwd_pair_waves() &&
+            p->dkdv->waves == fa::bwd_pair_waves() &&
+            fa::bwd_pair_launcher(dt, di, causal) != nullptr;
+  if (p->pair) {
+    // Beside the dQ work-groups the dK/dV chunks need not fill the GPU alone
+    // (still split: the plan exists for launches whose key tiles are too few).
+    const int64_t dkdv_wgs = (Nkv + p->dkdv->rows - 1) / p->dkdv->rows * B * Hkv;
+    const int64_t dq_wgs = (N + p->dq->rows - 1) / p->dq->rows * B * Hq;
+    p->dkdv_nsplit = (int)std::max<int64_t>(
+        2, chunks_for(std::max<int64_t>(kPairTargetWorkgroups - dq_wgs, dkdv_wgs), dkdv_wgs,
+                      dkdv_tile_units(Hq, Hkv, N, causal), kPairMinSplitUnits));
+  }
+  p->dq_bytes = dq_workspace_bytes(p->dq_split, B, Hq, N, D);
+  p->dkdv_offset = (p->dq_bytes + 255) / 256 * 256;
+  p->dkdv_bytes = split_workspace_bytes(p->dkdv_nsplit, B, Hkv, Nkv, D);
+  p->total = p->dkdv_bytes > 0 ? p->dkdv_offset + p->dkdv_bytes : p->dq_bytes;
+  return true;
+}
+
+int64_t fa_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+                               int64_t D, int causal) {
+  int rc = check_common(B, Hq, Hkv, N_q, D);
+  if (rc) return rc;
+  if ((rc = check_kv_length(N_kv, D))) return rc;
+  int64_t bytes = 0;  // enough for either element type
+  for (int dt : {fa::kF16, fa::kBF16}) {
+    BwdPlan p;
+    if (!plan_bwd(dt, B, Hq, Hkv, N_q, N_kv, D, causal, &p))
+      return fail(FA_ERR_BAD_TILING, "fa_bwd_workspace_bytes: no kernel for the selected tiling");
+    bytes = std::max(bytes, p.total);
+  }
+  return bytes;
+}
+
+static int bwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t* k,
+                    const fa_half_t* v, const fa_half_t* o, const fa_half_t* dO,
+                    const float* lse, float* delta, fa_half_t* dq, fa_half_t* dk, fa_half_t* dv,
+                    int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv, int64_t D,
+                    float scale, int causal, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
+  if (!q || !k || !v || !o || !dO || !lse || !delta || !dq || !dk || !dv)
+    return fail(FA_ERR_NULL_POINTER, "%s: null pointer", name);
+  int rc = check_common(B, Hq, Hkv, N, D);
+  if (rc) return rc;
+  if ((rc = check_kv_length(Nkv, D))) return rc;
+  if ((rc = check_aligned(name, {q, k, v, o, dO, lse, delta, dq, dk, dv}))) return rc;
+  if ((rc = check_scale(scale))) return rc;
+  BwdPlan p;
+  if (!plan_bwd(dt, B, Hq, Hkv, N, Nkv, D, causal, &p))
+    return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
+  char* ws = static_cast<char*>(workspace);
+  if (ws != nullptr && p.total > 0) {
+    if (workspace_bytes < p.total)
+      return fail(FA_ERR_BAD_SHAPE, "%s: workspace of %lld bytes is smaller than the %lld bytes "
+                  "fa_bwd_workspace_bytes reports", name, (long long)workspace_bytes,
+                  (long long)p.total);
+    if ((rc = check_aligned(name, {workspace}))) return rc;
+  }
+  if (p.pair && ws != nullptr) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const auto* o16 = reinterpret_cast<const fa::half_t*>(o);
+    const auto* do16 = reinterpret_cast<const fa::half_t*>(dO);
+    hipError_t e = fa::launch_preprocess(o16, do16, delta, B * Hq * N, (int)D, dt, s);
+    if (e != hipSuccess) return launch_result(e, name);
+    fa::BwdArgs ad = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
+    ad.dk = reinterpret_cast<fa::half_t*>(dk);
+    ad.dv = reinterpret_cast<fa::half_t*>(dv);
+    ad.nsplit = p.dkdv_nsplit;
+    ad.part = reinterpret_cast<float*>(ws + p.dkdv_offset);
+    fa::BwdArgs aq = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
+    aq.dq = reinterpret_cast<fa::half_t*>(dq);
+    e = fa::bwd_pair_launcher(dt, fa::head_dim_index(D), causal)(ad, aq, s);
+    if (e != hipSuccess) return launch_result(e, name);
+    return launch_result(
+        fa::launch_split_reduce(ad.part, ad.dk, ad.dv, B * Hkv * Nkv * D, p.dkdv_nsplit, dt, s),
+        name);
+  }
+  rc = dq_delta_impl(dt, name, q, k, v, o, dO, lse, delta, dq, B, Hq, Hkv, N, Nkv, D, scale,
+                     causal, stream, p.dq_bytes > 0 ? ws : nullptr, p.dq_bytes);
+  if (rc) return rc;
+  return dkdv_ws_impl(dt, name, q, k, v, dO, lse, delta, dk, dv, B, Hq, Hkv, N, Nkv, D, scale,
+                      causal, p.dkdv_bytes > 0 && ws ? ws + p.dkdv_offset : nullptr,
+                      p.dkdv_bytes, stream);
+}
+
+int fa_bwd(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* o,
+           const fa_half_t* dO, const float* lse, float* delta, fa_half_t* dq, fa_half_t* dk,
+           fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv,
+           int64_t D, float scale, int causal, void* workspace, int64_t workspace_bytes,
+           void* stream) {
+  return bwd_impl(fa::kF16, "fa_bwd", q, k, v, o, dO, lse, delta, dq, dk, dv, B, Hq, Hkv, N_q,
+                  N_kv, D, scale, causal, workspace, workspace_bytes, stream);
+}
+int fa_bwd_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v, const fa_half_t* o,
+                const fa_half_t* dO, const float* lse, float* delta, fa_half_t* dq,
+                fa_half_t* dk, fa_half_t* dv, int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q,
+                int64_t N_kv, int64_t D, float scale, int causal, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  return bwd_impl(fa::kBF16, "fa_bwd_bf16", q, k, v, o, dO, lse, delta, dq, dk, dv, B, Hq, Hkv,
+                  N_q, N_kv, D, scale, causal, workspace, workspace_bytes, stream);
 }
 
 // ---- exported launches: fp16 (the reference's dtype) and bf16 twins ------

@@ -110,11 +110,22 @@ enum DType { kF16 = 0, kBF16 = 1 };
 constexpr int kFusesDelta = 1;
 // The forward variant has the split-KV mode (FwdArgs::nsplit > 1).
 constexpr int kSplitsKv = 2;
+// The backward variant (pipelined dK/dV or dQ, D <= 64) also runs in the
+// combined launch of bwd_pair_launcher.
+constexpr int kPairs = 4;
 
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);
 const Variant* dkdv_variants(int* count);
 const Variant* dq_variants(int* count);
+
+// Combined dK/dV + dQ launch (fa_bwd_pair.hip): `dkdv` as for the pipelined
+// dK/dV launch (split mode allowed), `dq` as for the pipelined dQ launch in one
+// pass that reads Delta (o == nullptr). Null for head sizes other than 32, 64.
+typedef hipError_t (*bwd_pair_launch_fn)(const BwdArgs& dkdv, const BwdArgs& dq, hipStream_t);
+bwd_pair_launch_fn bwd_pair_launcher(int dtype, int di, int causal);
+// Waves per work-group of the combined launch (both kinds' tiling).
+int bwd_pair_waves();
 
 // Sum of the nsplit fp32 partial planes into fp16 dK, dV (fixed order).
 // dtype: kF16 or kBF16 (the element type of the 16-bit tensors).

@@ -20,8 +20,8 @@ INCLUDE_DIR = PACKAGE_DIR.parent.parent / "include"
 LIB_NAME = "libfa_gfx950.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
 
-SOURCES = ("fa_fwd.hip", "fa_bwd.hip", "fa_capi.hip")
-HEADERS = ("fa_common.hpp", "fa_kernels.hpp")
+SOURCES = ("fa_fwd.hip", "fa_bwd.hip", "fa_bwd_pair.hip", "fa_capi.hip")
+HEADERS = ("fa_common.hpp", "fa_kernels.hpp", "fa_bwd_pipe.hpp")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in generated code.
 # -amdgpu-mfma-vgpr-form: MFMA accumulators live in ordinary VGPRs, so the

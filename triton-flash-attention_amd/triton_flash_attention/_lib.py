@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 FA_OK = 0
 FA_ERR_NULL_POINTER = -1
@@ -83,6 +83,14 @@ SIGNATURES["fa_fwd_ws_bf16"] = SIGNATURES["fa_fwd_ws"]
 SIGNATURES["fa_bwd_dq_workspace_bytes"] = SIGNATURES["fa_fwd_workspace_bytes"]
 SIGNATURES["fa_bwd_dq_delta_ws"] = (_INT, SIGNATURES["fa_bwd_dq_delta_kv"][1][:-1] + (_P, _I64, _P))
 SIGNATURES["fa_bwd_dq_delta_ws_bf16"] = SIGNATURES["fa_bwd_dq_delta_ws"]
+# Whole backward: q, k, v, o, dO, lse, delta, dq, dk, dv, B, Hq, Hkv, N_q, N_kv, D, scale,
+# causal, workspace, its size, stream.
+SIGNATURES["fa_bwd_workspace_bytes"] = SIGNATURES["fa_fwd_workspace_bytes"]
+SIGNATURES["fa_bwd"] = (
+    _INT,
+    (_P,) * 10 + (_I64, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P, _I64, _P),
+)
+SIGNATURES["fa_bwd_bf16"] = SIGNATURES["fa_bwd"]
 # Forward without allocation (device-resident scratch): fa_fwd_kv's arguments.
 SIGNATURES["fa_fwd_noalloc"] = SIGNATURES["fa_fwd_kv"]
 SIGNATURES["fa_fwd_noalloc_max_workspace_bytes"] = (_I64, ())

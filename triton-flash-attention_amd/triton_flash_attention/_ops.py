@@ -12,6 +12,7 @@ Reference launches replaced (triton_flash_attention/attention.py):
     flash_bwd_dkdv       -> _attn_bwd[grid], phase 1     754-770 (428-505)
     flash_bwd_dq         -> _attn_bwd[grid], phase 2     754-770 (507-573)
     flash_bwd_dq_delta   -> preprocess + phase 2         736-744, 754-770
+    flash_bwd            -> preprocess + both phases     720-770 (TritonAttention.backward)
 
 The forward and the backward also serve cross-attention (key/value length
 N_kv != query length N), which the reference sends to torch SDPA
@@ -311,10 +312,14 @@ def flash_bwd_dq_delta(q, k, v, o, do, lse, causal: bool, scale: float):
 def flash_bwd(
     q, k, v, o, lse, do, causal: bool, scale: float
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """dQ, dK, dV: dQ together with Delta (the reference's preprocess), then
-    dK/dV, which reads that Delta — what :func:`flash_bwd_dq_delta` followed by
-    :func:`flash_bwd_dkdv` do, with one pass of checks, allocations and stream
-    lookup for both launches (the host cost matters at small shapes)."""
+    """dQ, dK, dV of one backward through the library's whole-backward entry
+    point ``fa_bwd`` (all of TritonAttention.backward's launches,
+    attention.py:720-770), with one pass of checks, allocations and stream
+    lookup (the host cost matters at small shapes). The split workspace, when
+    the shape needs one, comes from the caching allocator. The library picks
+    the launch plan: dQ with Delta fused, then dK/dV reading that Delta; or,
+    when the dK/dV launch has too few key tiles to fill the GPU and splits
+    while dQ does not, a Delta pass and one combined dK/dV + dQ launch."""
     dt = _elem_dtype(q, "q")
     for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("dO", do)):
         _require(t, name, dt, q.device)
@@ -327,18 +332,7 @@ def flash_bwd(
     q, k, v, o, do, lse = _aligned_all(q, k, v, o, do, lse)
     lib = _lib.load()
     c = int(bool(causal))
-    dq_ws_bytes = lib.fa_bwd_dq_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c)
-    if dq_ws_bytes < 0:
-        _lib.check(dq_ws_bytes)
-    if dq_ws_bytes > 0:  # few work-groups: dQ splits its keys over a workspace
-        dq_fn, lengths = _entry(lib, "fa_bwd_dq_delta_ws", dt), (N, Nkv)
-    else:
-        dq_fn, lengths = _entry_lengths(lib, "fa_bwd_dq_delta", dt, N, Nkv)
-    dkdv_fn, dkdv_lengths = _entry_lengths(lib, "fa_bwd_dkdv_ws", dt, N, Nkv)
-    if N == Nkv:
-        ws_bytes = lib.fa_bwd_dkdv_workspace_bytes(B, Hq, Hkv, N, D, c)
-    else:
-        ws_bytes = lib.fa_bwd_dkdv_workspace_bytes_kv(B, Hq, Hkv, N, Nkv, D, c)
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, Nkv, D, c)
     if ws_bytes < 0:
         _lib.check(ws_bytes)
     delta = torch.empty((B, Hq, N), device=q.device, dtype=torch.float32)
@@ -346,24 +340,12 @@ def flash_bwd(
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
-    dq_extra = ()
-    if dq_ws_bytes > 0:
-        dq_ws = torch.empty(dq_ws_bytes, dtype=torch.uint8, device=q.device)
-        dq_extra = (dq_ws.data_ptr(), dq_ws_bytes)
-    scale = float(scale)
     with _device_guard(q.device):
-        stream = _stream(q)
         _lib.check(_launch(
-            "dq", dq_fn,
+            "bwd", _entry(lib, "fa_bwd", dt),
             q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(),
-            lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
-            B, Hq, Hkv, *lengths, D, scale, c, *dq_extra, stream,
-        ))
-        _lib.check(_launch(
-            "dkdv", dkdv_fn,
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(), lse.data_ptr(),
-            delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-            B, Hq, Hkv, *dkdv_lengths, D, scale, c,
-            ws.data_ptr() if ws is not None else None, ws_bytes, stream,
+            lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+            B, Hq, Hkv, N, Nkv, D, float(scale), c,
+            ws.data_ptr() if ws is not None else None, ws_bytes, _stream(q),
         ))
     return dq, dk, dv

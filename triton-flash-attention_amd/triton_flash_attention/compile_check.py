@@ -31,7 +31,8 @@ SUPPORTED_ARCHS = ("gfx950",)
 # Kernel instances the default tiling table (kDefault in csrc/fa_capi.hip) and
 # its shape rules select, as demangled name prefixes, for D = 32, 64, 128, both
 # mask modes and both element types (at D = 128 the forward takes the 8-wave
-# pipelined kernel, and the 4-wave one for short queries).
+# pipelined kernel, and the 4-wave one for short queries; at D <= 64 a backward
+# whose dK/dV launch splits runs the combined dK/dV + dQ kernel).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
@@ -41,6 +42,7 @@ def _defaults() -> tuple[str, ...]:
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
                       f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
                       f"fa::dq_pipe_kernel<32, {c}, 4, {e}>", f"fa::dq_pipe_kernel<64, {c}, 4, {e}>",
+                      f"fa::bwd_pair_kernel<32, {c}, 4, {e}>", f"fa::bwd_pair_kernel<64, {c}, 4, {e}>",
                       f"fa::dq_pipe_kernel<128, false, 4, {e}>" if c == "false"
                       else f"fa::dq_kernel<128, true, 4, 32, {e}>"]
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
