@@ -292,6 +292,29 @@ def test_combined_backward_launch_matches_separate_launches_and_reference(case, 
         _note(f"  {name}: max-abs {ma:.2e} rel-L2 {rl:.2e}")
 
 
+def test_two_key_group_forward_rule_matches_oracle():
+    """D = 32 causal launches over few heads run the two-key-group forward
+    (each work-group's keys split over two 4-wave groups, merged through LDS):
+    results match the oracle and, to fp32 rounding, the table's forward."""
+    for (B, Hq, Hkv, N) in [(1, 4, 2, 1500), (1, 2, 1, 333)]:
+        tag = f"key-group forward B={B} Hq={Hq} Hkv={Hkv} N={N} D=32"
+        _note(tag)
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, 32, seed=N)
+        got = run_kernel(q, k, v, do, True)
+        check_against_oracle(got, q, k, v, do, True, tag=tag)
+        qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+        o_rule, lse_rule = _ops.flash_fwd(qd, kd, vd, True, 32 ** -0.5)
+        _lib.set_tiling(_lib.KERNEL_FWD, 32, True, 6)
+        try:
+            o_tab, lse_tab = _ops.flash_fwd(qd, kd, vd, True, 32 ** -0.5)
+        finally:
+            _lib.set_tiling(_lib.KERNEL_FWD, 32, True, -1)
+        torch.cuda.synchronize()
+        assert_close(tag + " o vs table forward", o_rule.float(), o_tab.float(),
+                     max_abs=2e-3, rel_l2=1e-3)
+        assert float((lse_rule - lse_tab).abs().max()) <= 1e-5, tag
+
+
 def test_whole_backward_without_a_workspace_runs_one_pass():
     """fa_bwd with no workspace on a shape that would take the combined plan
     runs every launch in one pass (fused-Delta dQ, unsplit dK/dV): the same

@@ -63,7 +63,8 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //         3 = 2 waves, 64; 4 = 4 waves, 128; 5 = 4 waves, 32-key units, software-
 //         pipelined, 2 units per barrier (D <= 64); 6 = the same, 1 unit per
 //         barrier and a 6-slot ring (three work-groups per CU); 7 = 8 waves, 32-key
-//         units, pipelined, one work-group per CU (D = 128)
+//         units, pipelined, one work-group per CU (D = 128); 8 = 8 waves as two
+//         4-wave groups that split the keys of 128 queries (D <= 64)
 //         (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;
@@ -143,17 +144,30 @@ const fa::Variant* select_dq(int di, int causal, int64_t N, int dt) {
 // set with fa_set_tiling is used as set.
 constexpr int kFwdWideVariant = 7;
 constexpr int kFwdNarrowVariant = 2;
+// At D = 32 a causal launch over few heads (B*H * (query tiles + 1) < 1536)
+// takes the two-key-group forward: 8 waves per work-group as two groups that
+// split its keys, so a CU whose last long tiles run alone keeps twice the
+// waves busy (MI355X, one box: B1 H8 N16381 217 vs 225 us, B2 H8 N4096 43.0
+// vs 47.5 us; with launches that fill the GPU, B4 H16 N4096, and at D = 64,
+// where it runs one work-group per CU, it is slower: 205 vs 164 us, B2 H16
+// N2049 41 vs 34 us).
+constexpr int kFwdKeyGroupVariant = 8;
 
 const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt) {
   int index = -1;
   const fa::Variant* var = select(fa::kFwd, di, causal, &index, dt);
-  if (!var || index != kFwdWideVariant || g_override[fa::kFwd][di][causal ? 1 : 0] >= 0)
-    return var;
-  if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
+  if (!var || g_override[fa::kFwd][di][causal ? 1 : 0] >= 0) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kFwd, &count);
-  if (kFwdNarrowVariant < count && usable(vs[kFwdNarrowVariant], di, causal, dt))
-    return &vs[kFwdNarrowVariant];
+  auto pick = [&](int v) {
+    return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var;
+  };
+  if (index == kFwdWideVariant) {
+    if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
+    return pick(kFwdNarrowVariant);
+  }
+  if (di == fa::head_dim_index(32) && causal && N > 32 && BH * ((N + 127) / 128 + 1) < 1536)
+    return pick(kFwdKeyGroupVariant);
   return var;
 }
 
@@ -306,7 +320,7 @@ struct FwdSplit {
 // (decoding) pack gcd(group, waves) heads, which then share each K/V tile the
 // work-group streams; otherwise 1.
 int fwd_pack(const fa::Variant& var, int64_t group, int64_t N) {
-  if (N > 32 || group < 2) return 1;
+  if (N > 32 || group < 2 || (var.flags & fa::kKeyGroups)) return 1;
   return (int)std::gcd<int64_t>(group, var.waves);
 }
 

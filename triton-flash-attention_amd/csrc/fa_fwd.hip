@@ -379,9 +379,16 @@ __global__ __launch_bounds__(64 * NW) void fwd_kernel(FwdArgs a) {
 // ---------------------------------------------------------------------------
 // UPS = units per barrier step: 2 (8-slot ring, 64 KiB at D = 64, two
 // work-groups per CU) or 1 (6-slot ring, 48 KiB, three work-groups per CU).
-template <int D, int NW, int UPS>
+// KG = key groups: with KG = 2 the NW waves form two groups of NW/2 that
+// serve the same queries, each streaming one half of the work-group's key
+// range through a ring of its own with the UPS = 1 pipeline; the two partial
+// results are merged through LDS at the end. That halves the longest
+// work-group of a causal launch whose end is set by its last query tiles
+// (few heads: the tiles reading all keys run alone on the GPU at the end).
+template <int D, int NW, int UPS, int KG = 1>
 struct FwdPipeTile {
-  static constexpr int BM = 32 * NW;
+  static constexpr int NWG = NW / KG;  // waves per key group
+  static constexpr int BM = 32 * NWG;
   static constexpr int NT = 64 * NW;
   static constexpr int KT = 32;
   static constexpr int TILE = KT * D;  // halves of the K (or V) unit
@@ -389,18 +396,22 @@ struct FwdPipeTile {
   static constexpr int NSTAGE = UPS == 2 ? 8 : 6;
   static constexpr int AHEAD = UPS == 2 ? 5 : 4;  // units issued before step 0
   // Work-groups per CU: three 4-wave work-groups with one unit per barrier,
-  // two with two; an 8-wave work-group (D = 128: 16 KiB units) takes a CU alone.
-  static constexpr int WGS_PER_CU = NW == 8 ? 1 : (UPS == 2 ? 2 : 3);
+  // two with two; an 8-wave work-group (D = 128: 16 KiB units) takes a CU
+  // alone; with two key groups (two rings) two at D = 32 and one at D = 64.
+  static constexpr int WGS_PER_CU =
+      KG == 2 ? (D <= 32 ? 2 : 1) : (NW == 8 ? 1 : (UPS == 2 ? 2 : 3));
   static constexpr int WAVES_PER_SIMD = WGS_PER_CU * NW / 4;
   static_assert(UPS == 1 || UPS == 2, "units per step");
+  static_assert(KG == 1 || (KG == 2 && UPS == 1 && NW == 8), "two 4-wave key groups, one unit each");
 };
 
-template <int D, int NW, int UPS>
+template <int D, int NW, int UPS, int KG = 1>
 constexpr bool fwd_pipe_tiling_ok() {
-  using T = FwdPipeTile<D, NW, UPS>;
+  using T = FwdPipeTile<D, NW, UPS, KG>;
   constexpr int instr = T::TILE * 2 / 1024;
-  return (T::TILE * 2) % 1024 == 0 && instr <= NW && NW % instr == 0 &&
-         T::WGS_PER_CU * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 && (D <= 64 || NW == 8);
+  return (T::TILE * 2) % 1024 == 0 && instr <= T::NWG && T::NWG % instr == 0 &&
+         T::WGS_PER_CU * KG * T::NSTAGE * T::STAGE * 2 <= 160 * 1024 &&
+         (KG == 1 ? (D <= 64 || NW == 8) : D <= 64);
 }
 
 #ifndef FA_FWD_LEAD
@@ -424,20 +435,24 @@ __device__ __forceinline__ void static_for_fwd_issue(F&& f) {
   fwd_static_for<0, N>(f);
 }
 
-template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16, int KG = 1>
 __global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS>::WAVES_PER_SIMD)))
+__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS, KG>::WAVES_PER_SIMD)))
 void fwd_pipe_kernel(FwdArgs a) {
-  using T = FwdPipeTile<D, NW, UPS>;
-  using Dma = DmaStager<D, T::KT, NW>;
+  using T = FwdPipeTile<D, NW, UPS, KG>;
+  using Dma = DmaStager<D, T::KT, T::NWG>;
   static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
   constexpr int NS = T::NSTAGE;
   constexpr int IPU = 2;  // this wave's DMA instructions per unit: K, V
-  __shared__ __attribute__((aligned(16))) half_t lds[NS * T::STAGE];
+  __shared__ __attribute__((aligned(16))) half_t lds_all[KG * NS * T::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_wg = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Key group of the wave and its place in the group (KG = 1: the work-group).
+  const int gk = KG == 1 ? 0 : wave_wg / T::NWG;
+  const int wave = wave_wg - gk * T::NWG;
+  half_t* const lds = lds_all + gk * (NS * T::STAGE);  // the group's ring
   const int ql = lane & 31;
   const int g = lane >> 5;
 
@@ -475,11 +490,16 @@ void fwd_pipe_kernel(FwdArgs a) {
   wait_all_vm();
 
   const int kv_end = CAUSAL ? min(Nkv, q0 + bm) : Nkv;
-  // This work-group's keys [kv_lo, kv_hi): all of [0, kv_end) unless split.
-  const int kv_lo = split * a.split_keys;
-  const int kv_hi = min(kv_end, kv_lo + a.split_keys);
-  const int nunits = kv_hi > kv_lo ? (kv_hi - kv_lo + T::KT - 1) / T::KT : 0;
-  const int npad = (nunits + NS - 1) / NS * NS;
+  // This work-group's keys: all of [0, kv_end) unless split; with two key
+  // groups, the first ceil(units / 2) units go to group 0, the rest to group
+  // 1, and both run the same (padded) number of steps.
+  const int kv_lo_wg = split * a.split_keys;
+  const int kv_hi_wg = min(kv_end, kv_lo_wg + a.split_keys);
+  const int n_wg = kv_hi_wg > kv_lo_wg ? (kv_hi_wg - kv_lo_wg + T::KT - 1) / T::KT : 0;
+  const int n_grp = (n_wg + KG - 1) / KG;
+  const int kv_lo = kv_lo_wg + gk * n_grp * T::KT;
+  const int kv_hi = KG == 1 ? kv_hi_wg : min(kv_hi_wg, kv_lo + n_grp * T::KT);
+  const int npad = (n_grp + NS - 1) / NS * NS;
 
   Dma dma;
   dma.init(wave, lane);
@@ -509,7 +529,8 @@ void fwd_pipe_kernel(FwdArgs a) {
   {
     half_t* zs = lds + (NS - 1) * T::STAGE + T::TILE;
     const u32x4 z = {0u, 0u, 0u, 0u};
-    for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
+    for (int i = tid - gk * 64 * T::NWG; i < T::TILE / 8; i += 64 * T::NWG)
+      *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
   }
   // Units 0 .. AHEAD-3 landed (the last two in flight), zeros written.
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
@@ -712,24 +733,56 @@ void fwd_pipe_kernel(FwdArgs a) {
   pv(lds + (NS - 1) * T::STAGE);  // O of the last unit (the ring's last slot)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  if constexpr (KG == 2) {
+    // Group 1 hands its O, m and l (per lane) to the group-0 wave serving the
+    // same queries through LDS (the rings are drained), [wave][value][lane].
+    constexpr int F = D / 32 * 16 + 2;
+    __syncthreads();
+    float* const xs = reinterpret_cast<float*>(lds_all) + wave * F * 64 + lane;
+    if (gk == 1) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) xs[(16 * db + j) * 64] = o[db][j];
+      xs[(F - 2) * 64] = m;
+      xs[(F - 1) * 64] = l;
+    }
+    __syncthreads();
+    if (gk == 1) return;
+    // O = O0 w0 + O1 w1, l = l0 w0 + l1 w1 against the larger reference max
+    // (a group that saw no key has m = -inf, l = 0 and weighs 0).
+    const float m1 = xs[(F - 2) * 64];
+    const float l1 = xs[(F - 1) * 64];
+    const float mt = __builtin_fmaxf(m, m1);
+    const float w0 = m == -inf ? 0.f : exp2_fast(m - mt);
+    const float w1 = m1 == -inf ? 0.f : exp2_fast(m1 - mt);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[db][j] = o[db][j] * w0 + xs[(16 * db + j) * 64] * w1;
+    l = l * w0 + l1 * w1;
+    m = mt;
+  }
+
   // Epilogue: lane (query qrow, half g) holds d = 32*db + 8*(j/4) + 4*g + j%4.
   const float lt = halves_sum(l);
   store_fwd_output<D, E>(a, ro, split, head, qrow, g, o, m, lt);
 }
 
-template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16, int KG = 1>
 hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
-  using T = FwdPipeTile<D, NW, UPS>;
+  using T = FwdPipeTile<D, NW, UPS, KG>;
   FwdArgs b = a;
-  if (b.pack < 1 || NW % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
+  if (b.pack < 1 || NW % b.pack != 0 || a.group % b.pack != 0 || (KG > 1 && b.pack != 1))
+    return hipErrorInvalidValue;
   b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
       (int64_t)b.nsplit * b.split_keys < a.Nkv)
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS, E>), dim3((unsigned)blocks), dim3(T::NT),
-                     0, stream, b);
+  hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS, E, KG>), dim3((unsigned)blocks),
+                     dim3(T::NT), 0, stream, b);
   return hipGetLastError();
 }
 
@@ -737,6 +790,14 @@ template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 constexpr void* fwd_pipe_entry() {
   if constexpr (fwd_pipe_tiling_ok<D, NW, UPS>())
     return (void*)&fwd_pipe_launch<D, CAUSAL, NW, UPS, E>;
+  else
+    return nullptr;
+}
+// The two-key-group forward (KG = 2).
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
+constexpr void* fwd_pipe_kg_entry() {
+  if constexpr (fwd_pipe_tiling_ok<D, NW, UPS, 2>())
+    return (void*)&fwd_pipe_launch<D, CAUSAL, NW, UPS, E, 2>;
   else
     return nullptr;
 }
@@ -854,6 +915,9 @@ static const Variant kFwdVariants[] = {
      kSplitsKv},
     {8, 256, 32, {FA_ENTRIES(fwd_pipe_entry, F16, 8, 1), FA_ENTRIES(fwd_pipe_entry, BF16, 8, 1)},
      kSplitsKv},
+    {8, 128, 32,
+     {FA_ENTRIES(fwd_pipe_kg_entry, F16, 8, 1), FA_ENTRIES(fwd_pipe_kg_entry, BF16, 8, 1)},
+     kSplitsKv | kKeyGroups},
 };
 
 const Variant* fwd_variants(int* count) {

@@ -113,6 +113,9 @@ constexpr int kSplitsKv = 2;
 // The backward variant (pipelined dK/dV or dQ, D <= 64) also runs in the
 // combined launch of bwd_pair_launcher.
 constexpr int kPairs = 4;
+// The forward variant splits each work-group's keys over two wave groups
+// (one query head per work-group: no packed GQA).
+constexpr int kKeyGroups = 8;
 
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);

@@ -31,7 +31,8 @@ SUPPORTED_ARCHS = ("gfx950",)
 # Kernel instances the default tiling table (kDefault in csrc/fa_capi.hip) and
 # its shape rules select, as demangled name prefixes, for D = 32, 64, 128, both
 # mask modes and both element types (at D = 128 the forward takes the 8-wave
-# pipelined kernel, and the 4-wave one for short queries; at D <= 64 a backward
+# pipelined kernel, and the 4-wave one for short queries; at D = 32 causal
+# launches over few heads take the two-key-group forward; at D <= 64 a backward
 # whose dK/dV launch splits runs the combined dK/dV + dQ kernel).
 def _defaults() -> tuple[str, ...]:
     names = []
@@ -45,6 +46,7 @@ def _defaults() -> tuple[str, ...]:
                       f"fa::bwd_pair_kernel<32, {c}, 4, {e}>", f"fa::bwd_pair_kernel<64, {c}, 4, {e}>",
                       f"fa::dq_pipe_kernel<128, false, 4, {e}>" if c == "false"
                       else f"fa::dq_kernel<128, true, 4, 32, {e}>"]
+        names.append(f"fa::fwd_pipe_kernel<32, true, 8, 1, {e}, 2>")
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
     return tuple(names)
