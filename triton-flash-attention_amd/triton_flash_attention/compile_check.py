@@ -38,8 +38,9 @@ def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
         for c in ("false", "true"):
-            names += [f"fa::fwd_pipe_kernel<32, {c}, 4, 1, {e}>", f"fa::fwd_pipe_kernel<64, {c}, 4, 1, {e}>",
-                      f"fa::fwd_pipe_kernel<128, {c}, 8, 1, {e}>", f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
+            names += [f"fa::fwd_pipe_kernel<32, {c}, 4, 1, {e}, 1>",
+                      f"fa::fwd_pipe_kernel<64, {c}, 4, 1, {e}, 1>",
+                      f"fa::fwd_pipe_kernel<128, {c}, 8, 1, {e}, 1>", f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
                       f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
                       f"fa::dq_pipe_kernel<32, {c}, 4, {e}>", f"fa::dq_pipe_kernel<64, {c}, 4, {e}>",
