@@ -59,9 +59,13 @@ def _time_us(fn, reps: int) -> float:
 
 
 def sweep(*, batch: int, query_heads: int, kv_heads: int, seq_len: int, head_dim: int,
-          causal: bool, kernels: list[str], reps: int = 10, seed: int = 0) -> list[dict[str, Any]]:
+          causal: bool, kernels: list[str], reps: int = 10, seed: int = 0,
+          with_choice: bool = False) -> list[dict[str, Any]]:
     """One row per (kernel, compiled tiling): waves, rows per work-group, tile,
-    whether the table picks it, mean µs per launch and executed TFLOP/s."""
+    whether the table picks it, mean µs per launch and executed TFLOP/s. With
+    ``with_choice`` each kernel also gets a row with variant ``"auto"``: no
+    tiling set, so the library runs what it picks for this shape (the table
+    refined by its shape rules)."""
     g = torch.Generator("cpu").manual_seed(seed)
     shapes = ((batch, query_heads, seq_len, head_dim), (batch, kv_heads, seq_len, head_dim),
               (batch, kv_heads, seq_len, head_dim), (batch, query_heads, seq_len, head_dim))
@@ -90,6 +94,11 @@ def sweep(*, batch: int, query_heads: int, kv_heads: int, seq_len: int, head_dim
                              "tflops_executed": round(flop / us / 1e6, 1)})
         finally:
             _lib.set_tiling(kind, head_dim, causal, -1)
+        if with_choice:
+            us = _time_us(runners[name], reps)
+            rows.append({"kernel": name, "variant": "auto", "waves": "", "rows": "", "tile": "",
+                         "table": False, "us": round(us, 1),
+                         "tflops_executed": round(flop / us / 1e6, 1)})
     return rows
 
 
@@ -124,7 +133,7 @@ def main(argv: list[str] | None = None) -> int:
         raise SystemExit("the tiling sweep needs a GPU")
     rows = sweep(batch=args.batch, query_heads=args.query_heads, kv_heads=kv_heads,
                  seq_len=args.seq_len, head_dim=args.head_dim, causal=args.mask == "causal",
-                 kernels=kernels, reps=args.reps)
+                 kernels=kernels, reps=args.reps, with_choice=True)
     print(f"B={args.batch} Hq={args.query_heads} Hkv={kv_heads} N={args.seq_len} "
           f"D={args.head_dim} {args.mask}")
     print("| kernel | variant | waves | rows | tile | table | µs | TFLOP/s executed |")
@@ -133,11 +142,13 @@ def main(argv: list[str] | None = None) -> int:
         print(f"| {r['kernel']} | {r['variant']} | {r['waves']} | {r['rows']} | {r['tile']} | "
               f"{'*' if r['table'] else ''} | {r['us']:.1f} | {r['tflops_executed']:.1f} |")
     for name in kernels:
-        mine = [r for r in rows if r["kernel"] == name]
+        mine = [r for r in rows if r["kernel"] == name and r["variant"] != "auto"]
         best = min(mine, key=lambda r: r["us"])
         table = next(r for r in mine if r["table"])
+        auto = next(r for r in rows if r["kernel"] == name and r["variant"] == "auto")
         print(f"{name}: fastest variant {best['variant']} ({best['us']:.1f} µs), "
-              f"table variant {table['variant']} ({table['us']:.1f} µs)")
+              f"table variant {table['variant']} ({table['us']:.1f} µs), "
+              f"library's choice for this shape {auto['us']:.1f} µs")
     if args.output is not None:
         args.output.parent.mkdir(parents=True, exist_ok=True)
         with args.output.open("w", newline="") as f:
