@@ -272,8 +272,8 @@ int fa_bwd_dq_delta_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_hal
  * workspace == NULL every launch runs in one pass; a non-NULL workspace smaller
  * than needed is rejected (FA_ERR_BAD_SHAPE). Launch plan: dQ with Delta fused,
  * then dK/dV (each split when its launch has few work-groups); except when
- * dK/dV splits and dQ does not (head_dim 32 or 64, the default tilings):
- * then Delta runs as its own pass and the dK/dV and dQ work-groups run in one
+ * dK/dV splits and dQ does not and has at most 768 work-groups of 128 queries
+ * (head_dim 32 or 64, the default tilings): then Delta runs as its own pass and the dK/dV and dQ work-groups run in one
  * combined launch, each filling the other's tail, before the dK/dV partials
  * are summed. Results are identical for a given plan on every call
  * (deterministic); the two plans differ only in how Delta reaches the dQ

@@ -253,22 +253,30 @@ def test_split_forward_workspace_sizing_and_rejection(lib):
 def test_whole_backward_workspace_is_both_splits_and_rejects_bad_arguments(lib):
     """fa_bwd's workspace holds the dQ partials, then (at a 256-byte boundary)
     the dK/dV partials: the sum of what the per-kernel queries report, except
-    that in the combined plan (dK/dV splits, dQ does not) the dK/dV launch
-    takes at most as many chunks, and at least two."""
+    that in the combined plan (dK/dV splits, dQ does not and has at most 768
+    work-groups of 128 queries) the dK/dV chunks aim at 3072 work-groups
+    counting the dQ ones, between 2 and 16 of them."""
     for args in [(4, 16, 16, 4096, 4096, 64, 1), (2, 16, 4, 2049, 2049, 64, 1),
                  (1, 8, 2, 16381, 16381, 32, 1), (1, 32, 8, 128, 32768, 128, 0),
                  (1, 8, 2, 5000, 300, 64, 1), (1, 4, 1, 700, 900, 64, 0),
-                 (1, 8, 2, 16381, 16381, 128, 1)]:
+                 (1, 8, 2, 16381, 16381, 128, 1), (1, 4, 1, 16381, 16381, 32, 1),
+                 (1, 6, 2, 16384, 16384, 64, 0)]:
         dq = lib.fa_bwd_dq_workspace_bytes(*args)
         dkdv = lib.fa_bwd_dkdv_workspace_bytes_kv(*args)
         assert dq >= 0 and dkdv >= 0
         got = lib.fa_bwd_workspace_bytes(*args)
         B, Hq, Hkv, N, Nkv, D, causal = args
-        if dkdv == 0 or dq > 0 or D == 128:  # the per-kernel launches, one after the other
+        dq_wgs = -(-N // 128) * B * Hq
+        if dkdv == 0 or dq > 0 or D == 128 or dq_wgs > 768:
+            # the per-kernel launches, one after the other
             assert got == (((dq + 255) // 256 * 256 + dkdv) if dkdv else dq), args
         else:  # combined launch
             plane = 2 * B * Hkv * Nkv * D * 4
-            assert got % plane == 0 and 2 <= got // plane and got <= dkdv, args
+            assert got % plane == 0 and 2 <= got // plane <= 16, args
+            if (B, Hq, Hkv, N, D, causal) == (2, 16, 4, 2049, 64, 1):
+                assert got == 4 * plane  # c3: capped by 32 query units per chunk
+            if (B, Hq, Hkv, N, D, causal) == (1, 6, 2, 16384, 64, 0):
+                assert got == 9 * plane  # (3072 - 768) / 256 rounded up
     assert lib.fa_bwd_workspace_bytes(4, 16, 16, 4096, 4096, 64, 1) == 0
     assert lib.fa_bwd_workspace_bytes(1, 8, 2, 16381, 16381, 48, 1) == _lib.FA_ERR_HEAD_DIM
     assert lib.fa_bwd_workspace_bytes(1, 8, 2, 16381, 0, 32, 1) == _lib.FA_ERR_BAD_SHAPE

@@ -682,8 +682,15 @@ struct BwdPlan {
 // B2 Hq16 Hkv4 N2049 D64 causal, backward 106 -> 97 us already with the two
 // launches on two streams, while with launches that fill the GPU (B4 H16
 // N4096) running them together is slower (505 vs 478 us).
-// Work-groups (dK/dV chunks plus dQ) the combined launch aims at, and the
-// fewest 32-query units per dK/dV chunk on average.
+// The dQ launch must be short too: the combined plan pays off while dQ has at
+// most 768 work-groups (1.5 waves of 2 per CU on 256 CUs). Measured on MI355X,
+// whole backward, combined vs separate launches: dQ with 512-544 work-groups
+// (B2 Hq16 Hkv4 N2049 D64/D32, B1 Hq4 Hkv1 N16381 D32, B1 Hq8 Hkv2 N8192 D32,
+// causal and not) 4-8 % faster; with 1024 (B1 Hq8 Hkv2 N16381 D32, B1 Hq16
+// Hkv4 N8192 D64, B1 Hq32 Hkv8 N4096 D64) between 1.5 % faster and 4.6 %
+// slower. Work-groups (dK/dV chunks plus dQ) the combined launch aims at, and
+// the fewest 32-query units per dK/dV chunk on average.
+constexpr int64_t kPairMaxDqWorkgroups = 768;
 constexpr int64_t kPairTargetWorkgroups = 3072;
 constexpr int64_t kPairMinSplitUnits = 32;
 
@@ -695,15 +702,15 @@ bool plan_bwd(int dt, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv
   if (!p->dq || !p->dkdv) return false;
   p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv);
   p->dkdv_nsplit = dkdv_split(*p->dkdv, B, Hq, Hkv, N, Nkv, causal);
-  p->pair = p->dkdv_nsplit > 1 && p->dq_split.nsplit == 1 && (p->dq->flags & fa::kPairs) &&
-            (p->dkdv->flags & fa::kPairs) && p->dq->waves == fa::bwd_pair_waves() &&
-            p->dkdv->waves == fa::bwd_pair_waves() &&
+  const int64_t dq_wgs = (N + p->dq->rows - 1) / p->dq->rows * B * Hq;
+  p->pair = p->dkdv_nsplit > 1 && p->dq_split.nsplit == 1 && dq_wgs <= kPairMaxDqWorkgroups &&
+            (p->dq->flags & fa::kPairs) && (p->dkdv->flags & fa::kPairs) &&
+            p->dq->waves == fa::bwd_pair_waves() && p->dkdv->waves == fa::bwd_pair_waves() &&
             fa::bwd_pair_launcher(dt, di, causal) != nullptr;
   if (p->pair) {
     // Beside the dQ work-groups the dK/dV chunks need not fill the GPU alone
     // (still split: the plan exists for launches whose key tiles are too few).
     const int64_t dkdv_wgs = (Nkv + p->dkdv->rows - 1) / p->dkdv->rows * B * Hkv;
-    const int64_t dq_wgs = (N + p->dq->rows - 1) / p->dq->rows * B * Hq;
     p->dkdv_nsplit = (int)std::max<int64_t>(
         2, chunks_for(std::max<int64_t>(kPairTargetWorkgroups - dq_wgs, dkdv_wgs), dkdv_wgs,
                       dkdv_tile_units(Hq, Hkv, N, causal), kPairMinSplitUnits));

@@ -319,7 +319,8 @@ def flash_bwd(
     the shape needs one, comes from the caching allocator. The library picks
     the launch plan: dQ with Delta fused, then dK/dV reading that Delta; or,
     when the dK/dV launch has too few key tiles to fill the GPU and splits
-    while dQ does not, a Delta pass and one combined dK/dV + dQ launch."""
+    while dQ does not and is short too, a Delta pass and one combined
+    dK/dV + dQ launch."""
     dt = _elem_dtype(q, "q")
     for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("dO", do)):
         _require(t, name, dt, q.device)

@@ -33,7 +33,8 @@ SUPPORTED_ARCHS = ("gfx950",)
 # mask modes and both element types (at D = 128 the forward takes the 8-wave
 # pipelined kernel, and the 4-wave one for short queries; at D = 32 causal
 # launches over few heads take the two-key-group forward; at D <= 64 a backward
-# whose dK/dV launch splits runs the combined dK/dV + dQ kernel).
+# whose dK/dV launch splits next to a short dQ launch runs the combined dK/dV + dQ
+# kernel).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
