@@ -171,6 +171,15 @@ def cpu_baseline(inputs, causal: bool, budget_s: float):
     return times[len(times) // 2], threads, affinity, len(times)
 
 
+def device_label() -> str:
+    """The device's marketing name, or (where the name table is missing and the
+    name comes back empty) its architecture and compute-unit count."""
+    props = torch.cuda.get_device_properties(torch.cuda.current_device())
+    arch = getattr(props, "gcnArchName", "")
+    label = f"{arch}, {props.multi_processor_count} CUs" if arch else f"{props.multi_processor_count} CUs"
+    return f"{props.name} ({label})" if props.name else label
+
+
 def load_traffic(workload: str, kernel: str):
     """HBM bytes per launch of ``kernel`` measured with rocprofv3 PMC counters
     (FETCH_SIZE + WRITE_SIZE, calibrated against a copy of known size), as
@@ -369,7 +378,7 @@ def main(argv=None) -> int:
         },
         "baseline_note": "vs_baseline divides by the reference's published 13.283 TFLOP/s "
                          "(Triton path, RTX 5050 Laptop GPU, README.md:159)",
-        "device": torch.cuda.get_device_name(),
+        "device": device_label(),
     }
 
     if reference_protocol is not None:
