@@ -593,6 +593,10 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
 // Each work-group rounds its unit count up to the 8-unit unroll (padding
 // units are zeros).
 // --------------------------------------------------------------------------
+#ifndef FA_DQ_NSTAGE
+#define FA_DQ_NSTAGE 8
+#endif
+
 template <int D, int NW>
 struct DqPipeTile {
   static constexpr int BQ = 32 * NW;
@@ -600,8 +604,11 @@ struct DqPipeTile {
   static constexpr int KT = 32;
   static constexpr int TILE = KT * D;   // halves of the K (or V) unit
   static constexpr int STAGE = 2 * TILE;
-  static constexpr int NSTAGE = 8;
-  static constexpr int AHEAD = 5;
+  static constexpr int NSTAGE = FA_DQ_NSTAGE;
+  // Units issued ahead: the ring less the three a step reads (its two units
+  // and the next unit's S operand).
+  static constexpr int AHEAD = NSTAGE - 3;
+  static_assert(NSTAGE % 2 == 0 && NSTAGE >= 8, "whole two-unit steps per ring turn");
   // D <= 64: two work-groups per CU; D = 128: one (dQ accumulated in AGPRs).
   static constexpr int WGS_PER_CU = D <= 64 ? 2 : 1;
 };
@@ -751,8 +758,9 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
     const u32x4 z = {0u, 0u, 0u, 0u};
     for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
   }
-  // Units 0, 1, 2 landed (3, 4 in flight), zeros written.
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
+  // Units 0, 1, 2 landed (the rest in flight), zeros written.
+  constexpr int kInFlight = (T::AHEAD - 3) * IPU;
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(kInFlight) : "memory");
 
   int r_off[D / 16];  // row reads: row row_perm(ql), chunk 2*kk + g
 #pragma unroll
@@ -919,19 +927,19 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
 
   auto step = [&](auto p_c) {
     constexpr int P = decltype(p_c)::value;
-    issue((2 * P + 5) % NS);
-    issue((2 * P + 6) % NS);
+    issue((2 * P + T::AHEAD) % NS);
+    issue((2 * P + T::AHEAD + 1) % NS);
     body(std::integral_constant<int, 2 * P>{});
     body(std::integral_constant<int, 2 * P + 1>{});
-    wait_vm_and_barrier<2 * IPU>();
+    // the next step reads up to unit 2P + 4; later ones may stay in flight
+    wait_vm_and_barrier<kInFlight>();
   };
 
   // Whole steps until the work-group's units are done (as in dK/dV above).
-  static_assert(NS == 8, "the loop below is unrolled for 8 slots");
   int left = nunits;
   int last = NS - 1;
   for (int u = 0; u < npad && left > 0; u += NS) {
-    bwd_static_for<0, 4>([&](auto p_c) {
+    bwd_static_for<0, NS / 2>([&](auto p_c) {
       if (left > 0) {
         step(p_c);
         last = 2 * decltype(p_c)::value + 1;
