@@ -642,7 +642,7 @@ void fwd_pipe_kernel(FwdArgs a) {
     };
     half8 pa[2];
     float pexp[16];
-    float lsum[2] = {0.f, 0.f};
+    float lsum[2];  // set by the first pair
     // Vector work on value pairs in two stages placed in different groups:
     //   A: p = exp2(s c - m)        B: row sums, fp16 P^T.
     auto stage_a = [&](int pr) {
@@ -657,7 +657,7 @@ void fwd_pipe_kernel(FwdArgs a) {
       half2v pp;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        lsum[e] += pexp[2 * pr + e];
+        lsum[e] = pr == 0 ? pexp[e] : lsum[e] + pexp[2 * pr + e];
         pp[e] = to_elem<E>(pexp[2 * pr + e]);
       }
       asm volatile("" : "+v"(pp));
