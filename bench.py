@@ -174,6 +174,8 @@ def cpu_baseline(inputs, causal: bool, budget_s: float):
 def device_label() -> str:
     """The device's marketing name, or (where the name table is missing and the
     name comes back empty) its architecture and compute-unit count."""
+    import torch
+
     props = torch.cuda.get_device_properties(torch.cuda.current_device())
     arch = getattr(props, "gcnArchName", "")
     label = f"{arch}, {props.multi_processor_count} CUs" if arch else f"{props.multi_processor_count} CUs"

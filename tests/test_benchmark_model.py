@@ -68,6 +68,25 @@ def test_bench_refuses_more_than_one_gpu(capsys) -> None:
     assert "one GPU" in capsys.readouterr().err
 
 
+def test_bench_device_label_without_a_marketing_name(monkeypatch) -> None:
+    """Where the device name table is missing the name comes back empty; the
+    bench line then names the architecture and compute units."""
+    import types
+
+    import torch
+
+    spec = importlib.util.spec_from_file_location("bench", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    props = types.SimpleNamespace(name="", gcnArchName="gfx950:sramecc+:xnack-",
+                                  multi_processor_count=256)
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(torch.cuda, "get_device_properties", lambda i: props)
+    assert bench.device_label() == "gfx950:sramecc+:xnack-, 256 CUs"
+    props.name = "AMD Instinct MI355X"
+    assert bench.device_label() == "AMD Instinct MI355X (gfx950:sramecc+:xnack-, 256 CUs)"
+
+
 def test_tiling_sweep_counts_executed_matmuls() -> None:
     """The sweep's executed FLOP: the forward equals the harness's forward count;
     dK/dV and dQ recompute S and dP, so the three kernels execute 9 matmuls
