@@ -500,12 +500,17 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int kv_lo = kv_lo_wg + gk * n_grp * T::KT;
   const int kv_hi = KG == 1 ? kv_hi_wg : min(kv_hi_wg, kv_lo + n_grp * T::KT);
   const int npad = (n_grp + NS - 1) / NS * NS;
+  // The group's units end in the ring's last slot: the first ring turn
+  // starts at step p0 (slot s0), so no padding unit runs (one at most with
+  // two units per step) and the loop over whole turns has no branches.
+  const int p0 = __builtin_amdgcn_readfirstlane((npad - n_grp) / UPS);
+  const int s0 = UPS * p0;
 
   Dma dma;
   dma.init(wave, lane);
   const uint32_t lds0 = lds_addr(lds);
   int i_row = kv_lo;  // first key row of the next unit to fetch
-  auto issue = [&](int slot) {
+  auto issue = [&](int slot) __attribute__((always_inline)) {
     const int row0 = i_row < kv_hi ? i_row : Nkv;  // past the range: zeros
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
@@ -523,11 +528,11 @@ void fwd_pipe_kernel(FwdArgs a) {
     i_row += T::KT;
   };
 #pragma unroll
-  for (int u = 0; u < T::AHEAD; ++u) issue(u);
+  for (int u = 0; u < T::AHEAD; ++u) issue(s0 + u < NS ? s0 + u : s0 + u - NS);
 
   // The V tile read as "unit -1" holds zeros (its P is zero too).
   {
-    half_t* zs = lds + (NS - 1) * T::STAGE + T::TILE;
+    half_t* zs = lds + (s0 > 0 ? s0 - 1 : NS - 1) * T::STAGE + T::TILE;
     const u32x4 z = {0u, 0u, 0u, 0u};
     for (int i = tid - gk * 64 * T::NWG; i < T::TILE / 8; i += 64 * T::NWG)
       *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
@@ -581,14 +586,14 @@ void fwd_pipe_kernel(FwdArgs a) {
   for (int j = 0; j < 16; ++j) s_cur[j] = 0.f;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
-    s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + k_off[kk]), qf[kk], s_cur);
+    s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + s0 * T::STAGE + k_off[kk]), qf[kk], s_cur);
   half8 pa_prev[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) pa_prev[h][e] = (half_t)0.f;
 
-  auto pv = [&](const half_t* slot) {
+  auto pv = [&](const half_t* slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -598,7 +603,7 @@ void fwd_pipe_kernel(FwdArgs a) {
 
   int c_key = kv_lo;  // first key of the unit the body works on
 
-  auto body = [&](auto slot_c) {
+  auto body = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;
     const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
     const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
@@ -717,7 +722,7 @@ void fwd_pipe_kernel(FwdArgs a) {
   // One barrier step: UPS units; issues the units AHEAD.. ahead into the
   // slots of units finished before the last barrier, then waits for all but
   // the two most recent units (the next step reads up to 2 units ahead).
-  auto step = [&](auto p_c) {
+  auto step = [&](auto p_c) __attribute__((always_inline)) {
     constexpr int P = decltype(p_c)::value;
     static_for_fwd_issue<UPS>([&](auto e_c) {
       issue((UPS * P + T::AHEAD + decltype(e_c)::value) % NS);
@@ -727,8 +732,14 @@ void fwd_pipe_kernel(FwdArgs a) {
   };
 
   static_assert(NS % UPS == 0, "whole steps per ring turn");
-  for (int u = 0; u < npad; u += NS) {
-    fwd_static_for<0, NS / UPS>([&](auto p_c) { step(p_c); });
+  if (npad > 0) {
+    // first turn from step p0 (the branches run once), then whole turns
+    fwd_static_for<0, NS / UPS>([&](auto p_c) {
+      if (decltype(p_c)::value >= p0) step(p_c);
+    });
+    for (int u = NS; u < npad; u += NS) {
+      fwd_static_for<0, NS / UPS>([&](auto p_c) { step(p_c); });
+    }
   }
   pv(lds + (NS - 1) * T::STAGE);  // O of the last unit (the ring's last slot)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
