@@ -184,6 +184,11 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
   const int u_lo = min(split * chunk, total_units);
   const int nunits = min(chunk, total_units - u_lo);
   const int npad = (nunits + NS - 1) / NS * NS;
+  // The units end in the ring's last slot: the first ring turn starts at step
+  // p0 (slot s0), so at most one padding unit runs and the loop over whole
+  // turns has no branches between its steps.
+  const int p0 = __builtin_amdgcn_readfirstlane((npad - nunits) / 2);
+  const int s0 = 2 * p0;
 
   // Issue cursor: query head gi of the group and first row of the next unit
   // to fetch; after the last unit the row is N (zeros from then on).
@@ -205,7 +210,7 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
   const uint32_t lds0 = lds_addr(lds);
   const uint32_t aux_lane = (uint32_t)lane * 4u;
   const uint32_t aux_lds = 2u * T::TILE * 2u + (is_lse ? 0u : 64u * 4u);
-  auto issue = [&](int slot) {
+  auto issue = [&](int slot) __attribute__((always_inline)) {
     const int row0 = i_left > 0 ? i_row : N;
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t va = (uint32_t)row0 * 4u + aux_lane;
@@ -256,12 +261,12 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
     }
   };
 #pragma unroll
-  for (int u = 0; u < T::AHEAD; ++u) issue(u);
+  for (int u = 0; u < T::AHEAD; ++u) issue(s0 + u < NS ? s0 + u : s0 + u - NS);
 
   // The slot read as "unit -1" holds zeros (its P and dS' are zero too);
   // the +inf table of fully masked units.
   {
-    half_t* zs = lds + (NS - 1) * T::STAGE;
+    half_t* zs = lds + (s0 > 0 ? s0 - 1 : NS - 1) * T::STAGE;
     const u32x4 z = {0u, 0u, 0u, 0u};
     for (int i = tid; i < 2 * T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
     if (tid < 64) reinterpret_cast<float*>(lds)[kInfOff + tid] = __builtin_inff();
@@ -337,12 +342,13 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
   // previous one.
   float16v s_cur, dp_cur;
   {
-    dp_cur = table16(reinterpret_cast<const float*>(lds + 2 * T::TILE) + 64 + 8 * g);
-    s_cur = table16(fl + lse_table(0, c_row));
+    const half_t* first = lds + s0 * T::STAGE;
+    dp_cur = table16(reinterpret_cast<const float*>(first + 2 * T::TILE) + 64 + 8 * g);
+    s_cur = table16(fl + lse_table(s0, c_row));
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + r_off[kk]), kf[kk], s_cur);
-      dp_cur = mma<E>(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), vn[kk], dp_cur);
+      s_cur = mma<E>(*reinterpret_cast<const half8*>(first + r_off[kk]), kf[kk], s_cur);
+      dp_cur = mma<E>(*reinterpret_cast<const half8*>(first + T::TILE + r_off[kk]), vn[kk], dp_cur);
     }
   }
   half8 pa_prev[2], sa_prev[2];
@@ -371,7 +377,7 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
   };
 
   // Body of one unit in ring slot SLOT (see the header comment).
-  auto body = [&](auto slot_c) {
+  auto body = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;
     const half_t* cur = lds + SLOT * T::STAGE;
     const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
@@ -506,7 +512,7 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
 
   // Step p of the unrolled loop: units in slots 2p, 2p+1; issues the units
   // 5 and 6 ahead (slots of the units finished before the last barrier).
-  auto step = [&](auto p_c) {
+  auto step = [&](auto p_c) __attribute__((always_inline)) {
     constexpr int P = decltype(p_c)::value;
     issue((2 * P + 5) % NS);
     issue((2 * P + 6) % NS);
@@ -516,23 +522,17 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
     wait_vm_and_barrier<2 * IPU>();
   };
 
-  // Whole steps until the work-group's units are done (the unrolled ring turn
-  // may end early: padding to the turn would run masked units for nothing).
-  // `last` is the ring slot of the last unit run, the zeroed slot if none.
-  static_assert(NS == 8, "the loop below is unrolled for 8 slots");
-  int left = nunits;
-  int last = NS - 1;
-  for (int u = 0; u < npad && left > 0; u += NS) {
-    bwd_static_for<0, 4>([&](auto p_c) {
-      if (left > 0) {
-        step(p_c);
-        last = 2 * decltype(p_c)::value + 1;
-        left -= 2;
-      }
+  // The first turn from step p0 (its branches run once), then whole turns.
+  static_assert(NS % 2 == 0, "whole two-unit steps per ring turn");
+  if (npad > 0) {
+    bwd_static_for<0, NS / 2>([&](auto p_c) {
+      if (decltype(p_c)::value >= p0) step(p_c);
     });
+    for (int u = NS; u < npad; u += NS) bwd_static_for<0, NS / 2>([&](auto p_c) { step(p_c); });
   }
-  // dV/dK of the last unit run (zeros if it was a padding unit).
-  dvdk(lds + last * T::STAGE);
+  // dV/dK of the last unit run, in the ring's last slot (zeros if it was a
+  // padding unit, or the zeroed slot if no unit ran).
+  dvdk(lds + (NS - 1) * T::STAGE);
   if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -708,12 +708,17 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
   const int kv_hi = min(kv_end, kv_lo + a.split_keys);
   const int nunits = kv_hi > kv_lo ? (kv_hi - kv_lo + T::KT - 1) / T::KT : 0;
   const int npad = (nunits + NS - 1) / NS * NS;
+  // The units end in the ring's last slot: the first ring turn starts at step
+  // p0 (slot s0), so at most one padding unit runs and the loop over whole
+  // turns has no branches between its steps.
+  const int p0 = __builtin_amdgcn_readfirstlane((npad - nunits) / 2);
+  const int s0 = 2 * p0;
 
   Dma dma;
   dma.init(wave, lane);
   const uint32_t lds0 = lds_addr(lds);
   int i_row = kv_lo;  // first key row of the next unit to fetch
-  auto issue = [&](int slot) {
+  auto issue = [&](int slot) __attribute__((always_inline)) {
     const int row0 = i_row < kv_hi ? i_row : Nkv;  // past the range: zeros
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
@@ -750,11 +755,11 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
     i_row += T::KT;
   };
 #pragma unroll
-  for (int u = 0; u < T::AHEAD; ++u) issue(u);
+  for (int u = 0; u < T::AHEAD; ++u) issue(s0 + u < NS ? s0 + u : s0 + u - NS);
 
   // The slot read as "unit -1" holds zeros (its dS' is zero too).
   {
-    half_t* zs = lds + (NS - 1) * T::STAGE;
+    half_t* zs = lds + (s0 > 0 ? s0 - 1 : NS - 1) * T::STAGE;
     const u32x4 z = {0u, 0u, 0u, 0u};
     for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
   }
@@ -810,8 +815,9 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
   float16v s_cur = lse16, dp_cur = delta16;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) {
-    s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + r_off[kk]), qf[kk], s_cur);
-    dp_cur = mma<E>(*reinterpret_cast<const half8*>(lds + T::TILE + r_off[kk]), don[kk], dp_cur);
+    s_cur = mma<E>(*reinterpret_cast<const half8*>(lds + s0 * T::STAGE + r_off[kk]), qf[kk], s_cur);
+    dp_cur = mma<E>(*reinterpret_cast<const half8*>(lds + s0 * T::STAGE + T::TILE + r_off[kk]),
+                    don[kk], dp_cur);
   }
   half8 sa_prev[2];
 #pragma unroll
@@ -834,7 +840,7 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
 
   int c_key = kv_lo;  // first key of the unit the body works on
 
-  auto body = [&](auto slot_c) {
+  auto body = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;
     const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
     const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
@@ -925,7 +931,7 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
     for (int h = 0; h < 2; ++h) sa_prev[h] = sa[h];
   };
 
-  auto step = [&](auto p_c) {
+  auto step = [&](auto p_c) __attribute__((always_inline)) {
     constexpr int P = decltype(p_c)::value;
     issue((2 * P + T::AHEAD) % NS);
     issue((2 * P + T::AHEAD + 1) % NS);
@@ -935,19 +941,14 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
     wait_vm_and_barrier<kInFlight>();
   };
 
-  // Whole steps until the work-group's units are done (as in dK/dV above).
-  int left = nunits;
-  int last = NS - 1;
-  for (int u = 0; u < npad && left > 0; u += NS) {
+  // The first turn from step p0, then whole turns (as in dK/dV above).
+  if (npad > 0) {
     bwd_static_for<0, NS / 2>([&](auto p_c) {
-      if (left > 0) {
-        step(p_c);
-        last = 2 * decltype(p_c)::value + 1;
-        left -= 2;
-      }
+      if (decltype(p_c)::value >= p0) step(p_c);
     });
+    for (int u = NS; u < npad; u += NS) bwd_static_for<0, NS / 2>([&](auto p_c) { step(p_c); });
   }
-  dq_mm(lds + last * T::STAGE);  // dQ of the last unit run
+  dq_mm(lds + (NS - 1) * T::STAGE);  // dQ of the last unit run (the ring's last slot)
   if constexpr (kAgprAcc) agpr_acc_drain();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
