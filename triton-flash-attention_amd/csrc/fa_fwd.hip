@@ -492,7 +492,8 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int kv_end = CAUSAL ? min(Nkv, q0 + bm) : Nkv;
   // This work-group's keys: all of [0, kv_end) unless split; with two key
   // groups, the first ceil(units / 2) units go to group 0, the rest to group
-  // 1, and both run the same (padded) number of steps.
+  // 1, and both run the same number of steps (group 1's last unit may lie
+  // past its keys and then counts as dead).
   const int kv_lo_wg = split * a.split_keys;
   const int kv_hi_wg = min(kv_end, kv_lo_wg + a.split_keys);
   const int n_wg = kv_hi_wg > kv_lo_wg ? (kv_hi_wg - kv_lo_wg + T::KT - 1) / T::KT : 0;
