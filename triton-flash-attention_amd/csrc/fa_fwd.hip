@@ -417,6 +417,9 @@ constexpr bool fwd_pipe_tiling_ok() {
 #ifndef FA_FWD_LEAD
 #define FA_FWD_LEAD 3
 #endif
+#ifndef FA_FWD_SKEW
+#define FA_FWD_SKEW 1
+#endif
 
 template <int V>
 using fic = std::integral_constant<int, V>;
@@ -648,13 +651,26 @@ void fwd_pipe_kernel(FwdArgs a) {
     };
     half8 pa[2];
     float pexp[16];
-    float lsum[2];  // set by the first pair
-    // Vector work on value pairs in two stages placed in different groups:
-    //   A: p = exp2(s c - m)        B: row sums, fp16 P^T.
+    float targ[16];  // s c - m of the pairs whose exp runs in the next group
+    float lsum[2];   // set by the first pair
+    // Vector work on value pairs in stages placed in different groups:
+    //   F: s c - m   A: p = exp2(F)   B: row sums, fp16 P^T.
+    // With FA_FWD_SKEW the F stage of a pair runs one group before its A
+    // stage, so no exp waits on the fma just issued.
+    auto stage_f = [&](int pr) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) targ[2 * pr + e] = fmaf(s_cur[2 * pr + e], c, -m_eff);
+      asm volatile("" : "+v"(targ[2 * pr]), "+v"(targ[2 * pr + 1]));
+    };
     auto stage_a = [&](int pr) {
       float p2[2];
+      if constexpr (FA_FWD_SKEW) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -m_eff));
+        for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(targ[2 * pr + e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(fmaf(s_cur[2 * pr + e], c, -m_eff));
+      }
       asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
       pexp[2 * pr] = p2[0];
       pexp[2 * pr + 1] = p2[1];
@@ -677,6 +693,11 @@ void fwd_pipe_kernel(FwdArgs a) {
     asm volatile("" : "+v"(m_eff));
     fwd_static_for<0, (kLead < NTASK ? kLead : NTASK)>(
         [&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+    if constexpr (FA_FWD_SKEW) {
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr)
+        if ((2 * pr * NTASK) / 16 == 0) stage_f(pr);
+    }
     __builtin_amdgcn_sched_barrier(0);
     fwd_static_for<0, NTASK>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
@@ -688,6 +709,11 @@ void fwd_pipe_kernel(FwdArgs a) {
         const int gb = ga + 1 < NTASK ? ga + 1 : NTASK - 1;
         if (ga == i) stage_a(pr);
         if (gb == i) stage_b(pr);
+      }
+      if constexpr (FA_FWD_SKEW) {
+#pragma unroll
+        for (int pr = 0; pr < 8; ++pr)
+          if ((2 * pr * NTASK) / 16 == i + 1) stage_f(pr);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
