@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 6
+#define FA_ABI_VERSION 7
 
 /* Error codes returned before any HIP call is made. */
 #define FA_OK 0
@@ -234,6 +234,20 @@ int fa_fwd_ws_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
                    int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
                    float scale, int causal, void* workspace, int64_t workspace_bytes,
                    void* stream);
+
+/* The forward's launch plan for these sizes (fp16; bf16 uses the same
+ * tilings): out4[0] = work-groups of the persistent job-plan grid, 0 when the
+ * launch runs the grid form (one work-group per (query tile, head) and key
+ * range); out4[1] = work-groups of the grid form; out4[2], out4[3] = the
+ * modelled makespans, in 32-key units per resident work-group slot, of the
+ * plan (0 without one) and of the grid form (0 where no plan is considered).
+ * compute_units > 0 plans for that many CUs, else for the current device.
+ * No HIP launch; no counterpart in the reference, whose forward grid is
+ * (cdiv(N, BLOCK_M), B * Hq) (attention.py:687-688): under the causal mask the
+ * library may instead launch one work-group per resident slot, each running a
+ * bin of (query tile, head) jobs packed to equal lengths. */
+int fa_fwd_plan_info(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                     int causal, int compute_units, int64_t* out4);
 
 /* dQ (with Delta) with split-KV for launches with few work-groups (a few
  * queries against many keys, or few heads): fa_bwd_dq_delta_kv's arguments

@@ -141,6 +141,50 @@ def test_tiling_override_round_trip(lib):
     assert _lib.get_tiling(_lib.KERNEL_FWD, 64, True) == default
 
 
+def _list_schedule_makespan(costs, slots):
+    """Jobs in the given order, each to the first slot to free up."""
+    import heapq
+
+    ends = [0] * slots
+    for c in costs:
+        heapq.heapreplace(ends, ends[0] + c)
+    return max(ends)
+
+
+def test_forward_job_plan_on_a_256_cu_device(lib):
+    """The persistent causal forward's job plan is host logic (no GPU needed
+    with an explicit CU count). At c2 (2048 causal jobs on 256 CUs x 3
+    work-groups) the grid form's heaviest-first list schedule ends in a tail;
+    the plan runs one work-group per slot with a bin of jobs whose modelled
+    length is below the grid's and not below the slots' mean (a lower bound
+    every schedule obeys). Job cost: the 32-key units it streams plus a fixed
+    2-unit part, as the library models it."""
+    plan_variant = 9
+    try:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, plan_variant)
+        info = _lib.fwd_plan_info(4, 16, 16, 4096, 4096, 64, True, 256)
+        costs = [4 * (t + 1) + 2 for t in reversed(range(32)) for _ in range(64)]
+        mean = -(-sum(costs) // 768)
+        assert info["grid_workgroups"] == 2048
+        assert info["grid_makespan"] == _list_schedule_makespan(costs, 768)
+        assert info["plan_workgroups"] == 768
+        assert mean <= info["plan_makespan"] <= 0.97 * info["grid_makespan"]
+        # the grid form where a plan cannot help: bidirectional (equal jobs),
+        # one slot round or less (c3), a longest job above the slots' mean
+        for args in [(4, 16, 16, 4096, 4096, 64, False), (2, 16, 4, 2049, 2049, 64, True),
+                     (2, 16, 16, 4096, 4096, 64, True)]:
+            assert _lib.fwd_plan_info(*args, 256)["plan_workgroups"] == 0, args
+        # a different CU count plans for its own slots
+        assert _lib.fwd_plan_info(4, 16, 16, 4096, 4096, 64, True, 128)["grid_makespan"] > \
+            info["grid_makespan"]
+    finally:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, -1)
+    # D = 128 has no plan variant
+    assert _lib.fwd_plan_info(2, 32, 32, 8192, 8192, 128, True, 256)["plan_workgroups"] == 0
+    with pytest.raises(_lib.FlashAttentionError):
+        _lib.fwd_plan_info(4, 16, 16, 4096, 4096, 48, True, 256)
+
+
 def test_launch_without_a_device_reports_the_hip_error(lib):
     """On a host with no GPU, a well-formed call reaches the launch and the HIP
     runtime's error comes back as a positive code with its message (the fake

@@ -10,8 +10,10 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <memory>
 #include <mutex>
 #include <numeric>
+#include <vector>
 
 #include "../../include/fa_gfx950.h"
 #include "fa_kernels.hpp"
@@ -64,7 +66,11 @@ int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
 //         pipelined, 2 units per barrier (D <= 64); 6 = the same, 1 unit per
 //         barrier and a 6-slot ring (three work-groups per CU); 7 = 8 waves, 32-key
 //         units, pipelined, one work-group per CU (D = 128); 8 = 8 waves as two
-//         4-wave groups that split the keys of 128 queries (D <= 64)
+//         4-wave groups that split the keys of 128 queries (D <= 64); 9 = tiling 6
+//         run as a persistent grid of bin-packed jobs under the causal mask when
+//         its job plan beats the grid's modelled tail (D <= 64; fwd_launch_plan;
+//         measured slower than 6 at every shape where a plan forms, so the table
+//         does not take it)
 //         (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;
@@ -355,6 +361,162 @@ int64_t fwd_workspace_bytes(const FwdSplit& sp, int64_t B, int64_t Hq, int64_t N
   return sp.nsplit > 1 ? (int64_t)sp.nsplit * B * Hq * N * (D + 1) * 4 : 0;
 }
 
+// ---- job plans of the persistent causal forward (variants with kJobs) ----
+// Under the causal mask query tile t streams min(N_kv, (t + 1) * rows) keys,
+// so the grid's work-groups differ in length. The grid deals them heaviest
+// first to the resident slots (list scheduling), and a launch of a few slot
+// rounds then ends with a tail: B4 H16 N4096 D64 has 2048 jobs of 4 .. 128
+// 32-key units on 768 slots (256 CUs x 3), makespan 196 units against 176 if
+// every slot got the same work. A plan instead gives each resident slot one
+// bin of jobs, packed to equal sums (there: tile t with tile 42 - t of the
+// same head, and the light tiles in groups). The plan is taken when its
+// modelled makespan beats the grid's by kPlanMinGain. Measured on MI355X the
+// persistent grid is the slower one wherever a plan forms (B4 H16 N4096 D64
+// 172 vs 162 us, D32 124 vs 114 us, B1 H16 N16384 D64 616 vs 589 us; job
+// overheads of 2, 6 and 12 units in the model change little), while the grid
+// form's own tail there is about 5 % (B8 takes 1.90x, not 2x, the time of B4),
+// so the table keeps the grid form and the plan variant stays a sweep option.
+//
+// Job cost model (32-key units): the units it streams plus kJobOverheadUnits
+// for its fixed part (query fragments, ring fill, epilogue).
+constexpr int kJobOverheadUnits = 2;
+constexpr double kPlanMinGain = 0.03;
+constexpr size_t kPlanCacheEntries = 64;
+
+int64_t fwd_job_cost(int t, int64_t rows, int64_t Nkv) {
+  const int64_t keys = std::min<int64_t>(Nkv, (t + 1) * rows);
+  return (keys + 31) / 32 + kJobOverheadUnits;
+}
+
+// Makespan of the grid form: jobs in grid order (tile rank r -> query tile
+// T - 1 - r, each over BH heads), each taken by the first slot to free up.
+int64_t grid_makespan(int64_t T, int64_t BH, int64_t rows, int64_t Nkv, int64_t slots) {
+  std::vector<int64_t> heap(std::max<int64_t>(1, slots), 0);  // min-heap of slot end times
+  auto cmp = [](int64_t a, int64_t b) { return a > b; };
+  for (int64_t r = 0; r < T; ++r) {
+    const int64_t c = fwd_job_cost((int)(T - 1 - r), rows, Nkv);
+    for (int64_t h = 0; h < BH; ++h) {
+      std::pop_heap(heap.begin(), heap.end(), cmp);
+      heap.back() += c;
+      std::push_heap(heap.begin(), heap.end(), cmp);
+    }
+  }
+  return *std::max_element(heap.begin(), heap.end());
+}
+
+// Best-fit decreasing of one head group's jobs (G heads x T tiles) into nbin
+// bins of capacity cap: each job, heaviest first, goes to the fullest bin it
+// still fits. Returns false when some job fits nowhere.
+bool pack_bins(int64_t G, int64_t T, int64_t rows, int64_t Nkv, int nbin, int64_t cap,
+               std::vector<std::vector<int>>* bins, int64_t* makespan) {
+  std::vector<int64_t> load(nbin, 0);
+  bins->assign(nbin, {});
+  for (int64_t t = T - 1; t >= 0; --t) {  // costs fall with the tile index
+    const int64_t c = fwd_job_cost((int)t, rows, Nkv);
+    for (int64_t h = 0; h < G; ++h) {
+      int best = -1;
+      for (int b = 0; b < nbin; ++b)
+        if (load[b] + c <= cap && (best < 0 || load[b] > load[best])) best = b;
+      if (best < 0) return false;
+      load[best] += c;
+      (*bins)[best].push_back((int)(h * fa::FwdJobs::kTileLimit + t));
+    }
+  }
+  *makespan = *std::max_element(load.begin(), load.end());
+  return true;
+}
+
+struct PlanKey {
+  int64_t N, Nkv, BH, rows, slots;  // slots: resident work-groups (CUs x per CU)
+  bool operator==(const PlanKey& o) const {
+    return N == o.N && Nkv == o.Nkv && BH == o.BH && rows == o.rows && slots == o.slots;
+  }
+};
+
+// The plan for a causal one-pass launch of BH heads over N queries and N_kv
+// keys on `slots` resident work-groups, or null where the grid form is as
+// good (one slot round or less, no packing within the plan's size limits, or
+// too small a gain). Head groups of G heads: ngroups = BH / G groups, each
+// packed into nbin = slots * G / BH bins; G is the smallest that packs.
+std::shared_ptr<const fa::FwdJobs> make_fwd_plan(const PlanKey& k) {
+  const int64_t T = (k.N + k.rows - 1) / k.rows;
+  if (T >= fa::FwdJobs::kTileLimit || T * k.BH <= k.slots) return nullptr;
+  const int64_t grid = grid_makespan(T, k.BH, k.rows, k.Nkv, k.slots);
+  int64_t head_cost = 0;
+  for (int64_t t = 0; t < T; ++t) head_cost += fwd_job_cost((int)t, k.rows, k.Nkv);
+  for (int64_t G = 1; G <= k.BH && G * T <= fa::FwdJobs::kMaxJobs; ++G) {
+    if (k.BH % G) continue;
+    const int64_t ngroups = k.BH / G;
+    if (k.BH % 8 == 0 && ngroups % 8 != 0) continue;  // keep heads on their XCD
+    const int64_t nbin = k.slots * G / k.BH;
+    if (nbin < 1 || nbin > fa::FwdJobs::kMaxBins) continue;
+    const int64_t total = G * head_cost;
+    std::vector<std::vector<int>> bins;
+    int64_t makespan = 0;
+    bool packed = false;
+    for (int64_t cap = (total + nbin - 1) / nbin; cap <= grid && !packed; ++cap)
+      packed = pack_bins(G, T, k.rows, k.Nkv, (int)nbin, cap, &bins, &makespan);
+    if (!packed) continue;
+    if ((double)makespan > (1.0 - kPlanMinGain) * (double)grid) return nullptr;
+    // Every job of the group exactly once.
+    std::vector<int> seen(G * T, 0);
+    for (const auto& bin : bins)
+      for (int e : bin) ++seen[(e / fa::FwdJobs::kTileLimit) * T + e % fa::FwdJobs::kTileLimit];
+    if (std::any_of(seen.begin(), seen.end(), [](int c) { return c != 1; })) return nullptr;
+    auto plan = std::make_shared<fa::FwdJobs>();
+    plan->ngroups = (int)ngroups;
+    plan->nbin = (int)nbin;
+    int n = 0;
+    for (int b = 0; b < nbin; ++b) {
+      plan->start[b] = n;
+      for (int e : bins[b]) plan->job[n++] = e;
+    }
+    plan->start[nbin] = n;
+    return plan;
+  }
+  return nullptr;
+}
+
+std::mutex g_plan_mu;
+std::vector<std::pair<PlanKey, std::shared_ptr<const fa::FwdJobs>>> g_plans;
+
+std::shared_ptr<const fa::FwdJobs> fwd_plan(const PlanKey& k) {
+  std::lock_guard<std::mutex> lock(g_plan_mu);
+  for (const auto& e : g_plans)
+    if (e.first == k) return e.second;
+  auto plan = make_fwd_plan(k);
+  if (g_plans.size() >= kPlanCacheEntries) g_plans.erase(g_plans.begin());
+  g_plans.emplace_back(k, plan);
+  return plan;
+}
+
+// Compute units of the current device (cached per device).
+int current_cu_count() {
+  static std::mutex mu;
+  static int cached[256] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cached[dev] = n > 0 ? n : -1;
+  }
+  return cached[dev];
+}
+
+// The job plan a forward launch with tiling `var` runs on `cus` compute units
+// (0: the current device's), or null for the grid form.
+std::shared_ptr<const fa::FwdJobs> fwd_launch_plan(const fa::Variant& var, int causal, int pack,
+                                                   int nsplit, int64_t BH, int64_t N,
+                                                   int64_t Nkv, int cus = 0) {
+  if (!(var.flags & fa::kJobs) || !causal || pack != 1 || nsplit != 1 || var.per_cu < 1)
+    return nullptr;
+  if (cus < 1) cus = current_cu_count();
+  if (cus < 1) return nullptr;
+  return fwd_plan({N, Nkv, BH, var.rows, (int64_t)cus * var.per_cu});
+}
+
 
 constexpr int kMaxScratchDevices = 256;
 std::mutex g_scratch_mu;
@@ -443,7 +605,11 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   a.nsplit = 1;
   a.split_keys = (int)((Nkv + 127) / 128 * 128);
   a.part = nullptr;
-  if (need == 0 || workspace == nullptr) return launch_result(fn(a, s), name);
+  if (need == 0 || workspace == nullptr) {
+    const auto plan = fwd_launch_plan(*var, causal, a.pack, 1, B * Hq, N, Nkv);
+    a.jobs = plan.get();
+    return launch_result(fn(a, s), name);
+  }
   if (workspace_bytes < need)
     return fail(FA_ERR_BAD_SHAPE, "%s: workspace of %lld bytes is smaller than the %lld bytes "
                 "fa_fwd_workspace_bytes reports", name, (long long)workspace_bytes, (long long)need);
@@ -471,6 +637,44 @@ int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, 
     bytes = std::max(bytes, fwd_workspace_bytes(sp, B, Hq, N_q, D));
   }
   return bytes;
+}
+
+int fa_fwd_plan_info(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_kv, int64_t D,
+                     int causal, int compute_units, int64_t* out4) {
+  if (!out4) return fail(FA_ERR_NULL_POINTER, "fa_fwd_plan_info: null pointer");
+  int rc = check_common(B, Hq, Hkv, N_q, D);
+  if (rc) return rc;
+  if ((rc = check_kv_length(N_kv, D))) return rc;
+  const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, fa::kF16);
+  if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_plan_info: no kernel for the selected tiling");
+  const int pack = fwd_pack(*var, Hq / Hkv, N_q);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, pack);
+  const int64_t grid_wgs = (N_q + var->rows / pack - 1) / (var->rows / pack) * (B * Hq / pack);
+  const auto plan = fwd_launch_plan(*var, causal, pack, sp.nsplit, B * Hq, N_q, N_kv,
+                                    compute_units);
+  out4[0] = plan ? (int64_t)plan->ngroups * plan->nbin : 0;
+  out4[1] = grid_wgs * sp.nsplit;
+  out4[2] = 0;
+  out4[3] = 0;
+  if ((var->flags & fa::kJobs) && causal && pack == 1 && sp.nsplit == 1) {
+    const int cus = compute_units > 0 ? compute_units : current_cu_count();
+    const int64_t slots = (int64_t)std::max(cus, 0) * var->per_cu;
+    const int64_t T = (N_q + var->rows - 1) / var->rows;
+    if (slots > 0) {
+      out4[3] = grid_makespan(T, B * Hq, var->rows, N_kv, slots);
+      if (plan) {
+        int64_t worst = 0;
+        for (int b = 0; b < plan->nbin; ++b) {
+          int64_t sum = 0;
+          for (int j = plan->start[b]; j < plan->start[b + 1]; ++j)
+            sum += fwd_job_cost(plan->job[j] % fa::FwdJobs::kTileLimit, var->rows, N_kv);
+          worst = std::max(worst, sum);
+        }
+        out4[2] = worst;
+      }
+    }
+  }
+  return FA_OK;
 }
 
 static int preprocess_impl(int dt, const char* name, const fa_half_t* o, const fa_half_t* dO,

@@ -438,16 +438,17 @@ __device__ __forceinline__ void static_for_fwd_issue(F&& f) {
   fwd_static_for<0, N>(f);
 }
 
-template <int D, bool CAUSAL, int NW, int UPS, class E = F16, int KG = 1>
-__global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS, KG>::WAVES_PER_SIMD)))
-void fwd_pipe_kernel(FwdArgs a) {
+// One job of the pipelined forward: query tile `qtile` of head block
+// `head_blk` (the work-group's P = a.pack query heads), keys of split `split`.
+// lds_all: the work-group's KG * NSTAGE * STAGE halves of LDS.
+template <int D, bool CAUSAL, int NW, int UPS, class E, int KG>
+__device__ __forceinline__ void fwd_pipe_body(const FwdArgs& a, int split, int qtile,
+                                              int head_blk, half_t* lds_all) {
   using T = FwdPipeTile<D, NW, UPS, KG>;
   using Dma = DmaStager<D, T::KT, T::NWG>;
   static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
   constexpr int NS = T::NSTAGE;
   constexpr int IPU = 2;  // this wave's DMA instructions per unit: K, V
-  __shared__ __attribute__((aligned(16))) half_t lds_all[KG * NS * T::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -459,15 +460,9 @@ void fwd_pipe_kernel(FwdArgs a) {
   const int ql = lane & 31;
   const int g = lane >> 5;
 
-  // Split-KV mode: the split index is the slowest-varying part of the block
-  // index. Packed GQA: the work-group serves P query heads, wave w head w % P.
+  // Packed GQA: the work-group serves P query heads, wave w head w % P.
   const int P = a.pack;
-  const int row_wgs = a.BH / P;  // work-groups per tile row
-  const int split = blockIdx.x / (a.num_tiles * row_wgs);
-  const TileHead th =
-      decode_block_grouped(blockIdx.x - split * a.num_tiles * row_wgs, row_wgs, a.group / P);
-  const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
-  const int head = th.head * P + wave % P;  // wave-uniform
+  const int head = head_blk * P + wave % P;  // wave-uniform
   const int b = head / a.Hq;
   const int hq = head - b * a.Hq;
   const int kvh = b * a.Hkv + hq / a.group;
@@ -537,7 +532,11 @@ void fwd_pipe_kernel(FwdArgs a) {
   // The V tile read as "unit -1" holds zeros (its P is zero too).
   {
     half_t* zs = lds + (s0 > 0 ? s0 - 1 : NS - 1) * T::STAGE + T::TILE;
-    const u32x4 z = {0u, 0u, 0u, 0u};
+    // The zero comes from an asm move, so the persistent form's job loop
+    // cannot hoist it and keep (or spill) it across the jobs.
+    unsigned zr;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zr));
+    const u32x4 z = {zr, zr, zr, zr};
     for (int i = tid - gk * 64 * T::NWG; i < T::TILE / 8; i += 64 * T::NWG)
       *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
   }
@@ -807,7 +806,91 @@ void fwd_pipe_kernel(FwdArgs a) {
   store_fwd_output<D, E>(a, ro, split, head, qrow, g, o, m, lt);
 }
 
+// The grid form: one job per work-group, tile-major / head-minor (heaviest
+// causal tiles first), the split index slowest.
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16, int KG = 1>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, UPS, KG>::WAVES_PER_SIMD)))
+void fwd_pipe_kernel(FwdArgs a) {
+  using T = FwdPipeTile<D, NW, UPS, KG>;
+  __shared__ __attribute__((aligned(16))) half_t lds_all[KG * T::NSTAGE * T::STAGE];
+  const int row_wgs = a.BH / a.pack;  // work-groups per tile row
+  const int split = blockIdx.x / (a.num_tiles * row_wgs);
+  const TileHead th = decode_block_grouped(blockIdx.x - split * a.num_tiles * row_wgs, row_wgs,
+                                           a.group / a.pack);
+  const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
+  fwd_pipe_body<D, CAUSAL, NW, UPS, E, KG>(a, split, qtile, th.head, lds_all);
+}
+
+// The persistent form (causal, one pass, one head per work-group): one
+// work-group per slot of the plan, running the jobs of its bin in order.
+// Slot s serves head group s % ngroups and bin s / ngroups; job (hoff, qtile)
+// of that bin is query tile qtile of head position ngroups * hoff + group,
+// mapped to a head as the grid form maps tile-row positions (so with the
+// same XCD for all of a key/value head's query heads when ngroups is a
+// multiple of 8). The LDS ring is reused from job to job: a barrier between
+// jobs keeps the next job's first DMA from overwriting tiles a slower wave
+// still reads.
+template <int D, int NW, class E = F16>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, NW, 1, 1>::WAVES_PER_SIMD)))
+void fwd_pipe_jobs_kernel(FwdArgs a, FwdJobs jobs) {
+  using T = FwdPipeTile<D, NW, 1, 1>;
+  __shared__ __attribute__((aligned(16))) half_t lds_all[T::NSTAGE * T::STAGE];
+  const int gi = blockIdx.x % jobs.ngroups;
+  const int bin = blockIdx.x / jobs.ngroups;
+  const int j0 = jobs.start[bin];
+  const int j1 = jobs.start[bin + 1];
+  const int bhkv = a.BH / a.group;
+  for (int j = j0; j < j1; ++j) {
+    const int e = jobs.job[j];
+    const int qtile = e & (FwdJobs::kTileLimit - 1);
+    const int p = gi + jobs.ngroups * (e / FwdJobs::kTileLimit);
+    const int head = (a.group > 1 && bhkv % 8 == 0) ? (p % bhkv) * a.group + p / bhkv : p;
+    if (j > j0) __syncthreads();
+    fwd_pipe_body<D, true, NW, 1, E, 1>(a, 0, qtile, head, lds_all);
+  }
+}
+
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16, int KG = 1>
+hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream);
+
+// The plan variants: the persistent form when the host attached a job plan
+// (causal, one pass, one head per work-group), else the grid form of the
+// same tiling (split-KV and packed GQA included).
+template <int D, bool CAUSAL, int NW, class E>
+hipError_t fwd_pipe_jobs_launch(const FwdArgs& a, hipStream_t stream) {
+  using T = FwdPipeTile<D, NW, 1, 1>;
+  if constexpr (!CAUSAL) {
+    return fwd_pipe_launch<D, CAUSAL, NW, 1, E, 1>(a, stream);
+  } else {
+    const FwdJobs* jb = a.jobs;
+    if (jb == nullptr) return fwd_pipe_launch<D, CAUSAL, NW, 1, E, 1>(a, stream);
+    if (a.pack != 1 || a.nsplit != 1 || jb->ngroups < 1 || jb->nbin < 1 ||
+        jb->nbin > FwdJobs::kMaxBins || jb->start[0] != 0 ||
+        jb->start[jb->nbin] > FwdJobs::kMaxJobs || a.BH % jb->ngroups != 0)
+      return hipErrorInvalidValue;
+    FwdArgs b = a;
+    b.num_tiles = (a.N + T::BM - 1) / T::BM;
+    // Every job must name a query tile and a head of this launch.
+    const int per_group = a.BH / jb->ngroups;
+    for (int i = 0; i < jb->nbin; ++i)
+      if (jb->start[i + 1] < jb->start[i]) return hipErrorInvalidValue;
+    for (int j = 0; j < jb->start[jb->nbin]; ++j) {
+      const int e = jb->job[j];
+      if (e < 0 || (e & (FwdJobs::kTileLimit - 1)) >= b.num_tiles ||
+          e / FwdJobs::kTileLimit >= per_group)
+        return hipErrorInvalidValue;
+    }
+    const int64_t blocks = (int64_t)jb->ngroups * jb->nbin;
+    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((fwd_pipe_jobs_kernel<D, NW, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
+                       stream, b, *jb);
+    return hipGetLastError();
+  }
+}
+
+template <int D, bool CAUSAL, int NW, int UPS, class E, int KG>
 hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdPipeTile<D, NW, UPS, KG>;
   FwdArgs b = a;
@@ -828,6 +911,14 @@ template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 constexpr void* fwd_pipe_entry() {
   if constexpr (fwd_pipe_tiling_ok<D, NW, UPS>())
     return (void*)&fwd_pipe_launch<D, CAUSAL, NW, UPS, E>;
+  else
+    return nullptr;
+}
+// The plan variants (one unit per barrier; grid form without a plan).
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
+constexpr void* fwd_pipe_jobs_entry() {
+  if constexpr (fwd_pipe_tiling_ok<D, NW, UPS>() && UPS == 1 && NW == 4 && D <= 64)
+    return (void*)&fwd_pipe_jobs_launch<D, CAUSAL, NW, E>;
   else
     return nullptr;
 }
@@ -956,6 +1047,11 @@ static const Variant kFwdVariants[] = {
     {8, 128, 32,
      {FA_ENTRIES(fwd_pipe_kg_entry, F16, 8, 1), FA_ENTRIES(fwd_pipe_kg_entry, BF16, 8, 1)},
      kSplitsKv | kKeyGroups},
+    // 9: tiling 6 with the persistent job-plan form under the mask (D <= 64;
+    // at D = 128 the 8-wave kernel's launches leave no tail to recover)
+    {4, 128, 32,
+     {FA_ENTRIES(fwd_pipe_jobs_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe_jobs_entry, BF16, 4, 1)},
+     kSplitsKv | kJobs, FwdPipeTile<64, 4, 1>::WGS_PER_CU},
 };
 
 const Variant* fwd_variants(int* count) {

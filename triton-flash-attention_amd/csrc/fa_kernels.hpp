@@ -12,6 +12,21 @@ typedef _Float16 half_t;
 // 1 / ln(2): converts natural-log scores to the base-2 domain (attention.py:20).
 constexpr float kLog2e = 1.4426950408889634f;
 
+// A persistent causal forward's job plan (the launch takes it by value): the
+// grid has ngroups * nbin work-groups; work-group s serves head group
+// s % ngroups and runs the jobs job[start[b] .. start[b + 1]) of bin
+// b = s / ngroups in order. A job is hoff * kTileLimit + qtile: query tile
+// qtile of the head at tile-row position ngroups * hoff + s % ngroups.
+struct FwdJobs {
+  static constexpr int kMaxBins = 64;
+  static constexpr int kMaxJobs = 256;
+  static constexpr int kTileLimit = 1 << 16;
+  int ngroups;
+  int nbin;
+  int start[kMaxBins + 1];
+  int job[kMaxJobs];
+};
+
 // Arguments of one forward launch (the values _attn_fwd receives at
 // attention.py:690-718, minus strides: every tensor is contiguous).
 struct FwdArgs {
@@ -41,6 +56,9 @@ struct FwdArgs {
   // head, wave w taking head w % pack and rows 32 * (w / pack) onward, so the
   // heads share each K/V tile the work-group streams.
   int pack;
+  // Host-side plan of the persistent forward variant (kJobs); its launcher
+  // passes *jobs to the kernel by value. Unused by the other variants.
+  const FwdJobs* jobs = nullptr;
 };
 
 // Arguments of the backward launches (attention.py:736-770).
@@ -92,7 +110,8 @@ struct Variant {
   int rows;
   int tile;
   void* fn[2][3][2];  // [element type: fp16, bf16][D index: 32, 64, 128][causal]; null = not compiled
-  int flags;          // kFusesDelta, kSplitsKv
+  int flags;          // kFusesDelta, kSplitsKv, kPairs, kKeyGroups, kJobs
+  int per_cu = 0;     // kJobs: work-groups resident per CU (the plan's slots per CU)
 };
 
 // Element type index of Variant::fn.
@@ -116,6 +135,9 @@ constexpr int kPairs = 4;
 // The forward variant splits each work-group's keys over two wave groups
 // (one query head per work-group: no packed GQA).
 constexpr int kKeyGroups = 8;
+// The forward variant runs a causal one-pass launch as a persistent grid when
+// the host attaches a job plan (FwdArgs::jobs), else as the grid form.
+constexpr int kJobs = 16;
 
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);

@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 FA_OK = 0
 FA_ERR_NULL_POINTER = -1
@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _INT,
         (_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _INT, _P),
     ),
+    "fa_fwd_plan_info": (_INT, (_I64, _I64, _I64, _I64, _I64, _I64, _INT, _INT, ctypes.POINTER(ctypes.c_int64))),
     "fa_last_error": (ctypes.c_char_p, ()),
     "fa_abi_version": (_INT, ()),
     "fa_get_tiling": (_INT, (_INT, _I64, _INT, _INT_P)),
@@ -197,6 +198,17 @@ def tiling_variants(kernel: int, head_dim: int, causal: bool) -> list[dict[str, 
         check(rc)
         result.append({"waves": out[0], "rows": out[1], "tile": out[2], "variant": out[3]})
     return result
+
+
+def fwd_plan_info(B: int, Hq: int, Hkv: int, N_q: int, N_kv: int, D: int, causal: bool,
+                  compute_units: int = 0) -> dict[str, int]:
+    """The forward's launch plan for these sizes (fa_fwd_plan_info): work-groups
+    of the persistent job-plan grid (0: the grid form runs), of the grid form,
+    and the modelled makespans (32-key units per slot) of both."""
+    out = (ctypes.c_int64 * 4)()
+    check(load().fa_fwd_plan_info(B, Hq, Hkv, N_q, N_kv, D, int(causal), compute_units, out))
+    return {"plan_workgroups": out[0], "grid_workgroups": out[1],
+            "plan_makespan": out[2], "grid_makespan": out[3]}
 
 
 def set_tiling(kernel: int, head_dim: int, causal: bool, variant: int) -> None:
