@@ -320,21 +320,24 @@ FWD_PLAN_VARIANT = 9  # the same tiling as a persistent grid of bin-packed jobs
 
 
 @pytest.mark.parametrize("case", [
-    (4, 16, 16, 4096, 64, torch.float16),   # c2: 2048 jobs of 4..128 units on 768 slots
-    (4, 16, 16, 4096, 32, torch.float16),
-    (1, 32, 8, 8192, 64, torch.float16),    # GQA: heads permuted so a group shares an XCD
-    (2, 16, 16, 8192, 64, torch.bfloat16),
-], ids=lambda c: "x".join(str(x) for x in c[:5]) + f"-{str(c[5])[6:]}")
+    # (B, Hq, Hkv, N_q, N_kv, D, dtype)
+    (4, 16, 16, 4096, 4096, 64, torch.float16),  # c2: 2048 jobs of 4..128 units on 768 slots
+    (4, 16, 16, 4096, 4096, 32, torch.float16),
+    (1, 32, 8, 8192, 8192, 64, torch.float16),   # GQA: heads permuted so a group shares an XCD
+    (2, 16, 16, 8192, 8192, 64, torch.bfloat16),
+    (4, 16, 16, 4000, 4096, 64, torch.float16),  # ragged last query tile, more keys
+    (8, 8, 2, 4096, 6000, 64, torch.float16),    # cross-attention, GQA
+], ids=lambda c: "x".join(str(x) for x in c[:6]) + f"-{str(c[6])[6:]}")
 def test_persistent_forward_plan_matches_grid_bitwise(case):
     """Under the causal mask the plan variant runs each (query tile, head) job
     with the grid form's code, in another order on a persistent grid: O and LSE
     equal the grid form's bit for bit (so every job ran once). On a 256-CU
     MI355X these shapes get a plan; the grid form itself is checked against
     the oracle elsewhere, and here against the fp32 reference on a few heads."""
-    B, Hq, Hkv, N, D, dt = case
-    tag = f"plan forward B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} {dt}"
+    B, Hq, Hkv, N, Nkv, D, dt = case
+    tag = f"plan forward B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} {dt}"
     _note(tag)
-    q, k, v, _ = make_inputs(B, Hq, Hkv, N, D, seed=N + D)
+    q, k, v, _ = make_inputs(B, Hq, Hkv, N, D, seed=N + D, n_kv=Nkv)
     qd, kd, vd = (t.to(DEV).to(dt) for t in (q, k, v))
     scale = D ** -0.5
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -342,7 +345,7 @@ def test_persistent_forward_plan_matches_grid_bitwise(case):
     for var in (FWD_GRID_VARIANT, FWD_PLAN_VARIANT):
         _lib.set_tiling(_lib.KERNEL_FWD, D, True, var)
         try:
-            info = _lib.fwd_plan_info(B, Hq, Hkv, N, N, D, True)
+            info = _lib.fwd_plan_info(B, Hq, Hkv, N, Nkv, D, True)
             outs[var] = _ops.flash_fwd(qd, kd, vd, True, scale)
         finally:
             _lib.set_tiling(_lib.KERNEL_FWD, D, True, -1)
@@ -357,15 +360,19 @@ def test_persistent_forward_plan_matches_grid_bitwise(case):
     (o_g, lse_g), (o_p, lse_p) = outs[FWD_GRID_VARIANT], outs[FWD_PLAN_VARIANT]
     assert torch.equal(o_p, o_g), tag + ": O differs from the grid form"
     assert torch.equal(lse_p, lse_g), tag + ": LSE differs from the grid form"
-    # a few heads against the fp32 reference (the causal last rows see every key)
-    hs = [0, Hq // 2, Hq - 1]
-    kv = [h // (Hq // Hkv) for h in hs]
-    q3, k3, v3 = qd[:1, hs].float(), kd[:1, kv].float(), vd[:1, kv].float()
-    ref = torch_reference_fp32(q3, k3, v3, torch.zeros_like(q3), True, scale)
-    assert_close(tag + " o vs fp32", o_p[:1, hs].double().cpu().numpy(),
-                 ref["o"].double().cpu().numpy())
-    lse_err = float((lse_p[:1, hs] - ref["lse"]).abs().max())
-    assert lse_err <= LSE_TOL, f"{tag} lse vs fp32: {lse_err:.3e}"
+    # a few heads against plain fp32 attention (top-left causal mask: query i
+    # sees keys 0..i, as SDPA's is_causal for any N_q, N_kv)
+    mask = torch.ones((N, Nkv), device=DEV, dtype=torch.bool).triu_(1)
+    for h in (0, Hq // 2, Hq - 1):
+        kvh = h // (Hq // Hkv)
+        s = torch.matmul(qd[0, h].float(), kd[0, kvh].float().t().contiguous()) * scale
+        s = s.masked_fill(mask, float("-inf"))
+        lse_ref = torch.logsumexp(s, dim=-1) * (1.0 / math.log(2.0))
+        o_ref = torch.matmul(torch.softmax(s, dim=-1), vd[0, kvh].float())
+        assert_close(f"{tag} head {h} o vs fp32", o_p[0, h].double().cpu().numpy(),
+                     o_ref.double().cpu().numpy())
+        lse_err = float((lse_p[0, h] - lse_ref).abs().max())
+        assert lse_err <= LSE_TOL, f"{tag} head {h} lse vs fp32: {lse_err:.3e}"
 
 
 def test_whole_backward_without_a_workspace_runs_one_pass():
