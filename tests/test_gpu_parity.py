@@ -1183,6 +1183,43 @@ def test_random_envelope_matches_oracle(case):
         assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name], **tols)
 
 
+def test_gradients_beyond_the_fp16_grid_of_the_tolerance():
+    """One key and 1845 queries under the causal mask: every query attends to
+    key 0 with P = 1, so dV of that key sums 1845 dO rows and reaches |dV| of
+    about 80. An fp16 output cannot hold such values to the north-star max-abs
+    2e-2: half an fp16 ulp is 0.031 on [64, 128). A 4000-shape random sweep
+    found this: the fp64 value 67.2196 lies 0.0009 above the rounding midpoint
+    67.21875, and the kernel's fp32 sum landed on the other neighbour, 67.1875
+    (error 0.032). The bound here is the tolerance or, where fp16 cannot meet
+    it, half an ulp of the fp64 value plus 1e-3 of fp32 summation; rel-L2 stays
+    at the north-star 5e-3."""
+    B, Hq, Hkv, N, Nkv, D = 2, 8, 8, 1845, 1, 64
+    tag = f"single key B={B} H={Hq} N_q={N} N_kv={Nkv} D={D} causal"
+    _note(tag)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=20000710, mult=0.5, n_kv=Nkv)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = scaled_dot_product_attention(qd, kd, vd, is_causal=True, backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
+    torch.cuda.synchronize()
+    f = lambda t: t.float().numpy()
+    ref = oracle.attention(f(q), f(k), f(v), f(do), True, None,
+                           o16=out.detach().float().cpu().numpy(), fold_bwd=True)
+    assert np.abs(ref["dv"]).max() > 64  # the case reaches past the tolerance's fp16 grid
+    # O = V[0], and dQ = dK = 0 in exact arithmetic (one key: dS = P (dP - Delta) = 0):
+    # the north-star tolerances as they stand
+    for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk)):
+        assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name])
+    got, exp = dv.double().cpu().numpy(), ref["dv"]
+    half_ulp = np.spacing(np.abs(exp).astype(np.float16)).astype(np.float64) / 2
+    bound = np.maximum(MAX_ABS_TOL, half_ulp + 1e-3)
+    err = np.abs(got - exp)
+    assert (err <= bound).all(), f"{tag} dv: {int((err > bound).sum())} beyond the bound"
+    rel = float(np.linalg.norm(got - exp) / np.linalg.norm(exp))
+    assert rel <= REL_L2_TOL, f"{tag} dv: rel-L2 {rel:.2e}"
+    _note(f"  dv: max-abs {err.max():.3e} at |ref| {np.abs(exp).flat[err.argmax()]:.2f}, "
+          f"rel-L2 {rel:.2e}")
+
+
 # ---------------------------------------------------------------------------
 # Split-KV forward (few work-groups: decoding, few heads)
 # ---------------------------------------------------------------------------
