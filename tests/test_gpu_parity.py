@@ -1183,6 +1183,82 @@ def test_random_envelope_matches_oracle(case):
         assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name], **tols)
 
 
+def _large_random_cases(count=8, seed=11):
+    """Seeded large shapes (N_q, N_kv 1000-16384, GQA groups 1-8, padded head
+    sizes, both masks and dtypes), bounded so the fp32 reference of one key/
+    value head group fits in a few GiB."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < count:
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        B = int(rng.choice([1, 2]))
+        N = int(rng.integers(1000, 16385))
+        Nkv = N if rng.random() < 0.7 else int(rng.integers(1000, 16385))
+        D = int(rng.choice([32, 64, 128, 128, 64, 96, 48]))
+        if G * N * Nkv > 2 ** 29 or B * Hkv * G * N * Nkv * D > 1e12:
+            continue
+        cases.append(dict(B=B, Hq=Hkv * G, Hkv=Hkv, N=N, Nkv=Nkv, D=D,
+                          causal=bool(rng.random() < 0.5),
+                          dtype=torch.bfloat16 if rng.random() < 0.25 else torch.float16,
+                          scale=None if rng.random() < 0.7 else float(rng.uniform(0.05, 0.4)),
+                          seed=seed * 1000 + len(cases)))
+    return cases
+
+
+def _fp32_group_reference(q, k, v, do, causal, scale):
+    """Plain fp32 attention of one key/value head on the GPU: q, do [G, N_q, D],
+    k, v [N_kv, D] (top-left causal mask). O, base-2 LSE, dQ, dK, dV."""
+    q, k, v = (t.float().clone().requires_grad_() for t in (q, k, v))
+    s = torch.matmul(q, k.t().contiguous().unsqueeze(0).expand(q.shape[0], -1, -1)) * scale
+    if causal:
+        mask = torch.ones((q.shape[1], k.shape[0]), device=q.device, dtype=torch.bool).triu_(1)
+        s = s.masked_fill(mask, float("-inf"))
+    lse2 = torch.logsumexp(s, dim=-1) * (1.0 / math.log(2.0))
+    o = torch.matmul(torch.softmax(s, dim=-1), v.unsqueeze(0).expand(q.shape[0], -1, -1))
+    dq, dk, dv = torch.autograd.grad(o, (q, k, v), do.float())
+    return o.detach(), lse2.detach(), dq, dk, dv
+
+
+@pytest.mark.parametrize("case", _large_random_cases(), ids=lambda c: f"seed{c['seed']}")
+def test_random_large_shapes_match_fp32_reference(case):
+    """Seeded random large shapes through the public API against plain fp32
+    attention on the GPU, one key/value head group at a time: O, dQ, dK, dV at
+    the north-star tolerances (bf16: 4x) and LSE at 1e-4 for the native head
+    sizes. (One-off runs of the same generator passed 400 shapes.)"""
+    c = case
+    tag = (f"large seed={c['seed']} B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} N_q={c['N']} "
+           f"N_kv={c['Nkv']} D={c['D']} causal={c['causal']} {str(c['dtype'])[6:]} "
+           f"scale={c['scale']}")
+    _note(tag)
+    B, Hq, Hkv, D = c["B"], c["Hq"], c["Hkv"], c["D"]
+    G = Hq // Hkv
+    q, k, v, do = make_inputs(B, Hq, Hkv, c["N"], D, seed=c["seed"], mult=0.5, dtype=c["dtype"],
+                              n_kv=c["Nkv"])
+    qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+    qg, kg, vg = (t.clone().requires_grad_() for t in (qd, kd, vd))
+    out = scaled_dot_product_attention(qg, kg, vg, is_causal=c["causal"], scale=c["scale"],
+                                       enable_gqa=G > 1, backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qg, kg, vg), dod)
+    scale = D ** -0.5 if c["scale"] is None else c["scale"]
+    lse = _ops.flash_fwd(qd, kd, vd, c["causal"], scale)[1] if D in (32, 64, 128) else None
+    torch.cuda.synchronize()
+    bf16 = c["dtype"] == torch.bfloat16
+    tols = dict(max_abs=BF16_MAX_ABS_TOL, rel_l2=BF16_REL_L2_TOL) if bf16 else {}
+    for b in range(B):
+        for h in range(Hkv):
+            hs = slice(h * G, (h + 1) * G)
+            o_r, l_r, dq_r, dk_r, dv_r = _fp32_group_reference(
+                qd[b, hs], kd[b, h], vd[b, h], dod[b, hs], c["causal"], scale)
+            for name, got, exp in (("o", out[b, hs], o_r), ("dq", dq[b, hs], dq_r),
+                                   ("dk", dk[b, h], dk_r), ("dv", dv[b, h], dv_r)):
+                assert_close(f"{tag} b{b} h{h} {name}", got.detach().double().cpu().numpy(),
+                             exp.double().cpu().numpy(), **tols)
+            if lse is not None:
+                err = float((lse[b, hs] - l_r).abs().max())
+                assert err <= LSE_TOL, f"{tag} b{b} h{h} lse {err:.2e}"
+
+
 def test_gradients_beyond_the_fp16_grid_of_the_tolerance():
     """One key and 1845 queries under the causal mask: every query attends to
     key 0 with P = 1, so dV of that key sums 1845 dO rows and reaches |dV| of
