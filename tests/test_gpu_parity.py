@@ -1259,6 +1259,57 @@ def test_random_large_shapes_match_fp32_reference(case):
                 assert err <= LSE_TOL, f"{tag} b{b} h{h} lse {err:.2e}"
 
 
+@pytest.mark.parametrize("case", [
+    # (B, Hq, Hkv, N_q, N_kv, D, causal, dtype)
+    (1, 2, 1, 100, 77, 64, False, torch.float16),    # keys past the last 32-key unit
+    (2, 4, 2, 142, 7, 64, True, torch.float16),      # causal cross-attention, N_q > N_kv
+    (1, 4, 4, 16, 3000, 64, False, torch.float16),   # split dQ: a range's padding unit
+    (1, 2, 1, 90, 45, 128, False, torch.bfloat16),
+    (1, 2, 1, 70, 33, 32, False, torch.float16),
+], ids=lambda c: "x".join(str(x) for x in c[:7]) + f"-{str(c[7])[6:]}")
+def test_dq_with_very_negative_scores_and_a_key_tail(case):
+    """Every score of every row far below zero (base-2 LSE below -128), with
+    keys past the last 32-key unit or past a split range. Those keys load as
+    zero rows; their P must be 0, as the reference's valid-key mask makes it
+    (attention.py:339-340). A zero score against an LSE below -128 would
+    otherwise overflow exp2 to inf, and inf times the zero key row is NaN in
+    dQ. A random sweep with inputs x4 and scales up to 8 found this in causal
+    cross-attention; bidirectional launches with N_kv % 32 != 0 and split dQ
+    ranges had the same exposure."""
+    B, Hq, Hkv, N, Nkv, D, causal, dt = case
+    tag = f"negative scores B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} causal={causal} {dt}"
+    _note(tag)
+    g = torch.Generator("cpu").manual_seed(N * 1000 + Nkv)
+    a = 4.6  # q ~ +a, k ~ -a per element: scores ~ -a^2 D, times scale log2(e) < -128
+    q = (a + 0.3 * torch.randn((B, Hq, N, D), generator=g)).to(dt)
+    k = (-a + 0.3 * torch.randn((B, Hkv, Nkv, D), generator=g)).to(dt)
+    v = torch.randn((B, Hkv, Nkv, D), generator=g).to(dt)
+    do = torch.randn((B, Hq, N, D), generator=g).to(dt)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    gqa = Hq != Hkv
+    out = scaled_dot_product_attention(qd, kd, vd, is_causal=causal, enable_gqa=gqa,
+                                       backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
+    _, lse = _ops.flash_fwd(qd.detach(), kd.detach(), vd.detach(), causal, D ** -0.5)
+    torch.cuda.synchronize()
+    assert float(lse.max()) < -128, f"{tag}: the case must put every LSE below -128"
+    for name, t in (("o", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert bool(torch.isfinite(t).all()), f"{tag}: {name} is not finite"
+    f = lambda t: t.float().numpy()
+    bf16 = dt == torch.bfloat16
+    ref = oracle.attention(f(q), f(k), f(v), f(do), causal, None,
+                           o16=out.detach().float().cpu().numpy(),
+                           fold_bwd="bfloat16" if bf16 else True)
+    max_abs, rel_l2 = (BF16_MAX_ABS_TOL, BF16_REL_L2_TOL) if bf16 else (MAX_ABS_TOL, REL_L2_TOL)
+    for name, t in (("o", out.detach()), ("dq", dq), ("dk", dk), ("dv", dv)):
+        # dQ sums scale dS K over keys whose common -4.6 part cancels (each row of
+        # dS sums to zero), leaving a result ~15x smaller than its terms: the
+        # operands' rounding weighs that much more in its relative error
+        rel = 4 * rel_l2 if name == "dq" else rel_l2
+        assert_close(f"{tag} {name}", t.double().cpu().numpy(), ref[name], max_abs=max_abs,
+                     rel_l2=rel)
+
+
 def test_gradients_beyond_the_fp16_grid_of_the_tolerance():
     """One key and 1845 queries under the causal mask: every query attends to
     key 0 with P = 1, so dV of that key sums 1845 dO rows and reaches |dV| of

@@ -713,13 +713,13 @@ hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
 }
 
 // One work-group of dq_pipe_body per block.
-template <int D, bool CAUSAL, int NW, class E = F16>
+template <int D, bool CAUSAL, int NW, class E = F16, bool TAIL = true>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(DqPipeTile<D, NW>::WGS_PER_CU)))
 void dq_pipe_kernel(BwdArgs a) {
   using T = DqPipeTile<D, NW>;
   __shared__ __attribute__((aligned(16))) half_t lds[T::NSTAGE * T::STAGE];
-  dq_pipe_body<D, CAUSAL, NW, E>(a, blockIdx.x, lds);
+  dq_pipe_body<D, CAUSAL, NW, E, TAIL>(a, blockIdx.x, lds);
 }
 
 template <int D, bool CAUSAL, int NW, class E = F16>
@@ -732,8 +732,12 @@ hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
-                     stream, b);
+  if (dq_tail_free(b, CAUSAL))
+    hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW, E, false>), dim3((unsigned)blocks),
+                       dim3(T::NT), 0, stream, b);
+  else
+    hipLaunchKernelGGL((dq_pipe_kernel<D, CAUSAL, NW, E, true>), dim3((unsigned)blocks),
+                       dim3(T::NT), 0, stream, b);
   return hipGetLastError();
 }
 

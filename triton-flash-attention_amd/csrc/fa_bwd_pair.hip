@@ -31,7 +31,7 @@ namespace fa {
 
 constexpr int kPairWaves = 4;
 
-template <int D, bool CAUSAL, int NW, class E>
+template <int D, bool CAUSAL, int NW, class E, bool TAIL>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(DkdvPipeTile<D, NW>::WGS_PER_CU)))
 void bwd_pair_kernel(BwdArgs ad, BwdArgs aq, unsigned n_dkdv, unsigned n_dq) {
@@ -47,7 +47,7 @@ void bwd_pair_kernel(BwdArgs ad, BwdArgs aq, unsigned n_dkdv, unsigned n_dq) {
   const bool dq = i < both ? (i & 1u) != 0 : n_dq > n_dkdv;
   const unsigned idx = i < both ? i >> 1 : both / 2 + (i - both);
   if (dq)
-    dq_pipe_body<D, CAUSAL, NW, E>(aq, idx, lds);
+    dq_pipe_body<D, CAUSAL, NW, E, TAIL>(aq, idx, lds);
   else
     dkdv_pipe_body<D, CAUSAL, NW, E>(ad, idx, lds);
 }
@@ -71,8 +71,12 @@ hipError_t bwd_pair_launch(const BwdArgs& dkdv, const BwdArgs& dq, hipStream_t s
   const int64_t nk = (int64_t)ad.num_tiles * ad.BHkv * ad.nsplit;
   const int64_t nq = (int64_t)aq.num_tiles * aq.BH;
   if (nk <= 0 || nq <= 0 || nk + nq > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((bwd_pair_kernel<D, CAUSAL, NW, E>), dim3((unsigned)(nk + nq)), dim3(TK::NT),
-                     0, stream, ad, aq, (unsigned)nk, (unsigned)nq);
+  if (dq_tail_free(aq, CAUSAL))
+    hipLaunchKernelGGL((bwd_pair_kernel<D, CAUSAL, NW, E, false>), dim3((unsigned)(nk + nq)),
+                       dim3(TK::NT), 0, stream, ad, aq, (unsigned)nk, (unsigned)nq);
+  else
+    hipLaunchKernelGGL((bwd_pair_kernel<D, CAUSAL, NW, E, true>), dim3((unsigned)(nk + nq)),
+                       dim3(TK::NT), 0, stream, ad, aq, (unsigned)nk, (unsigned)nq);
   return hipGetLastError();
 }
 

@@ -626,7 +626,18 @@ constexpr bool dq_pipe_tiling_ok() {
 #define FA_DQ_LEAD 3
 #endif
 
-template <int D, bool CAUSAL, int NW, class E>
+// A dQ launch whose key ranges have no unit reaching past them that its
+// queries see: the causal mask hides keys past N_kv when N_q <= N_kv (in one
+// pass), and a bidirectional pass over N_kv a multiple of 64 has whole units
+// in even number (no padding unit). Those launches skip the tail test.
+inline bool dq_tail_free(const BwdArgs& a, bool causal) {
+  if (a.nsplit != 1) return false;
+  return causal ? a.N <= a.Nkv : a.Nkv % 64 == 0;
+}
+
+// TAIL: the launch may have units with keys past its range (see the body);
+// dq_tail_free() says when it cannot.
+template <int D, bool CAUSAL, int NW, class E, bool TAIL = true>
 __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned block,
                                         half_t* __restrict__ lds) {
   using T = DqPipeTile<D, NW>;
@@ -847,16 +858,33 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
     const int ka = c_key;
     c_key += T::KT;
 
+    // Keys past the range (past N_kv, or a padding unit) load as zero rows and
+    // get P = 0, as the reference's invalid keys do (attention.py:339-340): a
+    // zero score against an LSE below -128 would overflow exp2, and inf times
+    // the zero key row is NaN. Such keys can only be in the range's last unit
+    // or the padding unit after it, which the rotated ring start puts in the
+    // ring's last two slots; the other bodies, and launches without such
+    // units (TAIL = false), carry no test for them.
+    constexpr bool kTailSlot = TAIL && SLOT >= NS - 2;
     if constexpr (CAUSAL) {
       if (ka > q0w) {
         // every key of the unit follows every query of the wave
 #pragma unroll
         for (int j = 0; j < 16; ++j) s_cur[j] = inf;
-      } else if (ka == q0w) {
-        // diagonal unit: key 16h + 8g + e (value j = 8h + e) is kept iff <= query ql
+      } else if (ka == q0w || (kTailSlot && ka + T::KT > kv_hi)) {
+        // diagonal or tail unit: key ka + 16h + 8g + e (value j = 8h + e) is
+        // kept iff it is <= the lane's query (and < kv_hi)
+        const int lim = kTailSlot ? min(q0w + ql, kv_hi - 1) - ka : ql;
 #pragma unroll
         for (int j = 0; j < 16; ++j)
-          if (16 * (j >> 3) + 8 * g + (j & 7) > ql) s_cur[j] = inf;
+          if (16 * (j >> 3) + 8 * g + (j & 7) > lim) s_cur[j] = inf;
+      }
+    } else if constexpr (kTailSlot) {
+      if (ka + T::KT > kv_hi) {
+        const int lim = kv_hi - 1 - ka;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (16 * (j >> 3) + 8 * g + (j & 7) > lim) s_cur[j] = inf;
       }
     }
 

@@ -44,10 +44,16 @@ def _defaults() -> tuple[str, ...]:
                       f"fa::fwd_pipe_kernel<128, {c}, 8, 1, {e}, 1>", f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
                       f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
-                      f"fa::dq_pipe_kernel<32, {c}, 4, {e}>", f"fa::dq_pipe_kernel<64, {c}, 4, {e}>",
-                      f"fa::bwd_pair_kernel<32, {c}, 4, {e}>", f"fa::bwd_pair_kernel<64, {c}, 4, {e}>",
-                      f"fa::dq_pipe_kernel<128, false, 4, {e}>" if c == "false"
-                      else f"fa::dq_kernel<128, true, 4, 32, {e}>"]
+                      f"fa::dq_kernel<128, true, 4, 32, {e}>" if c == "true"
+                      else f"fa::dq_pipe_kernel<128, false, 4, {e}, false>"]
+            # dQ with and without the key-tail test (dq_tail_free)
+            for t in ("false", "true"):
+                names += [f"fa::dq_pipe_kernel<32, {c}, 4, {e}, {t}>",
+                          f"fa::dq_pipe_kernel<64, {c}, 4, {e}, {t}>",
+                          f"fa::bwd_pair_kernel<32, {c}, 4, {e}, {t}>",
+                          f"fa::bwd_pair_kernel<64, {c}, 4, {e}, {t}>"]
+            if c == "false":
+                names.append(f"fa::dq_pipe_kernel<128, false, 4, {e}, true>")
         names.append(f"fa::fwd_pipe_kernel<32, true, 8, 1, {e}, 2>")
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
