@@ -29,7 +29,16 @@ import torch
 from . import _lib
 
 
+# torch's current raw stream handle of a device, without building a Python
+# Stream object (about 9 us per call on the public path); the public call where
+# this torch build lacks it.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    if _raw_stream is not None:
+        index = t.device.index
+        return ctypes.c_void_p(_raw_stream(torch.cuda.current_device() if index is None else index))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
