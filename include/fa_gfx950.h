@@ -346,7 +346,9 @@ int fa_abi_version(void);
  * process (variant < 0 restores the default). Used by tuning sweeps. One
  * shape rule refines the table: dQ at D = 128 without the mask runs the
  * classic 4 x 32 tiling (variant 1) for fewer than 128 queries, unless a
- * tiling was set. */
+ * tiling was set. fa_set_tiling is safe to call while other threads launch:
+ * each (kernel, D, causal) entry is an atomic that a launch reads once, so
+ * the launch runs either the previous or the new tiling. */
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);
 int fa_num_tiling_variants(int kernel, int64_t D, int causal);
 int fa_describe_tiling_variant(int kernel, int64_t D, int causal, int variant, int* out4);

@@ -164,6 +164,54 @@ def test_custom_scale_matches_oracle():
         check_against_oracle(got, q, k, v, do, True, scale=scale, tag=f"scale={scale}")
 
 
+# (B, Hq, Hkv, N, D): one MHA shape at a kernel head size, one padded head size
+# (40 runs at 64), one GQA group of 4 with a ragged length.
+NON_POSITIVE_SCALE_CASES = [(1, 2, 2, 150, 64), (1, 2, 2, 129, 40), (2, 8, 2, 97, 32)]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [-0.3, 0.0, 1e-40])
+@pytest.mark.parametrize("case", NON_POSITIVE_SCALE_CASES,
+                         ids=lambda c: "B{}Hq{}Hkv{}N{}D{}".format(*c))
+def test_non_positive_scales_run_forward_and_backward_on_the_kernels(case, scale, causal):
+    """Scales that are negative, zero or subnormal in float32 run on the gfx950
+    kernels through the query transforms of attention._kernel_scale ("negate":
+    -q at |scale|, dQ negated back; "zero": a zero q at scale 1, dQ = 0), with
+    head padding and GQA on top. O, dQ, dK, dV and the base-2 LSE are checked
+    against the fp64 oracle evaluated at the scale as given."""
+    from triton_flash_attention import attention as api
+
+    B, Hq, Hkv, N, D = case
+    tag = f"scale={scale} B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal}"
+    _note(tag)
+    assert api._kernel_scale(scale)[1] == ("negate" if scale < 0 else "zero")
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + D + int(causal), mult=0.8)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    assert explain_dispatch(qd, kd, vd, enable_gqa=Hq != Hkv).backend == "triton"
+    out = scaled_dot_product_attention(qd, kd, vd, is_causal=causal, scale=scale,
+                                       enable_gqa=Hq != Hkv, backend="triton")
+    dq, dk, dv = torch.autograd.grad(out, (qd, kd, vd), do.to(DEV))
+    with torch.no_grad():
+        lse = api._padded_forward(qd.detach(), kd.detach(), vd.detach(), causal, scale)[4]
+    torch.cuda.synchronize()
+    ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
+                           o16=out.detach().cpu().numpy(), fold_bwd=True)
+    report = {}
+    for name, t in (("o", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+        a = t.detach().double().cpu().numpy()
+        if name == "dq" and scale >= 0:
+            # The exact dQ is scale * dS K: |dQ| <= 1e-40 * |dS K| (0 at scale 0), which
+            # fp16 holds as 0, and the kernels return exact zeros.
+            assert not t.any(), f"{tag}: dQ of a zero or subnormal scale is exactly zero"
+            assert np.max(np.abs(ref["dq"])) < 1e-30
+            continue
+        report[name] = assert_close(f"{tag} {name}", a, ref[name])
+    lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - ref["lse"])))
+    assert lse_err <= LSE_TOL, f"{tag} lse: max-abs {lse_err:.3e} (tol {LSE_TOL:.0e})"
+    _note(f"{tag}: " + ", ".join(f"{k}={v[0]:.2e}/{v[1]:.2e}" for k, v in report.items())
+          + f", lse={lse_err:.2e}")
+
+
 # ---------------------------------------------------------------------------
 # Closed-form special cases (values fixed by the mathematics).
 # ---------------------------------------------------------------------------

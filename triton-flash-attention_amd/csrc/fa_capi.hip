@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <initializer_list>
 #include <memory>
 #include <mutex>
@@ -53,9 +54,16 @@ int launch_result(hipError_t e, const char* name) {
 }
 
 // Process-wide tiling choice per (kernel, D index, causal); -1 = table default.
-int g_override[fa::kNumKinds][3][2] = {{{-1, -1}, {-1, -1}, {-1, -1}},
-                                       {{-1, -1}, {-1, -1}, {-1, -1}},
-                                       {{-1, -1}, {-1, -1}, {-1, -1}}};
+// fa_set_tiling may run on one thread while others launch: every entry is an
+// atomic, read once per tiling decision (relaxed: each entry is independent and
+// every value stored is a valid choice), so a launch sees either the old or the
+// new tiling, never a torn value. The array is zero-initialised and holds
+// variant + 1, so 0 means "table default".
+std::atomic<int> g_override_plus1[fa::kNumKinds][3][2];
+
+int override_of(int kind, int di, int causal) {
+  return g_override_plus1[kind][di][causal ? 1 : 0].load(std::memory_order_relaxed) - 1;
+}
 
 // Static tiling table (replaces the Triton autotuner). Values are variant
 // indices into the registries of fa_fwd.hip / fa_bwd.hip, chosen from
@@ -109,15 +117,21 @@ bool usable(const fa::Variant& v, int di, int causal, int dt = fa::kF16) {
 // The tiling used for (kind, D, causal, element type): the override if set,
 // else the default; a bf16 call whose overridden tiling has no bf16 build
 // uses the default tiling.
-const fa::Variant* select(int kind, int di, int causal, int* index, int dt = fa::kF16) {
+// `ov` is the override as read once by the caller (override_of).
+const fa::Variant* select(int kind, int di, int causal, int ov, int* index, int dt = fa::kF16) {
   int count = 0;
   const fa::Variant* vs = registry(kind, &count);
   if (!vs) return nullptr;
-  int v = g_override[kind][di][causal ? 1 : 0];
+  int v = ov;
   if (v < 0 || (v < count && !usable(vs[v], di, causal, dt))) v = kDefault[kind][di][causal ? 1 : 0];
   if (v >= count || !usable(vs[v], di, causal, dt)) return nullptr;
   if (index) *index = v;
   return &vs[v];
+}
+
+// select() with the override as it stands now.
+const fa::Variant* select_current(int kind, int di, int causal, int* index, int dt = fa::kF16) {
+  return select(kind, di, causal, override_of(kind, di, causal), index, dt);
 }
 
 // dQ tiling for a launch of N queries. Without the mask at D = 128 the table's
@@ -129,10 +143,9 @@ const fa::Variant* select(int kind, int di, int causal, int* index, int dt = fa:
 constexpr int kDqShortQueryVariant = 1;
 
 const fa::Variant* select_dq(int di, int causal, int64_t N, int dt) {
-  const fa::Variant* var = select(fa::kDq, di, causal, nullptr, dt);
-  if (!var || di != fa::head_dim_index(128) || causal || N >= 128 ||
-      g_override[fa::kDq][di][0] >= 0)
-    return var;
+  const int ov = override_of(fa::kDq, di, causal);
+  const fa::Variant* var = select(fa::kDq, di, causal, ov, nullptr, dt);
+  if (!var || di != fa::head_dim_index(128) || causal || N >= 128 || ov >= 0) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kDq, &count);
   if (kDqShortQueryVariant < count && usable(vs[kDqShortQueryVariant], di, causal, dt))
@@ -161,8 +174,9 @@ constexpr int kFwdKeyGroupVariant = 8;
 
 const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt) {
   int index = -1;
-  const fa::Variant* var = select(fa::kFwd, di, causal, &index, dt);
-  if (!var || g_override[fa::kFwd][di][causal ? 1 : 0] >= 0) return var;
+  const int ov = override_of(fa::kFwd, di, causal);
+  const fa::Variant* var = select(fa::kFwd, di, causal, ov, &index, dt);
+  if (!var || ov >= 0) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kFwd, &count);
   auto pick = [&](int v) {
@@ -701,7 +715,7 @@ static int dkdv_impl(int dt, const char* name, const fa_half_t* q, const fa_half
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+  const fa::Variant* var = select_current(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
@@ -719,7 +733,7 @@ static int64_t dkdv_workspace_impl(const char* name, int64_t B, int64_t Hq, int6
   // bf16 calls on the default tiling, whose split can be larger).
   int64_t bytes = 0;
   for (int dt : {fa::kF16, fa::kBF16}) {
-    const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+    const fa::Variant* var = select_current(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
     bytes = std::max(bytes, split_workspace_bytes(dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal),
                                                   B, Hkv, Nkv, D));
@@ -744,7 +758,7 @@ static int dkdv_ws_impl(int dt, const char* name, const fa_half_t* q, const fa_h
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+  const fa::Variant* var = select_current(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
@@ -902,7 +916,7 @@ bool plan_bwd(int dt, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv
               int causal, BwdPlan* p) {
   const int di = fa::head_dim_index(D);
   p->dq = select_dq(di, causal, N, dt);
-  p->dkdv = select(fa::kDkdv, di, causal, nullptr, dt);
+  p->dkdv = select_current(fa::kDkdv, di, causal, nullptr, dt);
   if (!p->dq || !p->dkdv) return false;
   p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv);
   p->dkdv_nsplit = dkdv_split(*p->dkdv, B, Hq, Hkv, N, Nkv, causal);
@@ -1184,7 +1198,7 @@ int fa_get_tiling(int kernel, int64_t D, int causal, int* out4) {
   if (kernel < 0 || kernel >= fa::kNumKinds)
     return fail(FA_ERR_BAD_TILING, "unknown kernel %d", kernel);
   int index = -1;
-  const fa::Variant* var = select(kernel, di, causal, &index);
+  const fa::Variant* var = select_current(kernel, di, causal, &index);
   if (!var) return fail(FA_ERR_BAD_TILING, "no tiling for kernel %d", kernel);
   out4[0] = var->waves;
   out4[1] = var->rows;
@@ -1230,7 +1244,8 @@ int fa_set_tiling(int kernel, int64_t D, int causal, int variant) {
   if (variant >= 0 && !usable(registry(kernel, &count)[variant], di, causal))
     return fail(FA_ERR_BAD_TILING, "variant %d is not compiled for head_dim %lld", variant,
                 (long long)D);
-  g_override[kernel][di][causal ? 1 : 0] = variant < 0 ? -1 : variant;
+  g_override_plus1[kernel][di][causal ? 1 : 0].store(variant < 0 ? 0 : variant + 1,
+                                                      std::memory_order_relaxed);
   return FA_OK;
 }
 
