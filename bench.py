@@ -56,12 +56,16 @@ REFERENCE_PUBLISHED_TFLOPS = 13.283
 
 WORKLOADS = {
     # name: (B, Hq, Hkv, N, D, causal, input scale, seed)
+    "c1": (1, 4, 4, 257, 64, False, 1.0, 1001),
     "c2": (4, 16, 16, 4096, 64, True, 1.0, 1002),
     "c3": (2, 16, 4, 2049, 64, True, 1.0, 1003),
     "c4-bidir": (2, 32, 32, 8192, 128, False, 0.5, 1004),
     "c4-causal": (2, 32, 32, 8192, 128, True, 0.5, 1004),
     "c5": (1, 8, 2, 16381, 32, True, 1.0, 1005),
 }
+# c1 is the reference's forward-only case (an output O; its CPU fallback in the
+# reference): a step there is one forward, with inputs that need no gradient.
+FORWARD_ONLY = {"c1"}
 
 
 def make_inputs(B, Hq, Hkv, N, D, seed, mult):
@@ -134,7 +138,7 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(inputs, causal: bool, budget_s: float):
+def cpu_baseline(inputs, causal: bool, budget_s: float, forward_only: bool = False):
     """The reference's CPU path on the same workload: the public API with CPU
     tensors falls back to torch SDPA. Median of repetitions after one warmup,
     repeated until ``budget_s`` of CPU work has been spent. Threads: every CPU
@@ -148,11 +152,15 @@ def cpu_baseline(inputs, causal: bool, budget_s: float):
     torch.set_num_threads(threads)
     q, k, v, do = (t.clone() for t in inputs)
     gqa = q.shape[1] != k.shape[1]
-    q.requires_grad_()
-    k.requires_grad_()
-    v.requires_grad_()
+    if not forward_only:
+        q.requires_grad_()
+        k.requires_grad_()
+        v.requires_grad_()
 
     def step():
+        if forward_only:
+            scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa)
+            return
         q.grad = k.grad = v.grad = None
         scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa).backward(do)
 
@@ -160,7 +168,9 @@ def cpu_baseline(inputs, causal: bool, budget_s: float):
     step()  # warmup
     times = []
     spent = time.perf_counter() - t0
-    while spent < budget_s and len(times) < 7:
+    # At least one timed repetition, also when the warmup alone spent the budget
+    # (c4: one fwd+bwd on the host takes longer than the default 15 s).
+    while (spent < budget_s or not times) and len(times) < 7:
         t1 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t1)
@@ -206,7 +216,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=150)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2",
-                    help="c2 is the metric's configuration; the others are for exploration")
+                    help="c2 is the metric's configuration; the others are for exploration "
+                         "(c1 times one forward per step)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU-work budget of the CPU baseline (0 disables it)")
     ap.add_argument("--no-parity", action="store_true",
@@ -240,17 +251,24 @@ def main(argv=None) -> int:
     from triton_flash_attention import _ops, explain_dispatch, scaled_dot_product_attention
 
     B, Hq, Hkv, N, D, causal, mult, seed = WORKLOADS[args.workload]
+    forward_only = args.workload in FORWARD_ONLY
+    mode = "forward" if forward_only else "forward-backward"
     cpu_inputs = make_inputs(B, Hq, Hkv, N, D, seed, mult)
     q, k, v, do = (t.to("cuda") for t in cpu_inputs)
     decision = explain_dispatch(q, k, v, enable_gqa=Hq != Hkv)
     if decision.backend != "triton":
         print(f"custom kernel not selected: {decision.reason}", file=sys.stderr)
         return 1
-    q.requires_grad_()
-    k.requires_grad_()
-    v.requires_grad_()
+    if not forward_only:
+        q.requires_grad_()
+        k.requires_grad_()
+        v.requires_grad_()
 
     def step():
+        if forward_only:
+            scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=Hq != Hkv,
+                                         backend="triton")
+            return
         q.grad = k.grad = v.grad = None
         out = scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=Hq != Hkv,
                                            backend="triton")
@@ -259,7 +277,7 @@ def main(argv=None) -> int:
     print(f"[bench] {args.workload}: B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal}; "
           f"warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
     flops = attention_flops(batch=B, query_heads=Hq, sequence=N, head_dim=D, causal=causal,
-                            mode="forward-backward")
+                            mode=mode)
     # Validation and the reference-protocol timing come first (see the module
     # docstring); the headline region below is W warmup + K timed steps.
     parity = None
@@ -316,6 +334,8 @@ def main(argv=None) -> int:
     with _ops.LaunchTimer() as timer:
         for _ in range(args.steps):
             o_k, lse_k = _ops.flash_fwd(qd, kd, vd, causal, kscale)
+            if forward_only:
+                continue
             delta_k, _ = _ops.flash_bwd_dq_delta(qd, kd, vd, o_k, do, lse_k, causal, kscale)
             _ops.flash_bwd_dkdv(qd, kd, vd, do, lse_k, delta_k, causal, kscale)
     torch.cuda.synchronize()
@@ -336,7 +356,8 @@ def main(argv=None) -> int:
             f = kernel_flops(name, B, Hq, N, D, causal)
             entry["tflops"] = round(f / (mean * 1e-3) / 1e12, 2)
         kernels[name] = entry
-    dominant = max(("fwd", "dkdv", "dq"), key=lambda n: kernels[n]["mean_ms"])
+    dominant = max((n for n in ("fwd", "dkdv", "dq") if n in kernels),
+                   key=lambda n: kernels[n]["mean_ms"])
     dom_flops = kernel_flops(dominant, B, Hq, N, D, causal)
     achieved = dom_flops / (kernels[dominant]["mean_ms"] * 1e-3) / 1e12
 
@@ -356,7 +377,8 @@ def main(argv=None) -> int:
         "data": "synthetic (seeded N(0,1) fp32 -> fp16, resident in HBM)",
         "config": {
             "workload": f"{args.workload}: {'causal' if causal else 'bidirectional'} "
-                        f"fwd+bwd B={B} Hq={Hq} Hkv={Hkv} N={N} D={D}",
+                        f"{'fwd' if forward_only else 'fwd+bwd'} B={B} Hq={Hq} Hkv={Hkv} "
+                        f"N={N} D={D}",
             "batch": B, "q_heads": Hq, "kv_heads": Hkv, "seq_len": N, "head_dim": D,
             "causal": causal, "seed": seed, "input_scale": mult,
             "parallelism": "single GPU",
@@ -401,7 +423,8 @@ def main(argv=None) -> int:
         del src, dst
 
     if args.cpu_seconds > 0:
-        median_s, threads, affinity, reps = cpu_baseline(cpu_inputs, causal, args.cpu_seconds)
+        median_s, threads, affinity, reps = cpu_baseline(cpu_inputs, causal, args.cpu_seconds,
+                                                         forward_only)
         record["cpu_baseline"] = {
             "value": round(flops / median_s / 1e12, 4),
             "unit": "TFLOP/s",
@@ -410,7 +433,8 @@ def main(argv=None) -> int:
             "thread_cap": CPU_SHARE_PER_GPU,
             "cpu_model": cpu_model(),
             "kind": "reference",
-            "sample": (f"full {args.workload} workload (fwd+bwd, {flops / 1e9:.1f} GFLOP) through "
+            "sample": (f"full {args.workload} workload ({'fwd' if forward_only else 'fwd+bwd'}, "
+                       f"{flops / 1e9:.1f} GFLOP) through "
                        "the public API on CPU fp16 tensors, which is the reference's CPU path "
                        f"(torch SDPA); median of {reps} reps after 1 warmup, "
                        f"{median_s:.3f} s/rep, {threads} threads "

@@ -117,6 +117,47 @@ constexpr bool dkdv_pipe_tiling_ok() {
 #ifndef FA_DKDV_LEAD
 #define FA_DKDV_LEAD 3
 #endif
+// Task order of the pipelined dK/dV body (kinds 0 dV, 1 dK of unit u-1; 2 S,
+// 3 dPd of unit u+1; NQ tasks of each kind):
+//   0: (dV_q, dK_q, S_q, dPd_q) for q = 0 .. NQ-1;
+//   1: dV_0, dK_0, dV_1, dK_1, then (S_j, dPd_j, dV_j+2, dK_j+2) for
+//      j = 0 .. NQ-3, then S, dPd of NQ-2 and NQ-1: the first S and dPd tasks,
+//      whose accumulators start from the LSE' and Delta table reads issued at
+//      the top of the body, run four tasks in instead of two.
+// Order 1 measured no faster (MI355X, one box: dK/dV c2 292.4 vs 292.0 us, c3
+// 70.0 vs 70.8, B2 H32 N8192 D128 causal 2261 vs 2232), so 0 stays.
+#ifndef FA_DKDV_ORDER
+#define FA_DKDV_ORDER 0
+#endif
+// Cross-unit operand prefetch in the pipelined backward bodies (dK/dV and dQ):
+// a two-unit step publishes the rows of both of its units at its barrier, so
+// the second unit's first FA_*_LEAD operand reads are issued during the first
+// unit's last task groups instead of at the top of its own body, where the
+// first MFMA would wait out their whole LDS latency. Same results bit for bit;
+// MI355X, one box, min of two, us, off / on: dK/dV c2 292.0 / 288.2, c3 70.8 /
+// 68.5, c5 359.5 / 357.9, B2 H32 N8192 D128 causal 2232 / 2228; dQ c5 236.0 /
+// 233.8, c2, c3 and D = 128 even.
+#ifndef FA_BWD_XPREFETCH
+#define FA_BWD_XPREFETCH 1
+#endif
+
+// (kind, q) of task slot i of the pipelined dK/dV body (see FA_DKDV_ORDER).
+template <int NQ>
+constexpr int dkdv_task_kind(int i) {
+  if (FA_DKDV_ORDER == 0) return i % 4;
+  const int p = i / 2, w = i % 2;
+  if (p < 2) return w;
+  if (p < 2 + 2 * (NQ - 2)) return ((p - 2) % 2 == 0) ? 2 + w : w;
+  return 2 + w;
+}
+template <int NQ>
+constexpr int dkdv_task_q(int i) {
+  if (FA_DKDV_ORDER == 0) return i / 4;
+  const int p = i / 2;
+  if (p < 2) return p;
+  if (p < 2 + 2 * (NQ - 2)) return ((p - 2) % 2 == 0) ? (p - 2) / 2 : (p - 3) / 2 + 2;
+  return NQ - 2 + (p - 2 - 2 * (NQ - 2));
+}
 
 template <int D, bool CAUSAL, int NW, class E>
 __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned block,
@@ -377,8 +418,13 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
   };
 
   // Body of one unit in ring slot SLOT (see the header comment).
+  // Operands of the second unit of a step, read during the first (FA_BWD_XPREFETCH).
+  half8 xpre[FA_DKDV_LEAD];
   auto body = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;
+    // Steps run units in slots (2p, 2p+1): the even one prefetches for the odd one.
+    constexpr bool kMakesPre = FA_BWD_XPREFETCH && SLOT % 2 == 0;
+    constexpr bool kTakesPre = FA_BWD_XPREFETCH && SLOT % 2 == 1;
     const half_t* cur = lds + SLOT * T::STAGE;
     const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
     const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
@@ -405,23 +451,24 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
     constexpr int NQ = D / 16;  // tasks of each kind
     constexpr int NTASK = 4 * NQ;
     constexpr int kLead = FA_DKDV_LEAD;
-    const half_t* q_nxt = nxt;
-    const half_t* do_nxt = nxt + T::TILE;
-    const half_t* q_prv = prv;
-    const half_t* do_prv = prv + T::TILE;
-    auto load_op = [&](auto t_c) -> half8 {
+    // Operand of task t of the body whose previous unit's rows are at p and
+    // next unit's rows at n.
+    auto load_op_at = [&](auto t_c, const half_t* p, const half_t* n) -> half8 {
       constexpr int t = decltype(t_c)::value;
-      constexpr int kind = t % 4, q = t / 4;
+      constexpr int kind = dkdv_task_kind<NQ>(t), q = dkdv_task_q<NQ>(t);
       constexpr int h = q / (D / 32), db = q % (D / 32);
-      if constexpr (kind == 0) return tr8(do_prv + 16 * h * D, db);
-      else if constexpr (kind == 1) return tr8(q_prv + 16 * h * D, db);
-      else if constexpr (kind == 2) return *reinterpret_cast<const half8*>(q_nxt + r_off[q]);
-      else return *reinterpret_cast<const half8*>(do_nxt + r_off[q]);
+      if constexpr (kind == 0) return tr8(p + T::TILE + 16 * h * D, db);
+      else if constexpr (kind == 1) return tr8(p + 16 * h * D, db);
+      else if constexpr (kind == 2) return *reinterpret_cast<const half8*>(n + r_off[q]);
+      else return *reinterpret_cast<const half8*>(n + T::TILE + r_off[q]);
     };
+    auto load_op = [&](auto t_c) -> half8 { return load_op_at(t_c, prv, nxt); };
+    // The next body (slot SLOT + 1) reads its previous unit from this slot.
+    const half_t* nxt2 = lds + ((SLOT + 2) % NS) * T::STAGE;
     float16v s_nx, dp_nx;
     auto run_task = [&](auto t_c, const half8& op) {
       constexpr int t = decltype(t_c)::value;
-      constexpr int kind = t % 4, q = t / 4;
+      constexpr int kind = dkdv_task_kind<NQ>(t), q = dkdv_task_q<NQ>(t);
       constexpr int h = q / (D / 32), db = q % (D / 32);
       if constexpr (kind == 0) acc_mfma(dv[db], op, pa_prev[h]);
       else if constexpr (kind == 1) acc_mfma(dk[db], op, sa_prev[h]);
@@ -480,13 +527,20 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
     // fence instead of being split into the branches above.
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" : "+v"(ltab));
-    static_for<0, kLead>([&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+    static_for<0, kLead>([&](auto t_c) {
+      if constexpr (kTakesPre) op[decltype(t_c)::value] = xpre[decltype(t_c)::value];
+      else op[decltype(t_c)::value] = load_op(t_c);
+    });
     s_nx = table16(fl + ltab);
     dp_nx = table16(reinterpret_cast<const float*>(nxt + 2 * T::TILE) + 64 + 8 * g);
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NTASK>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
-      if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(std::integral_constant<int, i + kLead>{});
+      if constexpr (i + kLead < NTASK)
+        op[i + kLead] = load_op(std::integral_constant<int, i + kLead>{});
+      else if constexpr (kMakesPre)
+        xpre[i + kLead - NTASK] =
+            load_op_at(std::integral_constant<int, i + kLead - NTASK>{}, cur, nxt2);
       run_task(i_c, op[i]);
       // vector work of unit u: stage A of pair pr in group (2pr NTASK)/16,
       // stage B one group later (B of the last pair shares the last group)
@@ -851,10 +905,18 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
 
   int c_key = kv_lo;  // first key of the unit the body works on
 
+  // Operands of the second unit of a step, read during the first (FA_BWD_XPREFETCH).
+  half8 xpre[FA_DQ_LEAD];
+  static_assert(T::AHEAD >= 3 && T::AHEAD + 1 <= NS - 1,
+                "a step's DMA must not target the slots its two bodies read");
   auto body = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;
+    constexpr bool kMakesPre = FA_BWD_XPREFETCH && SLOT % 2 == 0;
+    constexpr bool kTakesPre = FA_BWD_XPREFETCH && SLOT % 2 == 1;
+    const half_t* cur = lds + SLOT * T::STAGE;
     const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
     const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
+    const half_t* nxt2 = lds + ((SLOT + 2) % NS) * T::STAGE;
     const int ka = c_key;
     c_key += T::KT;
 
@@ -894,16 +956,17 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
     constexpr int NQ = D / 16;
     constexpr int NTASK = 3 * NQ;
     constexpr int kLead = FA_DQ_LEAD;
-    const half_t* k_nxt = nxt;
-    const half_t* v_nxt = nxt + T::TILE;
-    auto load_op = [&](auto t_c) -> half8 {
+    // Operand of task t of the body whose previous unit's rows are at p and
+    // next unit's rows at n.
+    auto load_op_at = [&](auto t_c, const half_t* p, const half_t* n) -> half8 {
       constexpr int t = decltype(t_c)::value;
       constexpr int kind = t % 3, q = t / 3;
       constexpr int h = q / (D / 32), db = q % (D / 32);
-      if constexpr (kind == 0) return tr8(prv + 16 * h * D, db);
-      else if constexpr (kind == 1) return *reinterpret_cast<const half8*>(k_nxt + r_off[q]);
-      else return *reinterpret_cast<const half8*>(v_nxt + r_off[q]);
+      if constexpr (kind == 0) return tr8(p + 16 * h * D, db);
+      else if constexpr (kind == 1) return *reinterpret_cast<const half8*>(n + r_off[q]);
+      else return *reinterpret_cast<const half8*>(n + T::TILE + r_off[q]);
     };
+    auto load_op = [&](auto t_c) -> half8 { return load_op_at(t_c, prv, nxt); };
     float16v s_nx = lse16, dp_nx = delta16;
     auto run_task = [&](auto t_c, const half8& op) {
       constexpr int t = decltype(t_c)::value;
@@ -937,11 +1000,18 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
 
     half8 op[NTASK];
     __builtin_amdgcn_sched_barrier(0);
-    static_for<0, kLead>([&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+    static_for<0, kLead>([&](auto t_c) {
+      if constexpr (kTakesPre) op[decltype(t_c)::value] = xpre[decltype(t_c)::value];
+      else op[decltype(t_c)::value] = load_op(t_c);
+    });
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NTASK>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
-      if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(std::integral_constant<int, i + kLead>{});
+      if constexpr (i + kLead < NTASK)
+        op[i + kLead] = load_op(std::integral_constant<int, i + kLead>{});
+      else if constexpr (kMakesPre)
+        xpre[i + kLead - NTASK] =
+            load_op_at(std::integral_constant<int, i + kLead - NTASK>{}, cur, nxt2);
       run_task(i_c, op[i]);
 #pragma unroll
       for (int pr = 0; pr < 8; ++pr) {
