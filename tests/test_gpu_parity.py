@@ -199,11 +199,12 @@ def test_non_positive_scales_run_forward_and_backward_on_the_kernels(case, scale
     report = {}
     for name, t in (("o", out), ("dq", dq), ("dk", dk), ("dv", dv)):
         a = t.detach().double().cpu().numpy()
-        if name == "dq" and scale >= 0:
-            # The exact dQ is scale * dS K: |dQ| <= 1e-40 * |dS K| (0 at scale 0), which
-            # fp16 holds as 0, and the kernels return exact zeros.
-            assert not t.any(), f"{tag}: dQ of a zero or subnormal scale is exactly zero"
-            assert np.max(np.abs(ref["dq"])) < 1e-30
+        if name in ("dq", "dk") and scale >= 0:
+            # The exact dQ = scale dS K and dK = scale dS^T Q are below 1e-40 * |dS| |K|
+            # (0 at scale 0), which fp16 holds as 0; the kernels return exact zeros
+            # (dQ set to zero, dK from the zero query).
+            assert not t.any(), f"{tag}: {name} of a zero or subnormal scale is exactly zero"
+            assert np.max(np.abs(ref[name])) < 1e-30
             continue
         report[name] = assert_close(f"{tag} {name}", a, ref[name])
     lse_err = float(np.max(np.abs(lse.double().cpu().numpy() - ref["lse"])))
