@@ -308,7 +308,9 @@ int fa_bwd_bf16(const fa_half_t* q, const fa_half_t* k, const fa_half_t* v,
 
 /* Forward that allocates nothing: fa_fwd_ws's computation with the split-KV
  * partials kept in a device array inside the library (64 MiB per GPU, held
- * until the process ends) instead of a caller workspace. No counterpart in
+ * until the process ends; under HIP's default deferred code-object loading
+ * it is reserved at the first fa_fwd_noalloc call on a GPU, since its code
+ * object holds no kernel) instead of a caller workspace. No counterpart in
  * the reference; it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight decoding loops, harnesses that forbid
  * hipMalloc). Same arguments, checks and results as fa_fwd_ws with a large

@@ -22,7 +22,9 @@
 // Device-resident scratch of fa_fwd_noalloc: the split-KV forward's fp32
 // partials ([nsplit, B, Hq, N_q, D + 1]) for callers that cannot allocate.
 // Every GPU the library runs on holds its own copy for the life of the
-// process. In host code `scratch` only names the symbol; its device address
+// process. This translation unit has no kernels, so with HIP's default
+// deferred code-object loading the array is reserved on a GPU only when
+// hipGetSymbolAddress first asks for it (the first fa_fwd_noalloc there). In host code `scratch` only names the symbol; its device address
 // comes from hipGetSymbolAddress (scratch_address below), once per device.
 constexpr int64_t kNoallocScratchBytes = (int64_t)64 << 20;
 static __device__ __align__(256) float scratch[kNoallocScratchBytes / 4];
