@@ -13,6 +13,7 @@ HIP call.
 from __future__ import annotations
 
 import ctypes
+import json
 import sys
 
 import numpy as np
@@ -85,3 +86,65 @@ def test_noalloc_forward_matches_workspace_forward_twice():
         lse_err = float(np.max(np.abs(lse_na.double().cpu().numpy() - lse_ref)))
         assert lse_err <= LSE_TOL, f"{tag} lse {lse_err:.3e}"
         _note(f"{tag}: equal to fa_fwd_ws, lse err {lse_err:.2e}, partials {need} bytes")
+
+
+# Run in a fresh process: free device memory around loading the library, a
+# plain forward and the first fa_fwd_noalloc (inputs allocated beforehand, so
+# the caching allocator takes nothing in between).
+_RESIDENCY_SCRIPT = r'''
+import json, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+dev = torch.device("cuda")
+small = [torch.randn(1, 2, 64, 64, device=dev).half() for _ in range(3)]
+o_s, lse_s = torch.empty_like(small[0]), torch.empty(1, 2, 64, device=dev)
+B, Hq, Hkv, N, Nkv, D = 2, 8, 2, 3, 6000, 128
+q = torch.randn(B, Hq, N, D, device=dev).half()
+k = torch.randn(B, Hkv, Nkv, D, device=dev).half()
+v = torch.randn(B, Hkv, Nkv, D, device=dev).half()
+o, lse = torch.empty_like(q), torch.empty(B, Hq, N, device=dev)
+torch.cuda.synchronize()
+free = lambda: torch.cuda.mem_get_info()[0]
+r = [free()]
+from triton_flash_attention import _lib
+lib = _lib.load()
+torch.cuda.synchronize()
+r.append(free())
+s = torch.cuda.current_stream().cuda_stream
+_lib.check(lib.fa_fwd(*(t.data_ptr() for t in small), o_s.data_ptr(), lse_s.data_ptr(),
+                      1, 2, 2, 64, 64, 0.125, 1, s))
+torch.cuda.synchronize()
+r.append(free())
+_lib.check(lib.fa_fwd_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                              lse.data_ptr(), B, Hq, Hkv, N, Nkv, D, D ** -0.5, 0, s))
+torch.cuda.synchronize()
+r.append(free())
+print("RESULT " + json.dumps(r), flush=True)
+'''
+
+
+@pytest.mark.gpu
+def test_noalloc_scratch_is_reserved_at_the_first_noalloc_call():
+    """The 64 MiB array sits in a code object with no kernel, so under HIP's
+    default deferred code-object loading a process that only loads the
+    library and runs plain launches does not hold it; the first
+    fa_fwd_noalloc on the GPU does. Measured with hipMemGetInfo in a fresh
+    process (the environment's HIP_ENABLE_DEFERRED_LOADING is left as is)."""
+    import os
+    import subprocess
+    from pathlib import Path
+
+    pkg = Path(__file__).resolve().parent.parent / "triton-flash-attention_amd"
+    env = {k: v for k, v in os.environ.items() if k != "HIP_ENABLE_DEFERRED_LOADING"}
+    p = subprocess.run([sys.executable, "-c", _RESIDENCY_SCRIPT, str(pkg)], capture_output=True,
+                       text=True, timeout=240, env=env)
+    line = [ln for ln in p.stdout.splitlines() if ln.startswith("RESULT ")]
+    assert p.returncode == 0 and line, p.stdout[-2000:] + p.stderr[-2000:]
+    start, loaded, after_fwd, after_noalloc = json.loads(line[0][7:])
+    MiB = 1 << 20
+    _note(f"free-memory drops: dlopen {(start - loaded) / MiB:.0f} MiB, first fa_fwd "
+          f"{(loaded - after_fwd) / MiB:.0f} MiB, first fa_fwd_noalloc "
+          f"{(after_fwd - after_noalloc) / MiB:.0f} MiB")
+    limit = _lib.load().fa_fwd_noalloc_max_workspace_bytes()
+    assert start - after_fwd < limit // 2, "loading and a plain forward reserved the scratch"
+    assert after_fwd - after_noalloc >= limit, "the first fa_fwd_noalloc did not reserve it"
