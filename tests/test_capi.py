@@ -411,3 +411,31 @@ def test_split_dq_workspace_sizing_and_rejection(lib):
     rc = lib.fa_bwd_dq_delta_ws_bf16(P, P, P, P, P, P, P, P, 1, 32, 8, 128, 32768, 128, 0.09, 0,
                                      P + 4, ws, None)
     assert rc == _lib.FA_ERR_MISALIGNED
+
+
+def test_native_binding_loads_and_takes_the_library_entry_points(lib):
+    """The C++ autograd binding is built next to the library and initialised
+    with the library's own entry points (no GPU needed); the public API hands
+    it the plain training calls only."""
+    import torch
+
+    from triton_flash_attention import _native
+    from triton_flash_attention import attention as api
+
+    ok, why = _native.status()
+    assert ok, why
+    assert _native._module.ready()
+    for name in _native.ENTRY_POINTS:
+        assert name in declared_functions(), name
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    assert api._native_serves(q, q, 0.125)
+    assert not api._native_serves(q, q, -0.125)          # negated query: Python Function
+    assert not api._native_serves(q, q, 0.0)             # zero query: Python Function
+    assert not api._native_serves(q, q[..., :32], 0.125)  # D_v != D: padded
+    q40 = torch.zeros(1, 2, 8, 40, dtype=torch.float16)
+    assert not api._native_serves(q40, q40, 0.125)        # padded head size
+    # Arguments the binding cannot serve are rejected before any HIP call.
+    with pytest.raises(RuntimeError, match="one GPU"):
+        _native._module.attention(q, q, q, True, 0.125)
+    with pytest.raises(RuntimeError, match="must be 4-D"):
+        _native._module.attention(q[0], q[0], q[0], True, 0.125)

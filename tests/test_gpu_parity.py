@@ -164,6 +164,63 @@ def test_custom_scale_matches_oracle():
         check_against_oracle(got, q, k, v, do, True, scale=scale, tag=f"scale={scale}")
 
 
+# (B, Hq, Hkv, N_q, N_kv, D, causal, dtype): the C++ binding's envelope, including
+# the library's split plans (split-KV forward and split dQ, split dK/dV with the
+# combined launch) and cross-attention.
+NATIVE_CASES = [
+    (2, 4, 4, 300, 300, 64, True, torch.float16),
+    (1, 8, 2, 777, 777, 32, False, torch.float16),
+    (1, 4, 4, 260, 260, 128, True, torch.bfloat16),
+    (2, 16, 4, 2049, 2049, 64, True, torch.float16),
+    (1, 8, 2, 3, 6000, 128, False, torch.float16),
+    (1, 4, 2, 300, 900, 64, True, torch.float16),
+    (1, 4, 1, 900, 300, 32, False, torch.bfloat16),
+]
+
+
+def _api_fwd_bwd(q, k, v, do, causal, grad_of=(0, 1, 2)):
+    ts = [t.to(DEV) for t in (q, k, v)]
+    for i in grad_of:
+        ts[i].requires_grad_()
+    out = scaled_dot_product_attention(*ts, is_causal=causal, enable_gqa=q.shape[1] != k.shape[1],
+                                       backend="triton")
+    grads = torch.autograd.grad(out, [ts[i] for i in grad_of], do.to(DEV))
+    torch.cuda.synchronize()
+    return out.detach(), grads, type(out.grad_fn).__name__
+
+
+@pytest.mark.parametrize("case", NATIVE_CASES, ids=lambda c: "B{}Hq{}Hkv{}Nq{}Nkv{}D{}".format(
+    *c[:6]) + ("causal" if c[6] else "bidir") + str(c[7])[6:])
+def test_native_binding_matches_the_python_function_bitwise(case, monkeypatch):
+    """The public API's training path through the C++ autograd binding makes the
+    Python TritonAttention Function's library calls, so O, dQ, dK and dV are
+    equal bit for bit; also with a subset of inputs requiring grad and on a
+    side stream."""
+    from triton_flash_attention import _native
+    from triton_flash_attention import attention as api
+
+    B, Hq, Hkv, N, Nkv, D, causal, dtype = case
+    _note(f"native B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={D} causal={causal} {dtype}")
+    assert _native.available(), _native.status()
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv + D, n_kv=Nkv, dtype=dtype)
+    o_n, g_n, node_n = _api_fwd_bwd(q, k, v, do, causal)
+    with monkeypatch.context() as m:
+        m.setattr(api, "_native_serves", lambda *a: False)
+        o_p, g_p, node_p = _api_fwd_bwd(q, k, v, do, causal)
+        o_p2, g_p2, _ = _api_fwd_bwd(q, k, v, do, causal, grad_of=(1, 2))
+    assert node_p == "TritonAttentionBackward" and node_n != node_p, (node_n, node_p)
+    assert torch.equal(o_n, o_p)
+    for name, a, b in zip(("dq", "dk", "dv"), g_n, g_p):
+        assert torch.equal(a, b), name
+    o_n2, g_n2, _ = _api_fwd_bwd(q, k, v, do, causal, grad_of=(1, 2))
+    assert torch.equal(o_n2, o_p2) and all(torch.equal(a, b) for a, b in zip(g_n2, g_p2))
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        o_s, g_s, _ = _api_fwd_bwd(q, k, v, do, causal)
+    torch.cuda.synchronize()
+    assert torch.equal(o_s, o_p) and all(torch.equal(a, b) for a, b in zip(g_s, g_p))
+
+
 # (B, Hq, Hkv, N, D): one MHA shape at a kernel head size, one padded head size
 # (40 runs at 64), one GQA group of 4 with a ragged length.
 NON_POSITIVE_SCALE_CASES = [(1, 2, 2, 150, 64), (1, 2, 2, 129, 40), (2, 8, 2, 97, 32)]

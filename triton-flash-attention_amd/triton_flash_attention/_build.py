@@ -3,7 +3,10 @@
 The library is compiled in-tree with ``hipcc --offload-arch=gfx950`` so that
 the shared object travels with the source tree. No JIT cache is involved.
 
-    python -m triton_flash_attention._build        # (re)build the library
+    python -m triton_flash_attention._build        # (re)build the library and the binding
+
+The C++ autograd binding (csrc/fa_native.cpp, ``_fa_native.so``) is host code
+only; it is compiled with g++ against PyTorch's headers (``build_native``).
 """
 
 from __future__ import annotations
@@ -114,10 +117,48 @@ def build(output: Path = LIB_PATH, verbose: bool = False) -> Path:
     return output
 
 
+NATIVE_SOURCE = "fa_native.cpp"
+NATIVE_PATH = PACKAGE_DIR / "_fa_native.so"
+
+
+def native_command(output: Path = NATIVE_PATH) -> list[str]:
+    """g++ line of the C++ autograd binding (host code only: PyTorch's headers
+    and libraries, ROCm's HIP headers for torch's stream API)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    libdirs = cpp_extension.library_paths()
+    return [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *(f"-I{p}" for p in cpp_extension.include_paths()),
+        f"-I{sysconfig.get_paths()['include']}", f"-I{rocm}/include",
+        str(CSRC_DIR / NATIVE_SOURCE), "-o", str(output),
+        *(f"-L{p}" for p in libdirs), *(f"-Wl,-rpath,{p}" for p in libdirs),
+        "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+    ]
+
+
+def build_native(output: Path = NATIVE_PATH, verbose: bool = False) -> Path:
+    """Compile the C++ autograd binding into ``output`` (always recompiles)."""
+    tmp = output.with_name(output.name + ".tmp")
+    cmd = native_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _check(subprocess.run(cmd, capture_output=True, text=True))
+    os.replace(tmp, output)
+    return output
+
+
 def main(argv: list[str] | None = None) -> int:
     argv = sys.argv[1:] if argv is None else argv
     path = build(verbose="-v" in argv)
     print(f"built {path}")
+    print(f"built {build_native(verbose='-v' in argv)}")
     return 0
 
 

@@ -59,7 +59,7 @@ from typing import Literal
 
 import torch
 
-from . import _lib, _ops
+from . import _lib, _native, _ops
 
 _SUPPORTED_HEAD_DIMS = (32, 64, 128)  # the kernels' widths; smaller sizes are zero-padded
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
@@ -318,6 +318,17 @@ class TritonAttention(torch.autograd.Function):
         return grad_query, grad_key, grad_value, None, None
 
 
+def _native_serves(query: torch.Tensor, value: torch.Tensor, softmax_scale: float) -> bool:
+    """Whether the C++ autograd binding (``_native``) runs this training call:
+    it makes TritonAttention's launches for a positive scale and one kernel
+    head size for q, k and v; padded head sizes, negative or zero scales and
+    forward-mode AD stay with the Python Function."""
+    head_dim = query.shape[-1]
+    return (head_dim in _SUPPORTED_HEAD_DIMS and value.shape[-1] == head_dim
+            and not _forward_ad_active() and _kernel_scale(softmax_scale)[1] == "plain"
+            and _native.available())
+
+
 def _forward_ad_active() -> bool:
     """Inside a forward-mode AD level, dual tensors carry tangents without
     requires_grad; such calls go through the autograd Function, which (like
@@ -462,6 +473,9 @@ def scaled_dot_product_attention(
     query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
     if (torch.is_grad_enabled() and (query.requires_grad or key.requires_grad
                                      or value.requires_grad)) or _forward_ad_active():
+        if _native_serves(query, value, softmax_scale):
+            # The same library calls as TritonAttention, from C++ (less host time).
+            return _native.attention(query, key, value, is_causal, softmax_scale)
         return TritonAttention.apply(query, key, value, is_causal, softmax_scale)
     # No gradient can flow (inference, or under torch.no_grad()): the same
     # forward launch without the autograd Function's bookkeeping.
