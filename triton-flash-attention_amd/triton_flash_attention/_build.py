@@ -155,10 +155,13 @@ def build_native(output: Path = NATIVE_PATH, verbose: bool = False) -> Path:
 
 
 def main(argv: list[str] | None = None) -> int:
+    from concurrent.futures import ThreadPoolExecutor
+
     argv = sys.argv[1:] if argv is None else argv
-    path = build(verbose="-v" in argv)
-    print(f"built {path}")
-    print(f"built {build_native(verbose='-v' in argv)}")
+    with ThreadPoolExecutor(max_workers=1) as pool:
+        native = pool.submit(build_native, verbose="-v" in argv)
+        print(f"built {build(verbose='-v' in argv)}")
+        print(f"built {native.result()}")
     return 0
 
 
