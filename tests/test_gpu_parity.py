@@ -219,6 +219,12 @@ def test_native_binding_matches_the_python_function_bitwise(case, monkeypatch):
         o_s, g_s, _ = _api_fwd_bwd(q, k, v, do, causal)
     torch.cuda.synchronize()
     assert torch.equal(o_s, o_p) and all(torch.equal(a, b) for a, b in zip(g_s, g_p))
+    # No gradient: the binding's forward-only entry, the same launch.
+    with torch.no_grad():
+        o_i = scaled_dot_product_attention(q.to(DEV), k.to(DEV), v.to(DEV), is_causal=causal,
+                                           enable_gqa=Hq != Hkv, backend="triton")
+    torch.cuda.synchronize()
+    assert o_i.grad_fn is None and torch.equal(o_i, o_p)
 
 
 # (B, Hq, Hkv, N, D): one MHA shape at a kernel head size, one padded head size

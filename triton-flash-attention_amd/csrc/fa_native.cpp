@@ -9,9 +9,11 @@
 // calls from a C++ torch::autograd::Function: fa_fwd_kv (or fa_fwd_ws when the
 // forward splits its keys) and fa_bwd, with the same arguments, the same
 // workspaces and on torch's current stream, so its results are identical bit
-// for bit. It serves the plain case only: a positive scale and one kernel head
-// size (32, 64 or 128) for q, k and v; attention.py keeps the Python Function
-// for the rest (negative or zero scales, padded head sizes, forward-mode AD).
+// for bit. forward() serves calls that need no gradient the same way (the op
+// layer's flash_fwd, without the Python around it). Both serve the plain case
+// only: a positive scale and one kernel head size (32, 64 or 128) for q, k and
+// v; attention.py keeps the Python path for the rest (negative or zero scales,
+// padded head sizes, forward-mode AD).
 //
 // The library's entry points come from the copy Python has already loaded
 // (init() takes their addresses), so one libfa_gfx950.so serves both paths.
@@ -103,33 +105,45 @@ Dims dims_of(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
   return {q.size(0), q.size(1), k.size(1), q.size(2), k.size(2), q.size(3)};
 }
 
+// The forward launch (the op layer's flash_fwd): O and the base-2 LSE of
+// aligned q, k, v on the current stream of their device.
+struct Forward {
+  at::Tensor q, k, v, o, lse;
+};
+
+Forward run_forward(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                    bool causal, double scale) {
+  const Dims d = dims_of(query, key, value);
+  const int e = elem_index(query);
+  Forward f{aligned(query), aligned(key), aligned(value), at::Tensor(), at::Tensor()};
+  c10::DeviceGuard guard(f.q.device());
+  f.o = at::empty_like(f.q);
+  f.lse = at::empty({d.B, d.Hq, d.N}, f.q.options().dtype(at::kFloat));
+  const int c = causal ? 1 : 0;
+  const float s = static_cast<float>(scale);
+  const int64_t ws_bytes = g.fwd_ws_bytes(d.B, d.Hq, d.Hkv, d.N, d.Nkv, d.D, c);
+  const at::Tensor ws = workspace(ws_bytes, f.q);
+  void* stream = stream_of(f.q);
+  if (ws_bytes > 0)
+    check(g.fwd_ws[e](f.q.data_ptr(), f.k.data_ptr(), f.v.data_ptr(), f.o.data_ptr(),
+                      f.lse.data_ptr(), d.B, d.Hq, d.Hkv, d.N, d.Nkv, d.D, s, c, ws.data_ptr(),
+                      ws_bytes, stream));
+  else
+    check(g.fwd_kv[e](f.q.data_ptr(), f.k.data_ptr(), f.v.data_ptr(), f.o.data_ptr(),
+                      f.lse.data_ptr(), d.B, d.Hq, d.Hkv, d.N, d.Nkv, d.D, s, c, stream));
+  return f;
+}
+
 class FlashAttention : public torch::autograd::Function<FlashAttention> {
  public:
   static at::Tensor forward(torch::autograd::AutogradContext* ctx, const at::Tensor& query,
                             const at::Tensor& key, const at::Tensor& value, bool causal,
                             double scale) {
-    const Dims d = dims_of(query, key, value);
-    const int e = elem_index(query);
-    const at::Tensor q = aligned(query), k = aligned(key), v = aligned(value);
-    c10::DeviceGuard guard(q.device());
-    at::Tensor o = at::empty_like(q);
-    at::Tensor lse = at::empty({d.B, d.Hq, d.N}, q.options().dtype(at::kFloat));
-    const int c = causal ? 1 : 0;
-    const float s = static_cast<float>(scale);
-    const int64_t ws_bytes = g.fwd_ws_bytes(d.B, d.Hq, d.Hkv, d.N, d.Nkv, d.D, c);
-    const at::Tensor ws = workspace(ws_bytes, q);
-    void* stream = stream_of(q);
-    if (ws_bytes > 0)
-      check(g.fwd_ws[e](q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                        d.B, d.Hq, d.Hkv, d.N, d.Nkv, d.D, s, c, ws.data_ptr(), ws_bytes,
-                        stream));
-    else
-      check(g.fwd_kv[e](q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                        d.B, d.Hq, d.Hkv, d.N, d.Nkv, d.D, s, c, stream));
-    ctx->save_for_backward({q, k, v, o, lse});
+    Forward f = run_forward(query, key, value, causal, scale);
+    ctx->save_for_backward({f.q, f.k, f.v, f.o, f.lse});
     ctx->saved_data["causal"] = causal;
     ctx->saved_data["scale"] = scale;
-    return o;
+    return f.o;
   }
 
   static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
@@ -163,6 +177,13 @@ at::Tensor attention(const at::Tensor& query, const at::Tensor& key, const at::T
   return FlashAttention::apply(query, key, value, causal, scale);
 }
 
+// O without autograd (inference: no input needs a gradient).
+at::Tensor forward_only(const at::Tensor& query, const at::Tensor& key, const at::Tensor& value,
+                        bool causal, double scale) {
+  if (!ready()) throw std::runtime_error("gfx950 attention: init() has not run");
+  return run_forward(query, key, value, causal, scale).o;
+}
+
 // Takes the entry points' addresses: fa_fwd_kv, fa_fwd_kv_bf16, fa_fwd_ws,
 // fa_fwd_ws_bf16, fa_bwd, fa_bwd_bf16, fa_fwd_workspace_bytes,
 // fa_bwd_workspace_bytes, fa_last_error.
@@ -190,4 +211,5 @@ PYBIND11_MODULE(_fa_native, m) {
   m.def("init", &init);
   m.def("ready", &ready);
   m.def("attention", &attention);
+  m.def("forward", &forward_only);
 }

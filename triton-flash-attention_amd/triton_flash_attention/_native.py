@@ -67,6 +67,12 @@ def status() -> tuple[bool, str]:
     return available(), _error or ""
 
 
+def forward(query, key, value, causal: bool, scale: float):
+    """O = attention(query, key, value) without autograd, through the binding
+    (same served case as :func:`attention`)."""
+    return _module.forward(query, key, value, bool(causal), float(scale))
+
+
 def attention(query, key, value, causal: bool, scale: float):
     """O = attention(query, key, value), differentiable, through the binding.
     The caller guarantees the served case: contiguous fp16/bf16 GPU tensors,

@@ -319,10 +319,10 @@ class TritonAttention(torch.autograd.Function):
 
 
 def _native_serves(query: torch.Tensor, value: torch.Tensor, softmax_scale: float) -> bool:
-    """Whether the C++ autograd binding (``_native``) runs this training call:
-    it makes TritonAttention's launches for a positive scale and one kernel
-    head size for q, k and v; padded head sizes, negative or zero scales and
-    forward-mode AD stay with the Python Function."""
+    """Whether the C++ binding (``_native``) runs this call: it makes
+    TritonAttention's launches (or, without autograd, the forward's) for a
+    positive scale and one kernel head size for q, k and v; padded head sizes,
+    negative or zero scales and forward-mode AD stay in Python."""
     head_dim = query.shape[-1]
     return (head_dim in _SUPPORTED_HEAD_DIMS and value.shape[-1] == head_dim
             and not _forward_ad_active() and _kernel_scale(softmax_scale)[1] == "plain"
@@ -479,6 +479,8 @@ def scaled_dot_product_attention(
         return TritonAttention.apply(query, key, value, is_causal, softmax_scale)
     # No gradient can flow (inference, or under torch.no_grad()): the same
     # forward launch without the autograd Function's bookkeeping.
+    if _native_serves(query, value, softmax_scale):
+        return _native.forward(query, key, value, is_causal, softmax_scale)
     output = _padded_forward(query, key, value, is_causal, softmax_scale)[3]
     return _unpad_output(output, value.shape[-1])
 
