@@ -419,7 +419,10 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
 
   // Body of one unit in ring slot SLOT (see the header comment).
   // Operands of the second unit of a step, read during the first (FA_BWD_XPREFETCH).
+  // Step p reads the slots of units 2p-1 .. 2p+2 and its DMA fills those of
+  // units 2p+5, 2p+6 (see `step`), which are other slots of the 8-slot ring.
   half8 xpre[FA_DKDV_LEAD];
+  static_assert(NS == 8, "the step's DMA targets (units 2p+5, 2p+6) assume an 8-slot ring");
   auto body = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;
     // Steps run units in slots (2p, 2p+1): the even one prefetches for the odd one.
