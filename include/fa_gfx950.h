@@ -346,9 +346,10 @@ int fa_abi_version(void);
  * variants of a kernel (describe returns FA_ERR_BAD_TILING for one that is
  * not compiled for this head_dim); fa_set_tiling selects one for the
  * process (variant < 0 restores the default). Used by tuning sweeps. One
- * shape rule refines the table: dQ at D = 128 without the mask runs the
- * classic 4 x 32 tiling (variant 1) for fewer than 128 queries, unless a
- * tiling was set. fa_set_tiling is safe to call while other threads launch:
+ * Two shape rules refine the dQ entries at D = 128 unless a tiling was set:
+ * without the mask, fewer than 128 queries run the classic 4 x 32 tiling
+ * (variant 1); under the mask, launches of at least 128 queries and at most
+ * 768 work-groups of 128 queries run the pipelined tiling (variant 4). fa_set_tiling is safe to call while other threads launch:
  * each (kernel, D, causal) entry is an atomic that a launch reads once, so
  * the launch runs either the previous or the new tiling. */
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);

@@ -541,6 +541,38 @@ def test_short_query_dq_rule_matches_oracle_and_the_pipelined_tiling():
         torch.testing.assert_close(delta_rule, delta_pipe, rtol=1e-5, atol=1e-5, msg=tag)
 
 
+def test_causal_dq_rule_at_d128_matches_oracle_and_the_classic_tiling():
+    """dQ at D = 128 under the mask runs the pipelined tiling for launches of at
+    most 768 work-groups of 128 queries (a shape rule over the table's classic
+    4 x 32 tiling): results agree with the oracle and, to fp32 summation order,
+    with the classic tiling forced by fa_set_tiling, self- and cross-attention,
+    fp16 and bf16, one pass and with the split dQ."""
+    for (B, Hq, Hkv, N, Nkv, dtype) in [(1, 4, 1, 300, 300, torch.float16),
+                                        (2, 8, 2, 129, 700, torch.float16),
+                                        (1, 2, 2, 777, 777, torch.bfloat16),
+                                        (1, 4, 2, 128, 9000, torch.float16)]:
+        tag = f"causal dq rule B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D=128 {dtype}"
+        print(tag, flush=True)
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, 128, seed=N + Nkv + 1, mult=0.5, n_kv=Nkv,
+                                  dtype=dtype)
+        if dtype == torch.float16:
+            got = run_kernel(q, k, v, do, True)
+            check_against_oracle(got, q, k, v, do, True, tag=tag)
+        qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+        o, lse = _ops.flash_fwd(qd, kd, vd, True, 128 ** -0.5)
+        delta_rule, dq_rule = _ops.flash_bwd_dq_delta(qd, kd, vd, o, dod, lse, True, 128 ** -0.5)
+        _lib.set_tiling(_lib.KERNEL_DQ, 128, True, 1)
+        try:
+            delta_cl, dq_cl = _ops.flash_bwd_dq_delta(qd, kd, vd, o, dod, lse, True, 128 ** -0.5)
+        finally:
+            _lib.set_tiling(_lib.KERNEL_DQ, 128, True, -1)
+        torch.cuda.synchronize()
+        tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+            dict(max_abs=1e-2, rel_l2=4e-3)
+        assert_close(tag + " dq rule vs classic", dq_rule.float(), dq_cl.float(), **tol)
+        torch.testing.assert_close(delta_rule, delta_cl, rtol=1e-5, atol=1e-5, msg=tag)
+
+
 def test_forward_without_grad_matches_the_autograd_path():
     """Inputs that need no gradient (or calls under torch.no_grad()) take the
     forward launch without the autograd Function: bit-identical output, no

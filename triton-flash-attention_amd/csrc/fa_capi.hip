@@ -143,15 +143,28 @@ const fa::Variant* select_current(int kind, int di, int causal, int* index, int 
 // keys: 16 queries 147 vs 177 us, 128 queries 251 vs 239 us). A tiling set
 // with fa_set_tiling is used as set.
 constexpr int kDqShortQueryVariant = 1;
+// Under the causal mask at D = 128 the table takes that classic tiling: the
+// pipelined kernel's single wave per SIMD idles at every diagonal tile, which
+// costs more than its fused Delta pass saves once the launch has many
+// work-groups (MI355X, one box, tiling sweep, classic vs pipelined: B2 H32
+// N8192, 4096 work-groups of 128 queries, 1645 vs 1702 us; B4 H16 N4096, 2048,
+// 442 vs 465 us; B4 H16 N2048, 1024, 135 vs 136 us). Smaller launches run the
+// pipelined kernel: B1 H16 N4096, 512 work-groups, 147 vs 117 us; B1 H8 N8192,
+// 512, 277 vs 218 us; B4 H16 N1024, 512, 50 vs 45 us; B4 H16 N512, 256, 28 vs
+// 21 us.
+constexpr int kDqPipelinedVariant = 4;
+constexpr int64_t kDqPipelinedMaxWorkgroups = 768;
 
-const fa::Variant* select_dq(int di, int causal, int64_t N, int dt) {
+const fa::Variant* select_dq(int di, int causal, int64_t N, int64_t BH, int dt) {
   const int ov = override_of(fa::kDq, di, causal);
   const fa::Variant* var = select(fa::kDq, di, causal, ov, nullptr, dt);
-  if (!var || di != fa::head_dim_index(128) || causal || N >= 128 || ov >= 0) return var;
+  if (!var || di != fa::head_dim_index(128) || ov >= 0) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kDq, &count);
-  if (kDqShortQueryVariant < count && usable(vs[kDqShortQueryVariant], di, causal, dt))
-    return &vs[kDqShortQueryVariant];
+  auto pick = [&](int v) { return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var; };
+  if (!causal) return N < 128 ? pick(kDqShortQueryVariant) : var;
+  if (N >= 128 && (N + 127) / 128 * BH <= kDqPipelinedMaxWorkgroups)
+    return pick(kDqPipelinedVariant);
   return var;
 }
 
@@ -796,7 +809,7 @@ static int dq_impl(int dt, const char* name, const fa_half_t* q, const fa_half_t
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N, dt);
+  const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N, B * Hq, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
@@ -816,7 +829,7 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, dO, lse, delta, dq}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N, dt);
+  const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N, B * Hq, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   hipStream_t s = static_cast<hipStream_t>(stream);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
@@ -857,7 +870,7 @@ int64_t fa_bwd_dq_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_
   if ((rc = check_kv_length(N_kv, D))) return rc;
   int64_t bytes = 0;  // enough for either element type
   for (int dt : {fa::kF16, fa::kBF16}) {
-    const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N_q, dt);
+    const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N_q, B * Hq, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq_workspace_bytes: no kernel for the selected tiling");
     bytes = std::max(bytes, dq_workspace_bytes(dq_split(*var, B, Hq, N_q, N_kv), B, Hq, N_q, D));
   }
@@ -917,7 +930,7 @@ constexpr int64_t kPairMinSplitUnits = 32;
 bool plan_bwd(int dt, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv, int64_t D,
               int causal, BwdPlan* p) {
   const int di = fa::head_dim_index(D);
-  p->dq = select_dq(di, causal, N, dt);
+  p->dq = select_dq(di, causal, N, B * Hq, dt);
   p->dkdv = select_current(fa::kDkdv, di, causal, nullptr, dt);
   if (!p->dq || !p->dkdv) return false;
   p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv);
