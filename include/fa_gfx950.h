@@ -345,11 +345,14 @@ int fa_abi_version(void);
  * fa_num_tiling_variants / fa_describe_tiling_variant enumerate the
  * variants of a kernel (describe returns FA_ERR_BAD_TILING for one that is
  * not compiled for this head_dim); fa_set_tiling selects one for the
- * process (variant < 0 restores the default). Used by tuning sweeps. One
- * Two shape rules refine the dQ entries at D = 128 unless a tiling was set:
- * without the mask, fewer than 128 queries run the classic 4 x 32 tiling
- * (variant 1); under the mask, launches of at least 128 queries and at most
- * 768 work-groups of 128 queries run the pipelined tiling (variant 4). fa_set_tiling is safe to call while other threads launch:
+ * process (variant < 0 restores the default). Used by tuning sweeps.
+ * Three shape rules refine the dQ entries unless a tiling was set: at
+ * D = 64 without the mask, launches of at least 769 work-groups of 128
+ * queries run the pipelined tiling on 16x16x32 MFMAs (variant 5); at
+ * D = 128 without the mask, fewer than 128 queries run the classic 4 x 32
+ * tiling (variant 1); at D = 128 under the mask, launches of at least 128
+ * queries and at most 768 work-groups of 128 queries run the pipelined
+ * tiling (variant 4). fa_set_tiling is safe to call while other threads launch:
  * each (kernel, D, causal) entry is an atomic that a launch reads once, so
  * the launch runs either the previous or the new tiling. */
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);

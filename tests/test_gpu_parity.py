@@ -573,6 +573,45 @@ def test_causal_dq_rule_at_d128_matches_oracle_and_the_classic_tiling():
         torch.testing.assert_close(delta_rule, delta_cl, rtol=1e-5, atol=1e-5, msg=tag)
 
 
+def test_bidirectional_dq_rule_at_d64_runs_the_16x16_tiling():
+    """dQ at D = 64 without the mask runs the pipelined tiling on 16x16x32 MFMAs
+    (tiling 5) for launches of at least 769 work-groups of 128 queries: the
+    rule's result is bit-identical to tiling 5 forced by fa_set_tiling (so the
+    rule took it), agrees with the 32x32x16 tiling 4 to fp32 summation order,
+    and, through the public API at a small launch with tiling 5 set, with the
+    oracle. fp16 and bf16, MHA and GQA, a ragged N."""
+    for (B, Hq, Hkv, N, dtype) in [(4, 16, 16, 4096, torch.float16),
+                                   (2, 32, 8, 1600, torch.bfloat16)]:
+        assert (N + 127) // 128 * B * Hq >= 769
+        tag = f"bidirectional dq rule B={B} Hq={Hq} Hkv={Hkv} N={N} D=64 {dtype}"
+        print(tag, flush=True)
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, 64, seed=N + Hq, mult=0.5,
+                                                       dtype=dtype))
+        o, lse = _ops.flash_fwd(q, k, v, False, 0.125)
+        delta_rule, dq_rule = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, False, 0.125)
+        forced = {}
+        for variant in (5, 4):
+            _lib.set_tiling(_lib.KERNEL_DQ, 64, False, variant)
+            try:
+                forced[variant] = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, False, 0.125)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_DQ, 64, False, -1)
+        torch.cuda.synchronize()
+        assert torch.equal(dq_rule, forced[5][1]) and torch.equal(delta_rule, forced[5][0]), tag
+        tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+            dict(max_abs=1e-2, rel_l2=4e-3)
+        assert_close(tag + " dq 16x16 vs 32x32", dq_rule.float(), forced[4][1].float(), **tol)
+        torch.testing.assert_close(delta_rule, forced[4][0], rtol=1e-5, atol=1e-5, msg=tag)
+    # The 16x16 tiling through the public API against the oracle (GQA, ragged).
+    q, k, v, do = make_inputs(1, 6, 2, 333, 64, seed=3033, mult=0.5)
+    _lib.set_tiling(_lib.KERNEL_DQ, 64, False, 5)
+    try:
+        got = run_kernel(q, k, v, do, False)
+    finally:
+        _lib.set_tiling(_lib.KERNEL_DQ, 64, False, -1)
+    check_against_oracle(got, q, k, v, do, False, tag="dq tiling 5 B1 Hq6 Hkv2 N333 D64")
+
+
 def test_forward_without_grad_matches_the_autograd_path():
     """Inputs that need no gradient (or calls under torch.no_grad()) take the
     forward launch without the autograd Function: bit-identical output, no

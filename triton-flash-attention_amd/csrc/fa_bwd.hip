@@ -29,6 +29,7 @@
 #include <type_traits>
 
 #include "fa_bwd_pipe.hpp"
+#include "fa_bwd_pipe16.hpp"
 #include "fa_common.hpp"
 #include "fa_kernels.hpp"
 
@@ -741,6 +742,35 @@ hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// The same launch with the 16x16x32 body (fa_bwd_pipe16.hpp, D <= 64).
+template <int D, bool CAUSAL, int NW, class E = F16, bool TAIL = true>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(DqPipeTile<D, NW>::WGS_PER_CU)))
+void dq_pipe16_kernel(BwdArgs a) {
+  using T = DqPipeTile<D, NW>;
+  __shared__ __attribute__((aligned(16))) half_t lds[T::NSTAGE * T::STAGE];
+  dq_pipe16_body<D, CAUSAL, NW, E, TAIL>(a, blockIdx.x, lds);
+}
+
+template <int D, bool CAUSAL, int NW, class E = F16>
+hipError_t dq_pipe16_launch(const BwdArgs& a, hipStream_t stream) {
+  using T = DqPipeTile<D, NW>;
+  BwdArgs b = a;
+  b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
+      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (dq_tail_free(b, CAUSAL))
+    hipLaunchKernelGGL((dq_pipe16_kernel<D, CAUSAL, NW, E, false>), dim3((unsigned)blocks),
+                       dim3(T::NT), 0, stream, b);
+  else
+    hipLaunchKernelGGL((dq_pipe16_kernel<D, CAUSAL, NW, E, true>), dim3((unsigned)blocks),
+                       dim3(T::NT), 0, stream, b);
+  return hipGetLastError();
+}
+
 template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
 constexpr void* dkdv_entry() {
   if constexpr (dkdv_tiling_ok<D, NW, TILE>())
@@ -761,6 +791,14 @@ constexpr void* dq_pipe_entry() {
   static_assert(TILE == 32, "the pipelined dQ kernel streams 32-key units");
   if constexpr (dq_pipe_tiling_ok<D, NW>())
     return (void*)&dq_pipe_launch<D, CAUSAL, NW, E>;
+  else
+    return nullptr;
+}
+template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
+constexpr void* dq_pipe16_entry() {
+  static_assert(TILE == 32, "the pipelined dQ kernel streams 32-key units");
+  if constexpr (D <= 64 && dq_pipe_tiling_ok<D, NW>())
+    return (void*)&dq_pipe16_launch<D, CAUSAL, NW, E>;
   else
     return nullptr;
 }
@@ -793,6 +831,7 @@ static const Variant kDqVariants[] = {
     FA_BWD_VARIANT(dq_entry, 2, 64, 0),
     FA_BWD_VARIANT(dq_entry, 8, 64, 0),
     FA_BWD_VARIANT_BF(dq_pipe_entry, 4, 32, kFusesDelta | kPairs),
+    FA_BWD_VARIANT_BF(dq_pipe16_entry, 4, 32, kFusesDelta),
 };
 
 const Variant* dkdv_variants(int* count) {

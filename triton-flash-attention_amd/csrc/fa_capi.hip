@@ -88,7 +88,8 @@ int override_of(int kind, int di, int causal) {
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-key units, software-pipelined (all D;
 //         at D = 128 the classic 4 waves x 32 with its separate Delta pass stays
-//         faster under the causal mask)
+//         faster under the causal mask); 5 = tiling 4 on 16x16x32 MFMAs (D <= 64;
+//         select_dq takes it for large bidirectional launches at D = 64)
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
     {{6, 6}, {6, 6}, {7, 7}},  // fwd
@@ -154,14 +155,27 @@ constexpr int kDqShortQueryVariant = 1;
 // 21 us.
 constexpr int kDqPipelinedVariant = 4;
 constexpr int64_t kDqPipelinedMaxWorkgroups = 768;
+// Without the mask at D = 64, launches of more than 768 work-groups (more than
+// the combined dK/dV + dQ launch takes, whose dQ body is tiling 4's) run the
+// same pipeline on 16x16x32 MFMAs (tiling 5). The chip holds a higher clock
+// under them at its power limit (2.04 vs 1.70 GHz at B4 H16 N4096 causal,
+// rocprofv3), which pays where the MFMA pipe stays busiest: MI355X, dQ with
+// Delta, tiling 4 vs 5, B4 H16 N4096: bidirectional 359.8 vs 339.6 us and
+// 379.3 vs 370.6 us on two boxes; causal 198.6 vs 192.8 and 223.2 vs 225.8 us,
+// too close to take.
+constexpr int kDq16Variant = 5;
+constexpr int64_t kDq16MinWorkgroups = 769;
 
 const fa::Variant* select_dq(int di, int causal, int64_t N, int64_t BH, int dt) {
   const int ov = override_of(fa::kDq, di, causal);
   const fa::Variant* var = select(fa::kDq, di, causal, ov, nullptr, dt);
-  if (!var || di != fa::head_dim_index(128) || ov >= 0) return var;
+  if (!var || ov >= 0) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kDq, &count);
   auto pick = [&](int v) { return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var; };
+  if (di == fa::head_dim_index(64))
+    return !causal && (N + 127) / 128 * BH >= kDq16MinWorkgroups ? pick(kDq16Variant) : var;
+  if (di != fa::head_dim_index(128)) return var;
   if (!causal) return N < 128 ? pick(kDqShortQueryVariant) : var;
   if (N >= 128 && (N + 127) / 128 * BH <= kDqPipelinedMaxWorkgroups)
     return pick(kDqPipelinedVariant);

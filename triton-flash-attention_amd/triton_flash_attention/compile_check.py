@@ -34,7 +34,8 @@ SUPPORTED_ARCHS = ("gfx950",)
 # pipelined kernel, and the 4-wave one for short queries; at D = 32 causal
 # launches over few heads take the two-key-group forward; at D <= 64 a backward
 # whose dK/dV launch splits next to a short dQ launch runs the combined dK/dV + dQ
-# kernel).
+# kernel; dQ takes the pipelined kernel at D = 128 for short causal launches and
+# its 16x16x32 form at D = 64 for large bidirectional ones).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
@@ -54,6 +55,9 @@ def _defaults() -> tuple[str, ...]:
                           f"fa::bwd_pair_kernel<64, {c}, 4, {e}, {t}>"]
             if c == "false":
                 names.append(f"fa::dq_pipe_kernel<128, false, 4, {e}, true>")
+                names += [f"fa::dq_pipe16_kernel<64, false, 4, {e}, {t}>" for t in ("false", "true")]
+            else:
+                names += [f"fa::dq_pipe_kernel<128, true, 4, {e}, {t}>" for t in ("false", "true")]
         names.append(f"fa::fwd_pipe_kernel<32, true, 8, 1, {e}, 2>")
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
