@@ -612,6 +612,45 @@ def test_bidirectional_dq_rule_at_d64_runs_the_16x16_tiling():
     check_against_oracle(got, q, k, v, do, False, tag="dq tiling 5 B1 Hq6 Hkv2 N333 D64")
 
 
+def test_dkdv_rule_at_d64_runs_the_16x16_tiling():
+    """dK/dV at D = 64 runs the pipelined tiling on 16x16x32 MFMAs (tiling 5)
+    when the launch does not split: the rule's dK, dV are bit-identical to
+    tiling 5 forced by fa_set_tiling (so the rule took it) and agree with the
+    32x32x16 tiling 4 to fp32 summation order; through the whole backward
+    (fa_bwd) as well. A launch that splits keeps tiling 4 (bit-identical to it
+    forced). fp16 and bf16, both masks, MHA and GQA."""
+    cases = [(4, 16, 16, 4096, True, torch.float16, False),
+             (8, 32, 8, 2048, False, torch.bfloat16, False),  # 1024 key tiles
+             (2, 16, 4, 2049, True, torch.float16, True)]  # 136 key tiles: splits
+    for (B, Hq, Hkv, N, causal, dtype, splits) in cases:
+        assert ((N + 127) // 128 * B * Hkv < 768) == splits
+        tag = f"dkdv rule B={B} Hq={Hq} Hkv={Hkv} N={N} D=64 causal={causal} {dtype}"
+        print(tag, flush=True)
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, 64, seed=N + B, mult=0.5,
+                                                       dtype=dtype))
+        o, lse = _ops.flash_fwd(q, k, v, causal, 0.125)
+        delta = _ops.flash_bwd_preprocess(o, do)
+        rule = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, 0.125)
+        whole = _ops.flash_bwd(q, k, v, o, lse, do, causal, 0.125)
+        forced = {}
+        for variant in (5, 4):
+            _lib.set_tiling(_lib.KERNEL_DKDV, 64, causal, variant)
+            try:
+                forced[variant] = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, 0.125)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_DKDV, 64, causal, -1)
+        torch.cuda.synchronize()
+        same = forced[4] if splits else forced[5]
+        assert torch.equal(rule[0], same[0]) and torch.equal(rule[1], same[1]), tag
+        tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+            dict(max_abs=1e-2, rel_l2=4e-3)
+        for i, name in ((0, "dk"), (1, "dv")):
+            assert_close(f"{tag} {name} 16x16 vs 32x32", forced[5][i].float(), forced[4][i].float(),
+                         **tol)
+            assert_close(f"{tag} {name} whole backward", whole[i + 1].float(), rule[i].float(),
+                         **tol)
+
+
 def test_forward_without_grad_matches_the_autograd_path():
     """Inputs that need no gradient (or calls under torch.no_grad()) take the
     forward launch without the autograd Function: bit-identical output, no

@@ -742,7 +742,29 @@ hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// The same launch with the 16x16x32 body (fa_bwd_pipe16.hpp, D <= 64).
+// The pipelined dK/dV launch with the 16x16x32 body (fa_bwd_pipe16.hpp, D <= 64).
+template <int D, bool CAUSAL, int NW, class E = F16>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(DkdvPipeTile<D, NW>::WGS_PER_CU)))
+void dkdv_pipe16_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t lds[DkdvPipeTile<D, NW>::LDS_HALVES];
+  dkdv_pipe16_body<D, CAUSAL, NW, E>(a, blockIdx.x, lds);
+}
+
+template <int D, bool CAUSAL, int NW, class E = F16>
+hipError_t dkdv_pipe16_launch(const BwdArgs& a, hipStream_t stream) {
+  using T = DkdvPipeTile<D, NW>;
+  BwdArgs b = a;
+  b.num_tiles = (a.Nkv + T::BKV - 1) / T::BKV;
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr)) return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * a.BHkv * b.nsplit;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((dkdv_pipe16_kernel<D, CAUSAL, NW, E>), dim3((unsigned)blocks), dim3(T::NT),
+                     0, stream, b);
+  return hipGetLastError();
+}
+
+// The same dQ launch with the 16x16x32 body (fa_bwd_pipe16.hpp, D <= 64).
 template <int D, bool CAUSAL, int NW, class E = F16, bool TAIL = true>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(DqPipeTile<D, NW>::WGS_PER_CU)))
@@ -787,6 +809,14 @@ constexpr void* dkdv_pipe_entry() {
     return nullptr;
 }
 template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
+constexpr void* dkdv_pipe16_entry() {
+  static_assert(TILE == 32, "the pipelined dK/dV kernel streams 32-query units");
+  if constexpr (D <= 64 && dkdv_pipe_tiling_ok<D, NW>())
+    return (void*)&dkdv_pipe16_launch<D, CAUSAL, NW, E>;
+  else
+    return nullptr;
+}
+template <int D, bool CAUSAL, int NW, int TILE, class E = F16>
 constexpr void* dq_pipe_entry() {
   static_assert(TILE == 32, "the pipelined dQ kernel streams 32-key units");
   if constexpr (dq_pipe_tiling_ok<D, NW>())
@@ -823,6 +853,7 @@ static const Variant kDkdvVariants[] = {
     FA_BWD_VARIANT(dkdv_entry, 2, 64, 0),
     FA_BWD_VARIANT(dkdv_entry, 8, 64, 0),
     FA_BWD_VARIANT_BF(dkdv_pipe_entry, 4, 32, kPairs),
+    FA_BWD_VARIANT_BF(dkdv_pipe16_entry, 4, 32, 0),
 };
 
 static const Variant kDqVariants[] = {

@@ -84,7 +84,9 @@ int override_of(int kind, int di, int causal) {
 //         (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;
-//         D = 128 runs one work-group per CU with dK, dV in AGPRs)
+//         D = 128 runs one work-group per CU with dK, dV in AGPRs); 5 = tiling 4 on
+//         16x16x32 MFMAs (D <= 64; select_dkdv takes it at D = 64 when the launch
+//         does not split)
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-key units, software-pipelined (all D;
 //         at D = 128 the classic 4 waves x 32 with its separate Delta pass stays
@@ -343,6 +345,29 @@ int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t Hkv, int64
   const int64_t target =
       causal && 2 * wgs < kSplitTargetWorkgroups ? kSplitTargetWorkgroupsCausal : kSplitTargetWorkgroups;
   return (int)chunks_for(target, wgs, dkdv_tile_units(Hq, Hkv, N, causal), kMinSplitUnits);
+}
+
+// dK/dV tiling for a launch. At D = 64 a launch that does not split runs the
+// pipelined body on 16x16x32 MFMAs (tiling 5): the chip holds a higher clock
+// under them at its power limit (1.99 vs 1.76 GHz at B4 H16 N4096 causal,
+// rocprofv3). MI355X, one box, dK/dV tiling 4 vs 5, us: B4 H16 N4096 causal
+// 258.3 vs 246.1, bidirectional 484.8 vs 446.9; B8 H16 N2048 causal 144.6 vs
+// 140.6. Launches that split keep tiling 4, whose body the combined dK/dV + dQ
+// launch also runs (B2 Hq16 Hkv4 N2049 causal, split, 61.7 vs 62.7); at D = 32
+// tiling 5 was no faster (B1 Hq8 Hkv2 N16381 339.2 vs 337.5, B4 H16 N4096
+// 150.2 vs 153.5).
+constexpr int kDkdv16Variant = 5;
+
+const fa::Variant* select_dkdv(int di, int causal, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
+                               int64_t Nkv, int dt) {
+  const int ov = override_of(fa::kDkdv, di, causal);
+  const fa::Variant* var = select(fa::kDkdv, di, causal, ov, nullptr, dt);
+  if (!var || ov >= 0 || di != fa::head_dim_index(64)) return var;
+  if (dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal) != 1) return var;
+  int count = 0;
+  const fa::Variant* vs = registry(fa::kDkdv, &count);
+  return kDkdv16Variant < count && usable(vs[kDkdv16Variant], di, causal, dt) ? &vs[kDkdv16Variant]
+                                                                             : var;
 }
 
 int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D) {
@@ -744,7 +769,7 @@ static int dkdv_impl(int dt, const char* name, const fa_half_t* q, const fa_half
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select_current(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+  const fa::Variant* var = select_dkdv(fa::head_dim_index(D), causal, B, Hq, Hkv, N, Nkv, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
@@ -762,7 +787,7 @@ static int64_t dkdv_workspace_impl(const char* name, int64_t B, int64_t Hq, int6
   // bf16 calls on the default tiling, whose split can be larger).
   int64_t bytes = 0;
   for (int dt : {fa::kF16, fa::kBF16}) {
-    const fa::Variant* var = select_current(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+    const fa::Variant* var = select_dkdv(fa::head_dim_index(D), causal, B, Hq, Hkv, N, Nkv, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
     bytes = std::max(bytes, split_workspace_bytes(dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal),
                                                   B, Hkv, Nkv, D));
@@ -787,7 +812,7 @@ static int dkdv_ws_impl(int dt, const char* name, const fa_half_t* q, const fa_h
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, dO, lse, delta, dk, dv}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  const fa::Variant* var = select_current(fa::kDkdv, fa::head_dim_index(D), causal, nullptr, dt);
+  const fa::Variant* var = select_dkdv(fa::head_dim_index(D), causal, B, Hq, Hkv, N, Nkv, dt);
   if (!var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dk = reinterpret_cast<fa::half_t*>(dk);
@@ -945,7 +970,7 @@ bool plan_bwd(int dt, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv
               int causal, BwdPlan* p) {
   const int di = fa::head_dim_index(D);
   p->dq = select_dq(di, causal, N, B * Hq, dt);
-  p->dkdv = select_current(fa::kDkdv, di, causal, nullptr, dt);
+  p->dkdv = select_dkdv(di, causal, B, Hq, Hkv, N, Nkv, dt);
   if (!p->dq || !p->dkdv) return false;
   p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv);
   p->dkdv_nsplit = dkdv_split(*p->dkdv, B, Hq, Hkv, N, Nkv, causal);

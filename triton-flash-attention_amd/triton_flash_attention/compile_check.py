@@ -35,7 +35,8 @@ SUPPORTED_ARCHS = ("gfx950",)
 # launches over few heads take the two-key-group forward; at D <= 64 a backward
 # whose dK/dV launch splits next to a short dQ launch runs the combined dK/dV + dQ
 # kernel; dQ takes the pipelined kernel at D = 128 for short causal launches and
-# its 16x16x32 form at D = 64 for large bidirectional ones).
+# its 16x16x32 form at D = 64 for large bidirectional ones; dK/dV at D = 64 takes
+# its 16x16x32 form when the launch does not split).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
@@ -44,7 +45,7 @@ def _defaults() -> tuple[str, ...]:
                       f"fa::fwd_pipe_kernel<64, {c}, 4, 1, {e}, 1>",
                       f"fa::fwd_pipe_kernel<128, {c}, 8, 1, {e}, 1>", f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
-                      f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>",
+                      f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>", f"fa::dkdv_pipe16_kernel<64, {c}, 4, {e}>",
                       f"fa::dq_kernel<128, true, 4, 32, {e}>" if c == "true"
                       else f"fa::dq_pipe_kernel<128, false, 4, {e}, false>"]
             # dQ with and without the key-tail test (dq_tail_free)
