@@ -346,11 +346,12 @@ int fa_abi_version(void);
  * variants of a kernel (describe returns FA_ERR_BAD_TILING for one that is
  * not compiled for this head_dim); fa_set_tiling selects one for the
  * process (variant < 0 restores the default). Used by tuning sweeps.
- * At D = 64 a dK/dV launch that does not split runs the pipelined tiling on
- * 16x16x32 MFMAs (variant 5) unless a tiling was set.
- * Three shape rules refine the dQ entries unless a tiling was set: at
- * D = 64 without the mask, launches of at least 769 work-groups of 128
- * queries run the pipelined tiling on 16x16x32 MFMAs (variant 5); at
+ * A dK/dV launch that does not split runs the pipelined tiling on 16x16x32
+ * MFMAs (variant 5) at D = 64, and at D = 32 without the mask, unless a
+ * tiling was set.
+ * Three shape rules refine the dQ entries unless a tiling was set: launches
+ * of at least 769 work-groups of 128 queries run the pipelined tiling on
+ * 16x16x32 MFMAs (variant 5) at D = 64, and at D = 32 without the mask; at
  * D = 128 without the mask, fewer than 128 queries run the classic 4 x 32
  * tiling (variant 1); at D = 128 under the mask, launches of at least 128
  * queries and at most 768 work-groups of 128 queries run the pipelined

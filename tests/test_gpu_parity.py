@@ -573,74 +573,87 @@ def test_causal_dq_rule_at_d128_matches_oracle_and_the_classic_tiling():
         torch.testing.assert_close(delta_rule, delta_cl, rtol=1e-5, atol=1e-5, msg=tag)
 
 
-def test_bidirectional_dq_rule_at_d64_runs_the_16x16_tiling():
-    """dQ at D = 64 without the mask runs the pipelined tiling on 16x16x32 MFMAs
-    (tiling 5) for launches of at least 769 work-groups of 128 queries: the
-    rule's result is bit-identical to tiling 5 forced by fa_set_tiling (so the
-    rule took it), agrees with the 32x32x16 tiling 4 to fp32 summation order,
-    and, through the public API at a small launch with tiling 5 set, with the
-    oracle. fp16 and bf16, MHA and GQA, a ragged N."""
-    for (B, Hq, Hkv, N, dtype) in [(4, 16, 16, 4096, torch.float16),
-                                   (2, 32, 8, 1600, torch.bfloat16)]:
+def test_dq_rule_runs_the_16x16_tiling():
+    """dQ launches of at least 769 work-groups of 128 queries run the pipelined
+    tiling on 16x16x32 MFMAs (tiling 5) at D = 64, and at D = 32 without the
+    mask: the rule's result is bit-identical to the tiling it should take
+    forced by fa_set_tiling (5 there, the table's 4 for D = 32 under the mask)
+    and agrees with the other to fp32 summation order. Then, through the public
+    API at a small launch with tiling 5 set, against the oracle. fp16 and bf16,
+    MHA and GQA, ragged N."""
+    for (B, Hq, Hkv, N, D, causal, dtype, takes) in [
+            (4, 16, 16, 4096, 64, False, torch.float16, True),
+            (4, 16, 16, 4000, 64, True, torch.float16, True),
+            (2, 32, 8, 1600, 64, False, torch.bfloat16, True),
+            (4, 16, 16, 4096, 32, False, torch.float16, True),
+            (4, 16, 16, 4096, 32, True, torch.float16, False)]:
         assert (N + 127) // 128 * B * Hq >= 769
-        tag = f"bidirectional dq rule B={B} Hq={Hq} Hkv={Hkv} N={N} D=64 {dtype}"
+        tag = f"dq rule B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} {dtype}"
         print(tag, flush=True)
-        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, 64, seed=N + Hq, mult=0.5,
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + Hq, mult=0.5,
                                                        dtype=dtype))
-        o, lse = _ops.flash_fwd(q, k, v, False, 0.125)
-        delta_rule, dq_rule = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, False, 0.125)
+        scale = D ** -0.5
+        o, lse = _ops.flash_fwd(q, k, v, causal, scale)
+        delta_rule, dq_rule = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, causal, scale)
         forced = {}
         for variant in (5, 4):
-            _lib.set_tiling(_lib.KERNEL_DQ, 64, False, variant)
+            _lib.set_tiling(_lib.KERNEL_DQ, D, causal, variant)
             try:
-                forced[variant] = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, False, 0.125)
+                forced[variant] = _ops.flash_bwd_dq_delta(q, k, v, o, do, lse, causal, scale)
             finally:
-                _lib.set_tiling(_lib.KERNEL_DQ, 64, False, -1)
+                _lib.set_tiling(_lib.KERNEL_DQ, D, causal, -1)
         torch.cuda.synchronize()
-        assert torch.equal(dq_rule, forced[5][1]) and torch.equal(delta_rule, forced[5][0]), tag
+        same = forced[5] if takes else forced[4]
+        assert torch.equal(dq_rule, same[1]) and torch.equal(delta_rule, same[0]), tag
         tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
             dict(max_abs=1e-2, rel_l2=4e-3)
-        assert_close(tag + " dq 16x16 vs 32x32", dq_rule.float(), forced[4][1].float(), **tol)
-        torch.testing.assert_close(delta_rule, forced[4][0], rtol=1e-5, atol=1e-5, msg=tag)
+        assert_close(tag + " dq 16x16 vs 32x32", forced[5][1].float(), forced[4][1].float(), **tol)
+        torch.testing.assert_close(forced[5][0], forced[4][0], rtol=1e-5, atol=1e-5, msg=tag)
     # The 16x16 tiling through the public API against the oracle (GQA, ragged).
-    q, k, v, do = make_inputs(1, 6, 2, 333, 64, seed=3033, mult=0.5)
-    _lib.set_tiling(_lib.KERNEL_DQ, 64, False, 5)
-    try:
-        got = run_kernel(q, k, v, do, False)
-    finally:
-        _lib.set_tiling(_lib.KERNEL_DQ, 64, False, -1)
-    check_against_oracle(got, q, k, v, do, False, tag="dq tiling 5 B1 Hq6 Hkv2 N333 D64")
+    for D, causal in ((64, False), (64, True), (32, False)):
+        q, k, v, do = make_inputs(1, 6, 2, 333, D, seed=3033 + D, mult=0.5)
+        _lib.set_tiling(_lib.KERNEL_DQ, D, causal, 5)
+        try:
+            got = run_kernel(q, k, v, do, causal)
+        finally:
+            _lib.set_tiling(_lib.KERNEL_DQ, D, causal, -1)
+        check_against_oracle(got, q, k, v, do, causal,
+                             tag=f"dq tiling 5 B1 Hq6 Hkv2 N333 D{D} causal={causal}")
 
 
-def test_dkdv_rule_at_d64_runs_the_16x16_tiling():
-    """dK/dV at D = 64 runs the pipelined tiling on 16x16x32 MFMAs (tiling 5)
-    when the launch does not split: the rule's dK, dV are bit-identical to
-    tiling 5 forced by fa_set_tiling (so the rule took it) and agree with the
-    32x32x16 tiling 4 to fp32 summation order; through the whole backward
-    (fa_bwd) as well. A launch that splits keeps tiling 4 (bit-identical to it
-    forced). fp16 and bf16, both masks, MHA and GQA."""
-    cases = [(4, 16, 16, 4096, True, torch.float16, False),
-             (8, 32, 8, 2048, False, torch.bfloat16, False),  # 1024 key tiles
-             (2, 16, 4, 2049, True, torch.float16, True)]  # 136 key tiles: splits
-    for (B, Hq, Hkv, N, causal, dtype, splits) in cases:
-        assert ((N + 127) // 128 * B * Hkv < 768) == splits
-        tag = f"dkdv rule B={B} Hq={Hq} Hkv={Hkv} N={N} D=64 causal={causal} {dtype}"
+def test_dkdv_rule_runs_the_16x16_tiling():
+    """dK/dV launches that do not split run the pipelined tiling on 16x16x32
+    MFMAs (tiling 5) at D = 64, and at D = 32 without the mask: the rule's dK,
+    dV are bit-identical to the tiling it should take forced by fa_set_tiling
+    (5 there; the table's 4 for a split launch and for D = 32 under the mask)
+    and agree with the other to fp32 summation order; through the whole
+    backward (fa_bwd) as well. fp16 and bf16, both masks, MHA and GQA."""
+    cases = [(4, 16, 16, 4096, 64, True, torch.float16, True),
+             (8, 32, 8, 2048, 64, False, torch.bfloat16, True),  # 1024 key tiles
+             (2, 16, 4, 2049, 64, True, torch.float16, False),  # 136 key tiles: splits
+             (4, 16, 16, 4096, 32, False, torch.float16, True),
+             (4, 16, 16, 4096, 32, True, torch.float16, False)]
+    for (B, Hq, Hkv, N, D, causal, dtype, takes) in cases:
+        splits = (N + 127) // 128 * B * Hkv < 768
+        assert takes == (not splits and (D == 64 or not causal))
+        tag = f"dkdv rule B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} {dtype}"
         print(tag, flush=True)
-        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, 64, seed=N + B, mult=0.5,
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + B, mult=0.5,
                                                        dtype=dtype))
-        o, lse = _ops.flash_fwd(q, k, v, causal, 0.125)
+        scale = D ** -0.5
+        o, lse = _ops.flash_fwd(q, k, v, causal, scale)
         delta = _ops.flash_bwd_preprocess(o, do)
-        rule = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, 0.125)
-        whole = _ops.flash_bwd(q, k, v, o, lse, do, causal, 0.125)
+        rule = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, scale)
+        whole = _ops.flash_bwd(q, k, v, o, lse, do, causal, scale)
         forced = {}
         for variant in (5, 4):
-            _lib.set_tiling(_lib.KERNEL_DKDV, 64, causal, variant)
+            _lib.set_tiling(_lib.KERNEL_DKDV, D, causal, variant)
             try:
-                forced[variant] = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, 0.125)
+                forced[variant] = _ops.flash_bwd_dkdv(q, k, v, do, lse, delta, causal, scale)
             finally:
-                _lib.set_tiling(_lib.KERNEL_DKDV, 64, causal, -1)
+                _lib.set_tiling(_lib.KERNEL_DKDV, D, causal, -1)
         torch.cuda.synchronize()
-        same = forced[4] if splits else forced[5]
+        same = forced[5] if takes else forced[4]
         assert torch.equal(rule[0], same[0]) and torch.equal(rule[1], same[1]), tag
         tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
             dict(max_abs=1e-2, rel_l2=4e-3)

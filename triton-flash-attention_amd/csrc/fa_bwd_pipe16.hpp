@@ -15,7 +15,8 @@
 //
 // Layouts (lane l, c16 = l % 16, G = l / 16):
 //   S^T, dP^T block (kb, qb): lane holds query 16 qb + c16 of the wave and
-//     keys 16 kb + 4 G + j (j = 0..3) of the unit (the 16x16 result layout);
+//     keys 16 kb + 4 G + j (j = 0..3) of the unit (the 16x16 result layout;
+//     4 quad16(G) + j at D = 32, see rows16);
 //   value v = 8 kb + 4 qb + j of the lane's 16 score values;
 //   dQ^T block (dd, qb): lane holds query 16 qb + c16, d = 16 dd + 4 G + j.
 // dQ^T += K^T dS'^T: k-slot 8 G + 4 kb + j of the MFMA is key 16 kb + 4 G + j,
@@ -47,6 +48,22 @@ __device__ __forceinline__ float quarters_sum(float x) {
   return x + __shfl_xor(x, 32, 64);
 }
 
+// Row order of the 16x16x32 A operands read from LDS (K rows for dQ's S^T
+// and dP^T, Q and dO rows for dK/dV's S and dP). At D = 64 the natural order;
+// at D = 32 the quad swap of row_perm (quads 1 and 2 exchanged), without
+// which the transposing reads of a result quad (rows 4 G' .. 4 G' + 3 for the
+// lanes G = 0, 1 at once) hit the same banks as the quad four rows on under
+// the D = 32 swizzle (two-way conflicts, measured). Result row 4 G + j of a
+// 16-row block is then operand row 4 quad16<D>(G) + j.
+template <int D>
+__device__ __forceinline__ int rows16(int r) {
+  return D == 32 ? row_perm(r) : r;
+}
+template <int D>
+__device__ __forceinline__ int quad16(int G) {
+  return rows16<D>(4 * G) >> 2;
+}
+
 template <int D, bool CAUSAL, int NW, class E, bool TAIL = true>
 __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned block,
                                                half_t* __restrict__ lds) {
@@ -68,6 +85,7 @@ __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned 
   // the chunk order sg = -G mod 4 makes the K and V row reads free of LDS bank
   // conflicts (chunk 4 kd + G would be two-way conflicted, measured).
   const int sg = (4 - G) & 3;
+  const int gq = quad16<D>(G);  // key quad (of 16) of the lane's result rows
 
   // Split mode: the split index is the slowest-varying part of the block index.
   const int split = block / (a.num_tiles * a.BH);
@@ -213,17 +231,18 @@ __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned 
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int kd = 0; kd < KD; ++kd) r_off[kb][kd] = swz_offset<D>(16 * kb + c16, 4 * kd + sg);
+    for (int kd = 0; kd < KD; ++kd)
+      r_off[kb][kd] = swz_offset<D>(16 * kb + rows16<D>(c16), 4 * kd + sg);
   // Transposing reads of K (A operand of dQ^T += K^T dS'^T): in 16-lane group
-  // G, source lane i addresses key row 16 h + 4 G + i / 4, columns
-  // 16 dd + 4 (i % 4) .. +3, and lane i receives keys 16 h + 4 G + 0..3 of
+  // G, source lane i addresses key row 16 h + 4 gq + i / 4, columns
+  // 16 dd + 4 (i % 4) .. +3, and lane i receives keys 16 h + 4 gq + 0..3 of
   // column (d) 16 dd + i (ds_read_b64_tr_b16).
   int t_off[DD][2];
 #pragma unroll
   for (int dd = 0; dd < DD; ++dd)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int row = 16 * h + 4 * G + (c16 >> 2);
+      const int row = 16 * h + 4 * gq + (c16 >> 2);
       const int col = 16 * dd + 4 * (c16 & 3);
       t_off[dd][h] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
     }
@@ -317,7 +336,7 @@ __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned 
     // Masks as in dq_pipe_body: keys after every query of the wave, the
     // diagonal unit, and keys past the range (only in the ring's last two
     // slots, see there) get Sl = +inf, so P = 0 exactly. Value (kb, qb, j) is
-    // key ka + 16 kb + 4 G + j against query q0w + 16 qb + c16.
+    // key ka + 16 kb + 4 gq + j against query q0w + 16 qb + c16.
     constexpr bool kTailSlot = TAIL && SLOT >= NS - 2;
     auto mask_from = [&](const int (&lim)[2]) {
 #pragma unroll
@@ -326,7 +345,7 @@ __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned 
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            if (16 * kb + 4 * G + j > lim[qb]) s_cur[kb][qb][j] = inf;
+            if (16 * kb + 4 * gq + j > lim[qb]) s_cur[kb][qb][j] = inf;
     };
     if constexpr (CAUSAL) {
       if (ka > q0w) {
@@ -497,7 +516,8 @@ __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned 
 // 16 x 16 blocks (query block qb, key block kb).
 // Layouts (lane l, c16 = l % 16, G = l / 16):
 //   S, dP block (qb, kb): lane holds key 16 kb + c16 of the wave and queries
-//     16 qb + 4 G + j (j = 0..3) of the unit; value v = 8 qb + 4 kb + j;
+//     16 qb + 4 G + j (j = 0..3) of the unit (4 quad16(G) + j at D = 32);
+//     value v = 8 qb + 4 kb + j;
 //   dK^T, dV^T block (dd, kb): lane holds key 16 kb + c16, d = 16 dd + 4 G + j.
 // dV^T += dO^T P and dK^T += Q^T dS': k-slot 8 G + 4 qb + j is query
 // 16 qb + 4 G + j, so the lane's P (dS') values of blocks (0, kb), (1, kb) are
@@ -526,6 +546,7 @@ __device__ __forceinline__ void dkdv_pipe16_body(const BwdArgs& a, const unsigne
   // k-slots 8 G .. +7 of the S and dP MFMAs hold d = 32 kd + 8 sg .. +7 (the
   // conflict-free row-read order of dq_pipe16_body).
   const int sg = (4 - G) & 3;
+  const int gq = quad16<D>(G);  // query quad (of 16) of the lane's result rows
 
   const int split = block / (a.num_tiles * a.BHkv);
   const TileHead th = decode_block(block - split * a.num_tiles * a.BHkv, a.BHkv);
@@ -669,17 +690,18 @@ __device__ __forceinline__ void dkdv_pipe16_body(const BwdArgs& a, const unsigne
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int kd = 0; kd < KD; ++kd) r_off[qb][kd] = swz_offset<D>(16 * qb + c16, 4 * kd + sg);
+    for (int kd = 0; kd < KD; ++kd)
+      r_off[qb][kd] = swz_offset<D>(16 * qb + rows16<D>(c16), 4 * kd + sg);
   // Transposing reads of dO and Q (A operands of dV^T and dK^T): in 16-lane
-  // group G, source lane i addresses query row 16 h + 4 G + i / 4, columns
-  // 16 dd + 4 (i % 4) .. +3; lane i receives queries 16 h + 4 G + 0..3 of
+  // group G, source lane i addresses query row 16 h + 4 gq + i / 4, columns
+  // 16 dd + 4 (i % 4) .. +3; lane i receives queries 16 h + 4 gq + 0..3 of
   // column (d) 16 dd + i.
   int t_off[DD][2];
 #pragma unroll
   for (int dd = 0; dd < DD; ++dd)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int row = 16 * h + 4 * G + (c16 >> 2);
+      const int row = 16 * h + 4 * gq + (c16 >> 2);
       const int col = 16 * dd + 4 * (c16 & 3);
       t_off[dd][h] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
     }
@@ -697,9 +719,9 @@ __device__ __forceinline__ void dkdv_pipe16_body(const BwdArgs& a, const unsigne
     return v;
   };
   // The lane's four per-query floats of query block qb from a table of the
-  // unit's 32 queries: queries 16 qb + 4 G .. +3.
+  // unit's 32 queries: queries 16 qb + 4 gq .. +3.
   auto tab4 = [&](const float* tab, int qb) {
-    return *reinterpret_cast<const float4v*>(tab + 16 * qb + 4 * G);
+    return *reinterpret_cast<const float4v*>(tab + 16 * qb + 4 * gq);
   };
 
   float4v dk[DD][2], dv[DD][2];
@@ -790,7 +812,7 @@ __device__ __forceinline__ void dkdv_pipe16_body(const BwdArgs& a, const unsigne
     int ltab = lse_table((SLOT + 1) % NS, c_row);
     if constexpr (CAUSAL) {
       if (qa == k0w) {
-        // diagonal unit: value (qb, kb, j) is kept iff query 16 qb + 4 G + j
+        // diagonal unit: value (qb, kb, j) is kept iff query 16 qb + 4 gq + j
         // is >= key 16 kb + c16
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -798,7 +820,7 @@ __device__ __forceinline__ void dkdv_pipe16_body(const BwdArgs& a, const unsigne
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              if (16 * qb + 4 * G + j < 16 * kb + c16) s_cur[qb][kb][j] = __builtin_inff();
+              if (16 * qb + 4 * gq + j < 16 * kb + c16) s_cur[qb][kb][j] = __builtin_inff();
       }
     }
 

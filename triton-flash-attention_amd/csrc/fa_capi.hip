@@ -85,13 +85,14 @@ int override_of(int kind, int di, int causal) {
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;
 //         D = 128 runs one work-group per CU with dK, dV in AGPRs); 5 = tiling 4 on
-//         16x16x32 MFMAs (D <= 64; select_dkdv takes it at D = 64 when the launch
-//         does not split)
+//         16x16x32 MFMAs (D <= 64; select_dkdv takes it at D = 64, and at D = 32
+//         without the mask, when the launch does not split)
 //   dq  : 0 = 4 waves x 32 queries, 64-key tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-key units, software-pipelined (all D;
 //         at D = 128 the classic 4 waves x 32 with its separate Delta pass stays
 //         faster under the causal mask); 5 = tiling 4 on 16x16x32 MFMAs (D <= 64;
-//         select_dq takes it for large bidirectional launches at D = 64)
+//         select_dq takes it for large launches at D = 64, and at D = 32 without
+//         the mask)
 const int kDefault[fa::kNumKinds][3][2] = {
     // D=32     D=64     D=128   (each: {bidirectional, causal})
     {{6, 6}, {6, 6}, {7, 7}},  // fwd
@@ -157,14 +158,16 @@ constexpr int kDqShortQueryVariant = 1;
 // 21 us.
 constexpr int kDqPipelinedVariant = 4;
 constexpr int64_t kDqPipelinedMaxWorkgroups = 768;
-// Without the mask at D = 64, launches of more than 768 work-groups (more than
-// the combined dK/dV + dQ launch takes, whose dQ body is tiling 4's) run the
-// same pipeline on 16x16x32 MFMAs (tiling 5). The chip holds a higher clock
-// under them at its power limit (2.04 vs 1.70 GHz at B4 H16 N4096 causal,
-// rocprofv3), which pays where the MFMA pipe stays busiest: MI355X, dQ with
-// Delta, tiling 4 vs 5, B4 H16 N4096: bidirectional 359.8 vs 339.6 us and
-// 379.3 vs 370.6 us on two boxes; causal 198.6 vs 192.8 and 223.2 vs 225.8 us,
-// too close to take.
+// Launches of more than 768 work-groups (more than the combined dK/dV + dQ
+// launch takes, whose dQ body is tiling 4's) run the same pipeline on 16x16x32
+// MFMAs (tiling 5) at D = 64, and at D = 32 without the mask. The chip holds a
+// higher clock under them at its power limit (2.04 vs 1.70 GHz at B4 H16 N4096
+// causal, rocprofv3). MI355X, dQ with Delta, tiling 4 vs 5, us: B4 H16 N4096
+// bidirectional 359.8 vs 339.6, 379.3 vs 370.6, 409.4 vs 397.7 on three
+// boxes; causal 198.6 vs 192.8 and 223.2 vs 225.8, and the whole causal
+// training step with the 16x16x32 dK/dV 0.6567 vs 0.6518 and 0.6556 vs
+// 0.6510 ms on two boxes; D = 32, B4 H16 N4096: bidirectional 214.9 vs 207.5,
+// causal 119.3 vs 127.4 (B1 Hq8 Hkv2 N16381 causal 230.7 vs 234.6).
 constexpr int kDq16Variant = 5;
 constexpr int64_t kDq16MinWorkgroups = 769;
 
@@ -175,8 +178,11 @@ const fa::Variant* select_dq(int di, int causal, int64_t N, int64_t BH, int dt) 
   int count = 0;
   const fa::Variant* vs = registry(fa::kDq, &count);
   auto pick = [&](int v) { return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var; };
-  if (di == fa::head_dim_index(64))
-    return !causal && (N + 127) / 128 * BH >= kDq16MinWorkgroups ? pick(kDq16Variant) : var;
+  if (di != fa::head_dim_index(128)) {
+    const bool take = (di == fa::head_dim_index(64) || !causal) &&
+                      (N + 127) / 128 * BH >= kDq16MinWorkgroups;
+    return take ? pick(kDq16Variant) : var;
+  }
   if (di != fa::head_dim_index(128)) return var;
   if (!causal) return N < 128 ? pick(kDqShortQueryVariant) : var;
   if (N >= 128 && (N + 127) / 128 * BH <= kDqPipelinedMaxWorkgroups)
@@ -347,22 +353,23 @@ int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t Hkv, int64
   return (int)chunks_for(target, wgs, dkdv_tile_units(Hq, Hkv, N, causal), kMinSplitUnits);
 }
 
-// dK/dV tiling for a launch. At D = 64 a launch that does not split runs the
-// pipelined body on 16x16x32 MFMAs (tiling 5): the chip holds a higher clock
-// under them at its power limit (1.99 vs 1.76 GHz at B4 H16 N4096 causal,
-// rocprofv3). MI355X, one box, dK/dV tiling 4 vs 5, us: B4 H16 N4096 causal
-// 258.3 vs 246.1, bidirectional 484.8 vs 446.9; B8 H16 N2048 causal 144.6 vs
-// 140.6. Launches that split keep tiling 4, whose body the combined dK/dV + dQ
-// launch also runs (B2 Hq16 Hkv4 N2049 causal, split, 61.7 vs 62.7); at D = 32
-// tiling 5 was no faster (B1 Hq8 Hkv2 N16381 339.2 vs 337.5, B4 H16 N4096
-// 150.2 vs 153.5).
+// dK/dV tiling for a launch. A launch that does not split runs the pipelined
+// body on 16x16x32 MFMAs (tiling 5) at D = 64, and at D = 32 without the mask:
+// the chip holds a higher clock under them at its power limit (1.99 vs 1.76
+// GHz at B4 H16 N4096 causal, rocprofv3). MI355X, one box, dK/dV tiling 4 vs 5,
+// us: B4 H16 N4096 causal 258.3 vs 246.1, bidirectional 484.8 vs 446.9; B8 H16
+// N2048 causal 144.6 vs 140.6; D = 32 B4 H16 N4096 bidirectional 294.0 vs
+// 273.6, causal 154.1 vs 158.7 (B1 Hq8 Hkv2 N16381 344.5 vs 338.1: too close
+// to take). Launches that split keep tiling 4, whose body the combined dK/dV +
+// dQ launch also runs (B2 Hq16 Hkv4 N2049 causal, split, 61.7 vs 62.7).
 constexpr int kDkdv16Variant = 5;
 
 const fa::Variant* select_dkdv(int di, int causal, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
                                int64_t Nkv, int dt) {
   const int ov = override_of(fa::kDkdv, di, causal);
   const fa::Variant* var = select(fa::kDkdv, di, causal, ov, nullptr, dt);
-  if (!var || ov >= 0 || di != fa::head_dim_index(64)) return var;
+  if (!var || ov >= 0) return var;
+  if (di != fa::head_dim_index(64) && (di != fa::head_dim_index(32) || causal)) return var;
   if (dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal) != 1) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kDkdv, &count);

@@ -34,9 +34,8 @@ SUPPORTED_ARCHS = ("gfx950",)
 # pipelined kernel, and the 4-wave one for short queries; at D = 32 causal
 # launches over few heads take the two-key-group forward; at D <= 64 a backward
 # whose dK/dV launch splits next to a short dQ launch runs the combined dK/dV + dQ
-# kernel; dQ takes the pipelined kernel at D = 128 for short causal launches and
-# its 16x16x32 form at D = 64 for large bidirectional ones; dK/dV at D = 64 takes
-# its 16x16x32 form when the launch does not split).
+# kernel; dQ takes the pipelined kernel at D = 128 for short causal launches, and
+# dQ and dK/dV their 16x16x32 forms at D = 64 and, without the mask, D = 32).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
@@ -46,6 +45,7 @@ def _defaults() -> tuple[str, ...]:
                       f"fa::fwd_pipe_kernel<128, {c}, 8, 1, {e}, 1>", f"fa::fwd_kernel<128, {c}, 4, 32, {e}>",
                       f"fa::dkdv_pipe_kernel<32, {c}, 4, {e}>", f"fa::dkdv_pipe_kernel<64, {c}, 4, {e}>",
                       f"fa::dkdv_pipe_kernel<128, {c}, 4, {e}>", f"fa::dkdv_pipe16_kernel<64, {c}, 4, {e}>",
+                      f"fa::dkdv_pipe16_kernel<32, false, 4, {e}>",
                       f"fa::dq_kernel<128, true, 4, 32, {e}>" if c == "true"
                       else f"fa::dq_pipe_kernel<128, false, 4, {e}, false>"]
             # dQ with and without the key-tail test (dq_tail_free)
@@ -56,9 +56,11 @@ def _defaults() -> tuple[str, ...]:
                           f"fa::bwd_pair_kernel<64, {c}, 4, {e}, {t}>"]
             if c == "false":
                 names.append(f"fa::dq_pipe_kernel<128, false, 4, {e}, true>")
-                names += [f"fa::dq_pipe16_kernel<64, false, 4, {e}, {t}>" for t in ("false", "true")]
+                names += [f"fa::dq_pipe16_kernel<{d}, false, 4, {e}, {t}>"
+                          for d in (32, 64) for t in ("false", "true")]
             else:
                 names += [f"fa::dq_pipe_kernel<128, true, 4, {e}, {t}>" for t in ("false", "true")]
+                names += [f"fa::dq_pipe16_kernel<64, true, 4, {e}, {t}>" for t in ("false", "true")]
         names.append(f"fa::fwd_pipe_kernel<32, true, 8, 1, {e}, 2>")
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
