@@ -32,8 +32,10 @@ sys.path.insert(0, str(Path(__file__).resolve().parents[2]))
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 # The kernel of each bench.py kernel-pass entry (the launches of fa_bwd's
-# default plan: forward, dQ with Delta, dK/dV; split plans add helper kernels).
-KINDS = {"fwd": "fwd(_pipe)?_kernel", "dkdv": "dkdv(_pipe)?_kernel", "dq": "dq(_pipe)?_kernel"}
+# default plan: forward, dQ with Delta, dK/dV; split plans add helper kernels;
+# "pipe16" are the 16x16x32 MFMA forms).
+KINDS = {"fwd": "fwd(_pipe)?_kernel", "dkdv": "dkdv(_pipe(16)?)?_kernel",
+         "dq": "dq(_pipe(16)?)?_kernel"}
 
 
 def per_kernel_kib(path: Path, counter: str) -> dict[str, list[float]]:
