@@ -51,8 +51,8 @@ SIMDS = 1024
 
 KIND_OF = {
     "fwd_kernel": "fwd", "fwd_pipe_kernel": "fwd", "fwd_pipe_jobs_kernel": "fwd",
-    "dkdv_kernel": "dkdv", "dkdv_pipe_kernel": "dkdv",
-    "dq_kernel": "dq", "dq_pipe_kernel": "dq",
+    "dkdv_kernel": "dkdv", "dkdv_pipe_kernel": "dkdv", "dkdv_pipe16_kernel": "dkdv",
+    "dq_kernel": "dq", "dq_pipe_kernel": "dq", "dq_pipe16_kernel": "dq",
 }
 # Classic tilings (waves, streamed tile) -> variant index, as registered in
 # fa_fwd.hip (kFwdVariants) and fa_bwd.hip (kDkdvVariants, kDqVariants).
@@ -87,6 +87,8 @@ def parse_symbol(name: str):
         return kind, (7 if nw == 8 else 6), args
     if base in ("dkdv_pipe_kernel", "dq_pipe_kernel"):
         return kind, 4, args
+    if base in ("dkdv_pipe16_kernel", "dq_pipe16_kernel"):  # 16x16x32 MFMA form
+        return kind, 5, args
     # classic: <D, causal, NW, TILE, E>
     return kind, CLASSIC[kind].get((ints[1], ints[2])), args
 
