@@ -355,7 +355,14 @@ int fa_abi_version(void);
  * D = 128 without the mask, fewer than 128 queries run the classic 4 x 32
  * tiling (variant 1); at D = 128 under the mask, launches of at least 128
  * queries and at most 768 work-groups of 128 queries run the pipelined
- * tiling (variant 4). fa_set_tiling is safe to call while other threads launch:
+ * tiling (variant 4).
+ * The forward's shape rules, unless a tiling was set: at D = 128, fewer than
+ * 512 queries or fewer than 128 work-groups of 256 queries run the 4-wave
+ * tiling (variant 2) instead of the 8-wave one; at D = 32 under the mask,
+ * launches over few heads (B * Hq * (query tiles of 128 + 1) < 1536) run the
+ * two-key-group tiling (variant 8), and the other launches of at least 512
+ * queries the pipelined tiling on 16x16x32 MFMAs (variant 10).
+ * fa_set_tiling is safe to call while other threads launch:
  * each (kernel, D, causal) entry is an atomic that a launch reads once, so
  * the launch runs either the previous or the new tiling. */
 int fa_get_tiling(int kernel, int64_t D, int causal, int* out4);

@@ -664,6 +664,51 @@ def test_dkdv_rule_runs_the_16x16_tiling():
                          **tol)
 
 
+def test_d32_causal_forward_rule_runs_the_16x16_tiling():
+    """Causal forward launches at D = 32 from 512 queries that do not take the
+    two-key-group tiling run tiling 6 on 16x16x32 MFMAs (tiling 10): O and LSE
+    are bit-identical to the tiling the rule should take forced by
+    fa_set_tiling (10, 8 for few heads, the table's 6 otherwise), and tiling 10
+    agrees with 6 to fp32 summation order. Then tiling 10 through the public
+    API against the oracle (GQA, ragged N, both masks, D = 32 and 64)."""
+    for (B, Hq, Hkv, N, D, causal, dtype, expect) in [
+            (4, 16, 16, 4096, 32, True, torch.float16, 10),
+            (4, 16, 16, 4000, 32, True, torch.float16, 10),
+            (32, 16, 4, 512, 32, True, torch.bfloat16, 10),
+            (1, 16, 16, 8192, 32, True, torch.float16, 8),   # few heads: two key groups
+            (64, 16, 16, 256, 32, True, torch.float16, 6),   # short queries
+            (4, 16, 16, 4096, 32, False, torch.float16, 6),
+            (4, 16, 16, 4096, 64, True, torch.float16, 6)]:
+        tag = f"fwd rule B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal={causal} {dtype}"
+        print(tag, flush=True)
+        q, k, v, _ = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + B, dtype=dtype))
+        scale = D ** -0.5
+        rule = _ops.flash_fwd(q, k, v, causal, scale)
+        forced = {}
+        for variant in {expect, 10, 6}:
+            _lib.set_tiling(_lib.KERNEL_FWD, D, causal, variant)
+            try:
+                forced[variant] = _ops.flash_fwd(q, k, v, causal, scale)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_FWD, D, causal, -1)
+        torch.cuda.synchronize()
+        assert torch.equal(rule[0], forced[expect][0]) and \
+            torch.equal(rule[1], forced[expect][1]), tag
+        tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+            dict(max_abs=1e-2, rel_l2=4e-3)
+        assert_close(tag + " o 16x16 vs 32x32", forced[10][0].float(), forced[6][0].float(), **tol)
+        assert float((forced[10][1] - forced[6][1]).abs().max()) <= 1e-5, tag
+    for D, causal in ((32, True), (32, False), (64, True)):
+        q, k, v, do = make_inputs(1, 6, 2, 333, D, seed=4044 + D)
+        _lib.set_tiling(_lib.KERNEL_FWD, D, causal, 10)
+        try:
+            got = run_kernel(q, k, v, do, causal)
+        finally:
+            _lib.set_tiling(_lib.KERNEL_FWD, D, causal, -1)
+        check_against_oracle(got, q, k, v, do, causal,
+                             tag=f"fwd tiling 10 B1 Hq6 Hkv2 N333 D{D} causal={causal}")
+
+
 def test_forward_without_grad_matches_the_autograd_path():
     """Inputs that need no gradient (or calls under torch.no_grad()) take the
     forward launch without the autograd Function: bit-identical output, no

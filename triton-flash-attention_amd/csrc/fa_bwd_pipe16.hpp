@@ -29,41 +29,6 @@
 
 namespace fa {
 
-// D(16x16, fp32) += A(16x32) * B(32x16) in the element type. Lane l supplies
-// A row (l % 16) and B column (l % 16), each with k-values 8 (l / 16) .. +7;
-// the result: lane l holds column (l % 16), rows 4 (l / 16) + j, j = 0..3.
-template <class E> __device__ __forceinline__ float4v mma16(half8 a, half8 b, float4v c);
-template <> __device__ __forceinline__ float4v mma16<F16>(half8 a, half8 b, float4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-template <> __device__ __forceinline__ float4v mma16<BF16>(half8 a, half8 b, float4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// Sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes that hold the
-// four 8-wide quarters of a 32-wide d chunk of one query).
-__device__ __forceinline__ float quarters_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  return x + __shfl_xor(x, 32, 64);
-}
-
-// Row order of the 16x16x32 A operands read from LDS (K rows for dQ's S^T
-// and dP^T, Q and dO rows for dK/dV's S and dP). At D = 64 the natural order;
-// at D = 32 the quad swap of row_perm (quads 1 and 2 exchanged), without
-// which the transposing reads of a result quad (rows 4 G' .. 4 G' + 3 for the
-// lanes G = 0, 1 at once) hit the same banks as the quad four rows on under
-// the D = 32 swizzle (two-way conflicts, measured). Result row 4 G + j of a
-// 16-row block is then operand row 4 quad16<D>(G) + j.
-template <int D>
-__device__ __forceinline__ int rows16(int r) {
-  return D == 32 ? row_perm(r) : r;
-}
-template <int D>
-__device__ __forceinline__ int quad16(int G) {
-  return rows16<D>(4 * G) >> 2;
-}
-
 template <int D, bool CAUSAL, int NW, class E, bool TAIL = true>
 __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned block,
                                                half_t* __restrict__ lds) {

@@ -208,6 +208,13 @@ constexpr int kFwdNarrowVariant = 2;
 // where it runs one work-group per CU, it is slower: 205 vs 164 us, B2 H16
 // N2049 41 vs 34 us).
 constexpr int kFwdKeyGroupVariant = 8;
+// The other causal launches at D = 32 (from 512 queries) take tiling 6 on
+// 16x16x32 MFMAs: the chip holds a higher clock under them at its power limit
+// (MI355X, one box, tiling 6 vs 10, us: B4 H16 N4096 108.3 vs 102.0, B8 H16
+// N2048 60.6 vs 57.8, B2 H16 N8192 200.2 vs 190.1, B16 H16 N1024 38.1 vs 36.5,
+// B32 H16 N512 27.5 vs 25.9, B4 H16 N3072 64.4 vs 61.8). At D = 64 and
+// without the mask the two are within a few percent either way.
+constexpr int kFwd16Variant = 10;
 
 const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt) {
   int index = -1;
@@ -223,8 +230,10 @@ const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt)
     if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
     return pick(kFwdNarrowVariant);
   }
-  if (di == fa::head_dim_index(32) && causal && N > 32 && BH * ((N + 127) / 128 + 1) < 1536)
-    return pick(kFwdKeyGroupVariant);
+  if (di == fa::head_dim_index(32) && causal && N > 32) {
+    if (BH * ((N + 127) / 128 + 1) < 1536) return pick(kFwdKeyGroupVariant);
+    if (N >= 512) return pick(kFwd16Variant);
+  }
   return var;
 }
 

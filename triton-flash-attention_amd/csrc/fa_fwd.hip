@@ -806,6 +806,404 @@ __device__ __forceinline__ void fwd_pipe_body(const FwdArgs& a, int split, int q
   store_fwd_output<D, E>(a, ro, split, head, qrow, g, o, m, lt);
 }
 
+// --------------------------------------------------------------------------
+// The pipelined forward of tiling 6 (4 waves x 32 queries, 32-key units, one
+// unit per barrier, a 6-slot ring, three work-groups per CU) on 16x16x32
+// MFMAs (D <= 64). Each 32 x 32 block of scores is four 16 x 16 blocks (key
+// block kb, query block qb); each K row read and each transposed V read from
+// LDS feeds two MFMAs, so LDS traffic, vector work and FLOP are tiling 6's.
+// Layouts (lane l, c16 = l % 16, G = l / 16):
+//   S^T block (kb, qb): lane holds query 16 qb + c16 of the wave and keys
+//     16 kb + 4 gq + j (j = 0..3) of the unit (gq = quad16(G));
+//     value v = 8 kb + 4 qb + j of the lane's 16 score values;
+//   O^T block (dd, qb): lane holds query 16 qb + c16, d = 16 dd + 4 G + j.
+// A lane holds two queries, so the running max m and the row sums are kept
+// per query block, over the lane's 8 keys of each unit; the four lanes
+// l, l ^ 16, l ^ 32, l ^ 48 hold one query's keys, share its m (the rare
+// max update reduces over them) and add their sums at the end.
+// O^T += V^T P^T: k-slot 8 G + 4 kb + j is key 16 kb + 4 gq + j, so the
+// lane's P values of blocks (0, qb), (1, qb) are the B operand as they stand.
+// --------------------------------------------------------------------------
+template <int D, bool CAUSAL, class E>
+__device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int qtile,
+                                                int head_blk, half_t* lds) {
+  constexpr int NW = 4;
+  using T = FwdPipeTile<D, NW, 1, 1>;
+  using Dma = DmaStager<D, T::KT, NW>;
+  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
+  static_assert(D == 32 || D == 64, "16x16x32 forward: D <= 64");
+  constexpr int NS = T::NSTAGE;
+  constexpr int IPU = 2;   // this wave's DMA instructions per unit: K, V
+  constexpr int KD = D / 32;  // 32-wide d chunks: k-steps of S^T
+  constexpr int DD = D / 16;  // 16-row d blocks of O^T
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15;
+  const int G = lane >> 4;
+  const int sg = (4 - G) & 3;   // d chunk order of the k-slots (conflict-free row reads)
+  const int gq = quad16<D>(G);  // key quad (of 16) of the lane's result rows
+
+  // Packed GQA: the work-group serves P query heads, wave w head w % P.
+  const int P = a.pack;
+  const int head = head_blk * P + wave % P;  // wave-uniform
+  const int b = head / a.Hq;
+  const int hq = head - b * a.Hq;
+  const int kvh = b * a.Hkv + hq / a.group;
+  const int N = a.N;      // queries
+  const int Nkv = a.Nkv;  // keys
+  const uint32_t slab = (uint32_t)N * D * 2u;
+  const uint32_t kv_slab = (uint32_t)Nkv * D * 2u;
+  const rsrc_t rq = make_rsrc(a.q + (int64_t)head * N * D, slab);
+  const rsrc_t ro = make_rsrc(a.o + (int64_t)head * N * D, slab);
+  const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
+  const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
+
+  const int bm = T::BM / P;  // query rows per head
+  const int q0 = qtile * bm;
+  const int q0w = q0 + 32 * (wave / P);
+  const int qrow0 = q0w + c16;  // query of block qb: qrow0 + 16 qb
+
+  // Q^T operand fragments: column = query 16 qb + c16, d = 32 kd + 8 sg .. +7.
+  half8 qf[2][KD];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd)
+      qf[qb][kd] = __builtin_bit_cast(
+          half8, buf_load_b128(rq, (uint32_t)((qrow0 + 16 * qb) * D + 32 * kd + 8 * sg) * 2u));
+  wait_all_vm();
+
+  const int kv_end = CAUSAL ? min(Nkv, q0 + bm) : Nkv;
+  const int kv_lo = split * a.split_keys;
+  const int kv_hi = min(kv_end, kv_lo + a.split_keys);
+  const int n_units = kv_hi > kv_lo ? (kv_hi - kv_lo + T::KT - 1) / T::KT : 0;
+  const int npad = (n_units + NS - 1) / NS * NS;
+  // Rotated ring start, as in fwd_pipe_body: the units end in the ring's last slot.
+  const int p0 = __builtin_amdgcn_readfirstlane(npad - n_units);
+  const int s0 = p0;
+
+  Dma dma;
+  dma.init(wave, lane);
+  const uint32_t lds0 = lds_addr(lds);
+  int i_row = kv_lo;  // first key row of the next unit to fetch
+  auto issue = [&](int slot) __attribute__((always_inline)) {
+    const int row0 = i_row < kv_hi ? i_row : Nkv;  // past the range: zeros
+    const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
+    const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %4\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+        "s_mov_b32 m0, %5\n\t"
+        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
+        : "memory");
+    i_row += T::KT;
+  };
+#pragma unroll
+  for (int u = 0; u < T::AHEAD; ++u) issue(s0 + u < NS ? s0 + u : s0 + u - NS);
+
+  // The V tile read as "unit -1" holds zeros (its P is zero too).
+  {
+    half_t* zs = lds + (s0 > 0 ? s0 - 1 : NS - 1) * T::STAGE + T::TILE;
+    unsigned zr;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zr));
+    const u32x4 z = {zr, zr, zr, zr};
+    for (int i = tid; i < T::TILE / 8; i += T::NT) *reinterpret_cast<u32x4*>(zs + 8 * i) = z;
+  }
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(2 * IPU) : "memory");
+
+  // Row reads of K (A operand of S^T): key row 16 kb + rows16(c16), chunk 4 kd + sg.
+  int k_off[2][KD];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd)
+      k_off[kb][kd] = swz_offset<D>(16 * kb + rows16<D>(c16), 4 * kd + sg);
+  // Transposing reads of V (A operand of O^T += V^T P^T): in 16-lane group G,
+  // source lane i addresses key row 16 h + 4 gq + i / 4, columns
+  // 16 dd + 4 (i % 4) .. +3; lane i receives keys 16 h + 4 gq + 0..3 of
+  // column (d) 16 dd + i.
+  int v_off[DD][2];
+#pragma unroll
+  for (int dd = 0; dd < DD; ++dd)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = 16 * h + 4 * gq + (c16 >> 2);
+      const int col = 16 * dd + 4 * (c16 & 3);
+      v_off[dd][h] = row * D + 8 * swz_chunk<D>(row, col >> 3) + (col & 7);
+    }
+  auto trv = [&](const half_t* base, int dd) {
+    const half4 lo = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + v_off[dd][0])));
+    const half4 hi = __builtin_bit_cast(
+        half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + v_off[dd][1])));
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
+    return v;
+  };
+
+  float4v o[DD][2];
+#pragma unroll
+  for (int dd = 0; dd < DD; ++dd)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[dd][qb][j] = 0.f;
+  float m[2] = {-INFINITY, -INFINITY};  // reference max per query block (scaled, log2 units)
+  float l[2] = {0.f, 0.f};              // this lane's partial sums of exp2(s c - m)
+  const float c = a.c;
+  const float inf = __builtin_inff();
+
+  // Pipeline registers: S^T of the current unit ([kb][qb]), P^T of the previous
+  // one (B operands, [qb]).
+  float4v s_cur[2][2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_cur[kb][qb][j] = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd) {
+      const half8 ok = *reinterpret_cast<const half8*>(lds + s0 * T::STAGE + k_off[kb][kd]);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) s_cur[kb][qb] = mma16<E>(ok, qf[qb][kd], s_cur[kb][qb]);
+    }
+  half8 pa_prev[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pa_prev[qb][e] = (half_t)0.f;
+
+  int c_key = kv_lo;  // first key of the unit the body works on
+
+  auto body = [&](auto slot_c) __attribute__((always_inline)) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    const half_t* nxt = lds + ((SLOT + 1) % NS) * T::STAGE;
+    const half_t* prv = lds + ((SLOT + NS - 1) % NS) * T::STAGE;
+    const int ka = c_key;
+    c_key += T::KT;
+
+    // Unit modes (wave-uniform): keys all past the queries (or past N_kv), or
+    // a diagonal / tail unit whose masked scores become -inf.
+    const bool dead = (CAUSAL && ka > q0w) || ka >= kv_hi;
+    float m_eff[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) m_eff[qb] = dead ? inf : m[qb];
+    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > kv_hi)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int key = ka + 16 * kb + 4 * gq + j;
+            if (key >= kv_hi || (CAUSAL && key > qrow0 + 16 * qb)) s_cur[kb][qb][j] = -inf;
+          }
+    }
+
+    // Hand-ordered body: D/16 S^T tasks (unit u+1) and D/16 O^T tasks (unit
+    // u-1), alternating, each one LDS operand and two MFMAs; group i issues
+    // the LDS reads of task i + kLead, runs task i and part of unit u's
+    // vector work (as in fwd_pipe_body).
+    constexpr int NQ = D / 16;
+    constexpr int NTASK = 2 * NQ;
+    constexpr int kLead = FA_FWD_LEAD;
+    auto load_op = [&](auto t_c) -> half8 {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int q = t / 2;
+      constexpr int kb = q / KD, kd = q % KD;
+      if constexpr (t % 2 == 0) return *reinterpret_cast<const half8*>(nxt + k_off[kb][kd]);
+      else return trv(prv + T::TILE, q);
+    };
+    float4v s_nx[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s_nx[kb][qb][j] = 0.f;
+    auto run_task = [&](auto t_c, const half8& op) {
+      constexpr int t = decltype(t_c)::value;
+      constexpr int q = t / 2;
+      constexpr int kb = q / KD, kd = q % KD;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        if constexpr (t % 2 == 0) s_nx[kb][qb] = mma16<E>(op, qf[qb][kd], s_nx[kb][qb]);
+        else o[q][qb] = mma16<E>(op, pa_prev[qb], o[q][qb]);
+      }
+    };
+    half8 pa[2];
+    float pexp[16];
+    float targ[16];    // s c - m of the pairs whose exp runs in the next group
+    float lsum[2][2];  // per query block, set by its first pair
+    // Vector work on value pairs (v = 2 pr, 2 pr + 1: block kb = pr / 4,
+    // qb = pr / 2 % 2, j = 2 (pr % 2) + e) in stages placed in different
+    // groups:  F: s c - m   A: p = exp2(F)   B: row sums, fp16 P^T.
+    auto stage_f = [&](int pr) {
+      const int kb = pr >> 2, qb = (pr >> 1) & 1, j0 = 2 * (pr & 1);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) targ[2 * pr + e] = fmaf(s_cur[kb][qb][j0 + e], c, -m_eff[qb]);
+      asm volatile("" : "+v"(targ[2 * pr]), "+v"(targ[2 * pr + 1]));
+    };
+    auto stage_a = [&](int pr) {
+      float p2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) p2[e] = exp2_fast(targ[2 * pr + e]);
+      asm volatile("" : "+v"(p2[0]), "+v"(p2[1]));
+      pexp[2 * pr] = p2[0];
+      pexp[2 * pr + 1] = p2[1];
+    };
+    auto stage_b = [&](int pr) {
+      const int kb = pr >> 2, qb = (pr >> 1) & 1, j0 = 2 * (pr & 1);
+      const bool first = kb == 0 && (pr & 1) == 0;  // the block's first pair
+      half2v pp;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        lsum[qb][e] = first ? pexp[2 * pr + e] : lsum[qb][e] + pexp[2 * pr + e];
+        pp[e] = to_elem<E>(pexp[2 * pr + e]);
+      }
+      asm volatile("" : "+v"(pp));
+      pa[qb][4 * kb + j0] = pp[0];
+      pa[qb][4 * kb + j0 + 1] = pp[1];
+    };
+
+    half8 op[NTASK];
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(m_eff[0]), "+v"(m_eff[1]));
+    fwd_static_for<0, (kLead < NTASK ? kLead : NTASK)>(
+        [&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
+#pragma unroll
+    for (int pr = 0; pr < 8; ++pr)
+      if ((2 * pr * NTASK) / 16 == 0) stage_f(pr);
+    __builtin_amdgcn_sched_barrier(0);
+    fwd_static_for<0, NTASK>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(fic<i + kLead>{});
+      run_task(i_c, op[i]);
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr) {
+        const int ga = (2 * pr * NTASK) / 16;
+        const int gb = ga + 1 < NTASK ? ga + 1 : NTASK - 1;
+        if (ga == i) stage_a(pr);
+        if (gb == i) stage_b(pr);
+      }
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr)
+        if ((2 * pr * NTASK) / 16 == i + 1) stage_f(pr);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+
+    // Row sums of unit u; a rare branch moves the reference maxima (for both
+    // query blocks: the branch is wave-uniform).
+    float l_u[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) l_u[qb] = lsum[qb][0] + lsum[qb][1];
+    if (!dead && __builtin_amdgcn_ballot_w64(!(l_u[0] <= kSumLimit) || !(l_u[1] <= kSumLimit)) != 0) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float mt = s_cur[0][qb][0];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mt = __builtin_fmaxf(mt, s_cur[kb][qb][j]);
+        mt = quarters_max(mt) * c;
+        const float m_new = __builtin_fmaxf(m[qb], mt);
+        const float alpha = exp2_fast(m[qb] - m_new);
+        l[qb] *= alpha;
+#pragma unroll
+        for (int dd = 0; dd < DD; ++dd) o[dd][qb] *= alpha;
+        m[qb] = m_new;
+        l_u[qb] = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float p = exp2_fast(fmaf(s_cur[kb][qb][j], c, -m[qb]));
+            l_u[qb] += p;
+            pa[qb][4 * kb + j] = to_elem<E>(p);
+          }
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) l[qb] += l_u[qb];
+
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) s_cur[kb][qb] = s_nx[kb][qb];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) pa_prev[qb] = pa[qb];
+  };
+
+  // One barrier step per unit (tiling 6's pipeline): issue the unit AHEAD
+  // ahead into the slot of the unit finished before the last barrier, run the
+  // body, wait for all but the two most recent units.
+  auto step = [&](auto p_c) __attribute__((always_inline)) {
+    constexpr int Pp = decltype(p_c)::value;
+    issue((Pp + T::AHEAD) % NS);
+    body(fic<Pp>{});
+    wait_vm_and_barrier<2 * IPU>();
+  };
+  if (npad > 0) {
+    fwd_static_for<0, NS>([&](auto p_c) {
+      if (decltype(p_c)::value >= p0) step(p_c);
+    });
+    for (int u = NS; u < npad; u += NS) fwd_static_for<0, NS>([&](auto p_c) { step(p_c); });
+  }
+  // O of the last unit (the ring's last slot).
+#pragma unroll
+  for (int dd = 0; dd < DD; ++dd) {
+    const half8 op = trv(lds + (NS - 1) * T::STAGE + T::TILE, dd);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) o[dd][qb] = mma16<E>(op, pa_prev[qb], o[dd][qb]);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // Epilogue: the four lanes of a query add their sums; lane holds
+  // d = 16 dd + 4 G + j of query 16 qb + c16.
+  const bool split_mode = a.nsplit > 1;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float lt = quarters_sum(l[qb]);
+    const bool seen = lt > 0.f;
+    const float inv = seen ? 1.0f / lt : 0.f;
+    const int qrow = qrow0 + 16 * qb;
+    const bool row_ok = qrow < N;
+    const int64_t prow = ((int64_t)split * a.BH + head) * N + qrow;
+    float* po = split_mode ? a.part + prow * D : nullptr;  // part is null in one-pass mode
+#pragma unroll
+    for (int dd = 0; dd < DD; ++dd) {
+      float4v v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = o[dd][qb][e] * inv;
+      if (split_mode) {
+        if (row_ok) *reinterpret_cast<float4v*>(po + 16 * dd + 4 * G) = v;
+      } else {
+        buf_store_b64(ro, (uint32_t)(qrow * D + 16 * dd + 4 * G) * 2u,
+                      pack4<E>(v[0], v[1], v[2], v[3]));
+      }
+    }
+    if (G == 0 && row_ok) {
+      const float lse = seen ? m[qb] + log2_fast(lt) : -INFINITY;
+      if (split_mode) a.part[(int64_t)a.nsplit * a.BH * N * D + prow] = lse;
+      else a.lse[(int64_t)head * N + qrow] = lse;
+    }
+  }
+}
+
 // The grid form: one job per work-group, tile-major / head-minor (heaviest
 // causal tiles first), the split index slowest.
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16, int KG = 1>
@@ -905,6 +1303,45 @@ hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((fwd_pipe_kernel<D, CAUSAL, NW, UPS, E, KG>), dim3((unsigned)blocks),
                      dim3(T::NT), 0, stream, b);
   return hipGetLastError();
+}
+
+// Tiling 6 on 16x16x32 MFMAs (fwd_pipe16_body), grid form.
+template <int D, bool CAUSAL, class E = F16>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, 4, 1, 1>::WAVES_PER_SIMD)))
+void fwd_pipe16_kernel(FwdArgs a) {
+  using T = FwdPipeTile<D, 4, 1, 1>;
+  __shared__ __attribute__((aligned(16))) half_t lds[T::NSTAGE * T::STAGE];
+  const int row_wgs = a.BH / a.pack;  // work-groups per tile row
+  const int split = blockIdx.x / (a.num_tiles * row_wgs);
+  const TileHead th = decode_block_grouped(blockIdx.x - split * a.num_tiles * row_wgs, row_wgs,
+                                           a.group / a.pack);
+  const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
+  fwd_pipe16_body<D, CAUSAL, E>(a, split, qtile, th.head, lds);
+}
+
+template <int D, bool CAUSAL, class E>
+hipError_t fwd_pipe16_launch(const FwdArgs& a, hipStream_t stream) {
+  using T = FwdPipeTile<D, 4, 1, 1>;
+  FwdArgs b = a;
+  if (b.pack < 1 || 4 % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
+  b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
+  if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
+      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
+  if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((fwd_pipe16_kernel<D, CAUSAL, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
+                     stream, b);
+  return hipGetLastError();
+}
+
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
+constexpr void* fwd_pipe16_entry() {
+  if constexpr (D <= 64 && NW == 4 && UPS == 1 && fwd_pipe_tiling_ok<D, 4, 1>())
+    return (void*)&fwd_pipe16_launch<D, CAUSAL, E>;
+  else
+    return nullptr;
 }
 
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
@@ -1052,6 +1489,9 @@ static const Variant kFwdVariants[] = {
     {4, 128, 32,
      {FA_ENTRIES(fwd_pipe_jobs_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe_jobs_entry, BF16, 4, 1)},
      kSplitsKv | kJobs, FwdPipeTile<64, 4, 1>::WGS_PER_CU},
+    // 10: tiling 6 on 16x16x32 MFMAs (D <= 64)
+    {4, 128, 32, {FA_ENTRIES(fwd_pipe16_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe16_entry, BF16, 4, 1)},
+     kSplitsKv},
 };
 
 const Variant* fwd_variants(int* count) {
