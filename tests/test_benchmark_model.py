@@ -113,6 +113,10 @@ def test_tiling_sweep_rejects_bad_arguments() -> None:
         main(["--kernels", "fwd,bogus"])
     with pytest.raises(SystemExit):
         main(["--query-heads", "6", "--kv-heads", "4"])
+    with pytest.raises(SystemExit, match="comma-separated integers"):
+        main(["--variants", "6,x"])
+    with pytest.raises(SystemExit):
+        main(["--dtype", "float32"])
 
 
 def test_cross_attention_flops_count_top_left_visible_pairs() -> None:
@@ -129,3 +133,23 @@ def test_cross_attention_flops_count_top_left_visible_pairs() -> None:
             attention_flops(sequence=9, causal=causal, **kw)
     cross = memory_model(batch=1, query_heads=1, sequence=4, kv_sequence=1024)
     assert cross["naive_score_mib"] == memory_model(batch=1, query_heads=1, sequence=64)["naive_score_mib"]
+
+
+def test_tiling_ab_parses_shapes_and_rejects_bad_arguments() -> None:
+    import pytest
+
+    from benchmarks.tiling_ab import main, parse_shape
+
+    assert parse_shape("4,16,16,4096,64,causal") == {
+        "B": 4, "Hq": 16, "Hkv": 16, "N": 4096, "D": 64, "causal": True, "dtype": "float16"}
+    assert parse_shape("2,16,4,2049,32,noncausal,bfloat16")["dtype"] == "bfloat16"
+    for bad in ("4,16,16,4096,64", "4,16,16,4096,64,sliding", "4,16,16,4096,48,causal",
+                "4,6,4,4096,64,causal", "4,16,16,4096,64,causal,float32"):
+        with pytest.raises(ValueError):
+            parse_shape(bad)
+    with pytest.raises(SystemExit):
+        main(["--kernel", "fwd", "--variants", "6", "--shape", "1,1,1,64,64,causal"])
+    with pytest.raises(SystemExit):
+        main(["--kernel", "fwd", "--variants", "6,6", "--shape", "1,1,1,64,64,causal"])
+    with pytest.raises(SystemExit):
+        main(["--kernel", "fwd", "--variants", "6,10", "--shape", "1,1,1,64,65,causal"])

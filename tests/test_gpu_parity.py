@@ -808,6 +808,24 @@ def test_tiling_sweep_times_every_variant_and_restores_the_table():
         assert sum(r["table"] for r in mine) == 1
         assert all(r["us"] > 0 and r["tflops_executed"] > 0 for r in mine)
         assert _lib.get_tiling(kind, 64, True)["variant"] == before[kind]
+    # bf16, restricted to named tilings (both have bf16 builds)
+    rows = sweep(batch=1, query_heads=4, kv_heads=2, seq_len=300, head_dim=64, causal=True,
+                 kernels=["fwd"], reps=2, dtype=torch.bfloat16, variants=[6, 10])
+    assert [r["variant"] for r in rows] == [6, 10] and all(r["us"] > 0 for r in rows)
+    assert _lib.get_tiling(_lib.KERNEL_FWD, 64, True)["variant"] == before[_lib.KERNEL_FWD]
+
+
+def test_tiling_ab_alternates_tilings_and_restores_the_table():
+    """benchmarks.tiling_ab times the named tilings in interleaved rounds and
+    reports medians and ratios to the first; the table is selected afterwards."""
+    from benchmarks.tiling_ab import ab, parse_shape
+
+    for kernel, kind, variants in (("fwd", _lib.KERNEL_FWD, [6, 10]), ("dq", _lib.KERNEL_DQ, [4, 5])):
+        before = _lib.get_tiling(kind, 32, True)["variant"]
+        r = ab(kernel, variants, parse_shape("1,4,2,300,32,causal,bfloat16"), rounds=2, reps=2)
+        assert sorted(r["us"]) == sorted(str(v) for v in variants)
+        assert r["ratio"][str(variants[0])] == 1.0 and all(x > 0 for x in r["us"].values())
+        assert _lib.get_tiling(kind, 32, True)["variant"] == before
 
 
 @pytest.mark.parametrize("head_dim", [32, 64, 128])

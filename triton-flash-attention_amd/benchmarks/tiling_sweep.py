@@ -6,8 +6,10 @@ the place of the reference's Triton autotuning, which searches tile sizes per
 search, run offline: for each kernel it selects each compiled tiling with
 ``fa_set_tiling``, times that kernel alone through the op layer with HIP events
 on the current stream, and reports the fastest next to the table's choice. The
-table is restored when it returns, also after an error. fp16 only: bfloat16 is
-compiled for the table's tilings alone.
+table is restored when it returns, also after an error. Inputs are fp16 unless
+``--dtype bfloat16``; bfloat16 is compiled for some tilings only, and a bf16
+launch whose set tiling has no bf16 build runs the table's tiling
+(fa_set_tiling), so a bf16 sweep should name compiled ones with ``--variants``.
 
     python -m benchmarks.tiling_sweep --batch 4 --query-heads 16 --seq-len 4096 \\
         --head-dim 64 --mask causal
@@ -60,16 +62,18 @@ def _time_us(fn, reps: int) -> float:
 
 def sweep(*, batch: int, query_heads: int, kv_heads: int, seq_len: int, head_dim: int,
           causal: bool, kernels: list[str], reps: int = 10, seed: int = 0,
-          with_choice: bool = False) -> list[dict[str, Any]]:
+          with_choice: bool = False, dtype: torch.dtype = torch.float16,
+          variants: list[int] | None = None) -> list[dict[str, Any]]:
     """One row per (kernel, compiled tiling): waves, rows per work-group, tile,
     whether the table picks it, mean µs per launch and executed TFLOP/s. With
     ``with_choice`` each kernel also gets a row with variant ``"auto"``: no
     tiling set, so the library runs what it picks for this shape (the table
-    refined by its shape rules)."""
+    refined by its shape rules). ``variants`` restricts the sweep to those
+    tiling indices (all compiled ones by default)."""
     g = torch.Generator("cpu").manual_seed(seed)
     shapes = ((batch, query_heads, seq_len, head_dim), (batch, kv_heads, seq_len, head_dim),
               (batch, kv_heads, seq_len, head_dim), (batch, query_heads, seq_len, head_dim))
-    q, k, v, do = (torch.randn(s, generator=g).half().cuda() for s in shapes)
+    q, k, v, do = (torch.randn(s, generator=g).to(dtype).cuda() for s in shapes)
     scale = head_dim ** -0.5
     o, lse = _ops.flash_fwd(q, k, v, causal, scale)
     delta = _ops.flash_bwd_preprocess(o, do)
@@ -86,6 +90,8 @@ def sweep(*, batch: int, query_heads: int, kv_heads: int, seq_len: int, head_dim
                               head_dim=head_dim, causal=causal)
         try:
             for var in _lib.tiling_variants(kind, head_dim, causal):
+                if variants is not None and var["variant"] not in variants:
+                    continue
                 _lib.set_tiling(kind, head_dim, causal, var["variant"])
                 us = _time_us(runners[name], reps)
                 rows.append({"kernel": name, "variant": var["variant"], "waves": var["waves"],
@@ -114,6 +120,9 @@ def build_parser() -> argparse.ArgumentParser:
     parser.add_argument("--kernels", default="fwd,dkdv,dq",
                         help="comma-separated subset of fwd,dkdv,dq")
     parser.add_argument("--reps", type=int, default=10, help="launches per timing trial")
+    parser.add_argument("--dtype", choices=("float16", "bfloat16"), default="float16")
+    parser.add_argument("--variants", default=None,
+                        help="comma-separated tiling indices to time (default: every compiled one)")
     parser.add_argument("--output", type=Path, default=None, help="optional CSV file")
     return parser
 
@@ -129,13 +138,19 @@ def main(argv: list[str] | None = None) -> int:
         raise SystemExit("sizes and --reps must be positive")
     if args.query_heads % kv_heads:
         raise SystemExit("--query-heads must be a multiple of --kv-heads")
+    try:
+        variants = ([int(x) for x in args.variants.split(",") if x.strip()]
+                    if args.variants else None)
+    except ValueError:
+        raise SystemExit(f"--variants must be comma-separated integers, got {args.variants!r}")
     if not torch.cuda.is_available():
         raise SystemExit("the tiling sweep needs a GPU")
     rows = sweep(batch=args.batch, query_heads=args.query_heads, kv_heads=kv_heads,
                  seq_len=args.seq_len, head_dim=args.head_dim, causal=args.mask == "causal",
-                 kernels=kernels, reps=args.reps, with_choice=True)
+                 kernels=kernels, reps=args.reps, with_choice=True,
+                 dtype=getattr(torch, args.dtype), variants=variants)
     print(f"B={args.batch} Hq={args.query_heads} Hkv={kv_heads} N={args.seq_len} "
-          f"D={args.head_dim} {args.mask}")
+          f"D={args.head_dim} {args.mask}" + (f" {args.dtype}" if args.dtype != "float16" else ""))
     print("| kernel | variant | waves | rows | tile | table | µs | TFLOP/s executed |")
     print("|---|---:|---:|---:|---:|:---:|---:|---:|")
     for r in rows:
