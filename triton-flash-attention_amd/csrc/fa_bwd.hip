@@ -743,20 +743,21 @@ hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
 }
 
 // The pipelined dK/dV launch with the 16x16x32 body (fa_bwd_pipe16.hpp, D <= 64).
-// At D = 32 without the mask the body fits three waves per SIMD (164 VGPRs, no
-// spills; the ring leaves room for three work-groups per CU): B4 H16 N4000
-// bidirectional 310.6 -> 294.3 us on MI355X (two vs three, interleaved). Under
-// the mask three would spill, and the table runs the 32x32x16 tiling there.
-template <int D, bool CAUSAL>
+// At D = 32 without the mask the fp16 body fits three waves per SIMD (164
+// VGPRs, no spills; the ring leaves room for three work-groups per CU): B4 H16
+// N4000 bidirectional 299.4 -> 286.4 us on MI355X (two vs three, interleaved).
+// The bf16 body would spill (20 bytes per lane) and under the mask three would
+// spill as well, so those keep two.
+template <int D, bool CAUSAL, class E>
 constexpr int dkdv16_waves_per_simd() {
-  return D == 32 && !CAUSAL ? 3 : DkdvPipeTile<D, 4>::WGS_PER_CU;
+  return D == 32 && !CAUSAL && std::is_same_v<E, F16> ? 3 : DkdvPipeTile<D, 4>::WGS_PER_CU;
 }
 static_assert(3 * DkdvPipeTile<32, 4>::LDS_HALVES * 2 <= 160 * 1024,
               "three D = 32 dK/dV work-groups fit one CU's LDS");
 
 template <int D, bool CAUSAL, int NW, class E = F16>
 __global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(NW == 4 ? dkdv16_waves_per_simd<D, CAUSAL>()
+__attribute__((amdgpu_waves_per_eu(NW == 4 ? dkdv16_waves_per_simd<D, CAUSAL, E>()
                                            : DkdvPipeTile<D, NW>::WGS_PER_CU)))
 void dkdv_pipe16_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) half_t lds[DkdvPipeTile<D, NW>::LDS_HALVES];
