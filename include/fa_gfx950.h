@@ -358,7 +358,11 @@ int fa_abi_version(void);
  * tiling (variant 4).
  * The forward's shape rules, unless a tiling was set: at D = 128, fewer than
  * 512 queries or fewer than 128 work-groups of 256 queries run the 4-wave
- * tiling (variant 2) instead of the 8-wave one; at D = 32 under the mask,
+ * tiling (variant 2) instead of the 8-wave one; at D <= 64 under the mask,
+ * launches of at least 2048 queries with W = B * Hq * (query tiles of 128)
+ * between 384 and 512, or between 256 and 512 with at most 4096 queries, run
+ * the pipelined 16x16x32 tiling with 64-query work-groups (variant 11);
+ * otherwise at D = 32 under the mask,
  * launches over few heads (B * Hq * (query tiles of 128 + 1) < 1536) run the
  * two-key-group tiling (variant 8), and the other launches of at least 512
  * queries the pipelined tiling on 16x16x32 MFMAs (variant 10).

@@ -709,6 +709,53 @@ def test_d32_causal_forward_rule_runs_the_16x16_tiling():
                              tag=f"fwd tiling 10 B1 Hq6 Hkv2 N333 D{D} causal={causal}")
 
 
+def test_small_causal_forward_rule_runs_the_64_query_tiling():
+    """Causal launches at D <= 64 of at least 2048 queries whose 128-query
+    work-groups W number 384-512, or 256-512 with at most 4096 queries, run
+    the 16x16x32 forward with 64-query work-groups (tiling 11): O and LSE are
+    bit-identical to the tiling the rule should take forced by fa_set_tiling
+    (11 there; the other rules' 6 or 8 at the boundaries), and tiling 11
+    agrees with 6 to fp32 summation order. Then tiling 11 through the public
+    API against the oracle (GQA, ragged N, both masks, D = 32 and 64)."""
+    for (B, Hq, Hkv, N, D, dtype, expect) in [
+            (1, 16, 16, 2048, 64, torch.float16, 11),   # W = 256, N <= 4096
+            (1, 8, 8, 4096, 64, torch.bfloat16, 11),    # W = 256
+            (1, 24, 12, 2048, 64, torch.float16, 11),   # W = 384, GQA
+            (1, 16, 16, 4096, 32, torch.float16, 11),   # W = 512 (not two key groups)
+            (1, 4, 4, 8192, 64, torch.float16, 6),      # W = 256 with N > 4096: split-KV
+            (1, 4, 4, 8192, 32, torch.float16, 8),      # the same at D = 32: two key groups
+            (2, 16, 4, 2049, 64, torch.float16, 6),     # c3: W = 544
+            (1, 32, 8, 1024, 64, torch.float16, 6)]:    # N < 2048
+        tag = f"fwd rule B={B} Hq={Hq} Hkv={Hkv} N={N} D={D} causal {dtype}"
+        print(tag, flush=True)
+        q, k, v, _ = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + Hq, dtype=dtype))
+        scale = D ** -0.5
+        rule = _ops.flash_fwd(q, k, v, True, scale)
+        forced = {}
+        for variant in {expect, 11, 6}:
+            _lib.set_tiling(_lib.KERNEL_FWD, D, True, variant)
+            try:
+                forced[variant] = _ops.flash_fwd(q, k, v, True, scale)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_FWD, D, True, -1)
+        torch.cuda.synchronize()
+        assert torch.equal(rule[0], forced[expect][0]) and \
+            torch.equal(rule[1], forced[expect][1]), tag
+        tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+            dict(max_abs=1e-2, rel_l2=4e-3)
+        assert_close(tag + " o 64- vs 128-query", forced[11][0].float(), forced[6][0].float(), **tol)
+        assert float((forced[11][1] - forced[6][1]).abs().max()) <= 1e-5, tag
+    for D, causal in ((32, True), (32, False), (64, True), (64, False)):
+        q, k, v, do = make_inputs(1, 6, 2, 333, D, seed=5055 + D)
+        _lib.set_tiling(_lib.KERNEL_FWD, D, causal, 11)
+        try:
+            got = run_kernel(q, k, v, do, causal)
+        finally:
+            _lib.set_tiling(_lib.KERNEL_FWD, D, causal, -1)
+        check_against_oracle(got, q, k, v, do, causal,
+                             tag=f"fwd tiling 11 B1 Hq6 Hkv2 N333 D{D} causal={causal}")
+
+
 def test_forward_without_grad_matches_the_autograd_path():
     """Inputs that need no gradient (or calls under torch.no_grad()) take the
     forward launch without the autograd Function: bit-identical output, no

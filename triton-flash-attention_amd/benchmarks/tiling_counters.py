@@ -78,8 +78,8 @@ def parse_symbol(name: str):
     ints = [int(a) for a in args if re.fullmatch(r"-?\d+", a)]
     if base == "fwd_pipe_jobs_kernel":
         return kind, 9, args
-    if base == "fwd_pipe16_kernel":  # 16x16x32 MFMA form of tiling 6
-        return kind, 10, args
+    if base == "fwd_pipe16_kernel":  # 16x16x32 MFMA form of tiling 6: <D, causal, E, QB>
+        return kind, (11 if ints and ints[-1] == 1 else 10), args
     if base == "fwd_pipe_kernel":
         # <D, causal, NW, UPS, E, KG>
         nw, ups, kg = ints[1], ints[2], ints[3] if len(ints) > 3 else 1

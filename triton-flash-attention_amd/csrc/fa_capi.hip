@@ -215,6 +215,22 @@ constexpr int kFwdKeyGroupVariant = 8;
 // B32 H16 N512 27.5 vs 25.9, B4 H16 N3072 64.4 vs 61.8). At D = 64 and
 // without the mask the two are within a few percent either way.
 constexpr int kFwd16Variant = 10;
+// Causal launches at D <= 64 of 256-512 work-groups of 128 queries (W; 768
+// would fill the GPU at three per CU) take tiling 10 with one 16-row query
+// block per wave (tiling 11): 64 queries per work-group, so twice the
+// work-groups, and half the MFMA and vector work per unit on the longest key
+// loops. From W = 384 that fills the GPU; at W = 256 it still wins while the
+// key loops are short (N <= 4096). MI355X, interleaved A/B, tiling 6 (D = 64)
+// or the two-key-group tiling 8 (D = 32) against 11, us, two boxes: D = 64
+// B1 H16 N2048 30.3 / 22.3 and 30.0 / 21.7, B1 H24 N2048 34.5 / 23.9, B1 H8
+// N4096 45.7 / 38.6, B1 H12 N4096 49.4 / 43.2, B1 H16 N4096 53.5 / 48.1, B1 H8
+// N8192 99.6 / 91.0, B1 H4 N16384 192.8 / 180.3, B1 H32 N2048 30.5 / 29.4;
+// D = 32 B1 H16 N2048 24.8 / 18.3, B1 H24 N2048 28.5 / 18.5, B1 H16 N4096
+// 43.0 / 38.9, B1 H8 N8192 72.5 / 68.2. Not taken: B1 H4 N8192 (W = 256)
+// 72.0 / 78.1 at D = 64 and 46.3 / 61.2 at D = 32; c3 (W = 544) 30.6 / 31.7;
+// W = 1024 10-22 % slower. Measured from 2048 queries; shorter launches (and
+// decoding, where W counts heads only) keep the other rules.
+constexpr int kFwd16HalfVariant = 11;
 
 const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt) {
   int index = -1;
@@ -229,6 +245,11 @@ const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt)
   if (index == kFwdWideVariant) {
     if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
     return pick(kFwdNarrowVariant);
+  }
+  if (causal && di != fa::head_dim_index(128)) {
+    const int64_t W = (N + 127) / 128 * BH;
+    if (N >= 2048 && W <= 512 && (W >= 384 || (W >= 256 && N <= 4096)))
+      return pick(kFwd16HalfVariant);
   }
   if (di == fa::head_dim_index(32) && causal && N > 32) {
     if (BH * ((N + 127) / 128 + 1) < 1536) return pick(kFwdKeyGroupVariant);

@@ -807,24 +807,27 @@ __device__ __forceinline__ void fwd_pipe_body(const FwdArgs& a, int split, int q
 }
 
 // --------------------------------------------------------------------------
-// The pipelined forward of tiling 6 (4 waves x 32 queries, 32-key units, one
-// unit per barrier, a 6-slot ring, three work-groups per CU) on 16x16x32
-// MFMAs (D <= 64). Each 32 x 32 block of scores is four 16 x 16 blocks (key
-// block kb, query block qb); each K row read and each transposed V read from
-// LDS feeds two MFMAs, so LDS traffic, vector work and FLOP are tiling 6's.
+// The pipelined forward of tiling 6 (4 waves, 32-key units, one unit per
+// barrier, a 6-slot ring, three work-groups per CU) on 16x16x32 MFMAs
+// (D <= 64), with QB 16-row query blocks per wave: QB = 2 is tiling 6's
+// 32 queries per wave (tiling 10), QB = 1 halves the work-group to 64
+// queries (tiling 11: twice the work-groups and half the work per unit, for
+// launches too small to fill the GPU, whose time is their longest key loop).
+// Each 32-key unit against a query block is two 16 x 16 score blocks (key
+// block kb); each K row read and each transposed V read from LDS feeds QB
+// MFMAs, so with QB = 2 LDS traffic, vector work and FLOP are tiling 6's.
 // Layouts (lane l, c16 = l % 16, G = l / 16):
 //   S^T block (kb, qb): lane holds query 16 qb + c16 of the wave and keys
 //     16 kb + 4 gq + j (j = 0..3) of the unit (gq = quad16(G));
-//     value v = 8 kb + 4 qb + j of the lane's 16 score values;
 //   O^T block (dd, qb): lane holds query 16 qb + c16, d = 16 dd + 4 G + j.
-// A lane holds two queries, so the running max m and the row sums are kept
+// A lane holds QB queries, so the running max m and the row sums are kept
 // per query block, over the lane's 8 keys of each unit; the four lanes
 // l, l ^ 16, l ^ 32, l ^ 48 hold one query's keys, share its m (the rare
 // max update reduces over them) and add their sums at the end.
 // O^T += V^T P^T: k-slot 8 G + 4 kb + j is key 16 kb + 4 gq + j, so the
 // lane's P values of blocks (0, qb), (1, qb) are the B operand as they stand.
 // --------------------------------------------------------------------------
-template <int D, bool CAUSAL, class E>
+template <int D, bool CAUSAL, class E, int QB>
 __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int qtile,
                                                 int head_blk, half_t* lds) {
   constexpr int NW = 4;
@@ -832,6 +835,9 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
   using Dma = DmaStager<D, T::KT, NW>;
   static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
   static_assert(D == 32 || D == 64, "16x16x32 forward: D <= 64");
+  static_assert(QB == 1 || QB == 2, "one or two 16-row query blocks per wave");
+  constexpr int BM = 4 * 16 * QB;  // query rows per work-group
+  constexpr int NPAIR = 4 * QB;    // score value pairs per lane and unit
   constexpr int NS = T::NSTAGE;
   constexpr int IPU = 2;   // this wave's DMA instructions per unit: K, V
   constexpr int KD = D / 32;  // 32-wide d chunks: k-steps of S^T
@@ -860,15 +866,15 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
   const int4v r_k = make_rsrc_words(a.k + (int64_t)kvh * Nkv * D, kv_slab);
   const int4v r_v = make_rsrc_words(a.v + (int64_t)kvh * Nkv * D, kv_slab);
 
-  const int bm = T::BM / P;  // query rows per head
+  const int bm = BM / P;  // query rows per head
   const int q0 = qtile * bm;
-  const int q0w = q0 + 32 * (wave / P);
+  const int q0w = q0 + 16 * QB * (wave / P);
   const int qrow0 = q0w + c16;  // query of block qb: qrow0 + 16 qb
 
   // Q^T operand fragments: column = query 16 qb + c16, d = 32 kd + 8 sg .. +7.
-  half8 qf[2][KD];
+  half8 qf[QB][KD];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd)
       qf[qb][kd] = __builtin_bit_cast(
@@ -952,25 +958,30 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
     return v;
   };
 
-  float4v o[DD][2];
+  float4v o[DD][QB];
 #pragma unroll
   for (int dd = 0; dd < DD; ++dd)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) o[dd][qb][j] = 0.f;
-  float m[2] = {-INFINITY, -INFINITY};  // reference max per query block (scaled, log2 units)
-  float l[2] = {0.f, 0.f};              // this lane's partial sums of exp2(s c - m)
+  float m[QB], l[QB];  // reference max per query block (scaled, log2 units); this
+                       // lane's partial sums of exp2(s c - m)
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m[qb] = -INFINITY;
+    l[qb] = 0.f;
+  }
   const float c = a.c;
   const float inf = __builtin_inff();
 
   // Pipeline registers: S^T of the current unit ([kb][qb]), P^T of the previous
   // one (B operands, [qb]).
-  float4v s_cur[2][2];
+  float4v s_cur[2][QB];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int j = 0; j < 4; ++j) s_cur[kb][qb][j] = 0.f;
 #pragma unroll
@@ -979,11 +990,11 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
     for (int kd = 0; kd < KD; ++kd) {
       const half8 ok = *reinterpret_cast<const half8*>(lds + s0 * T::STAGE + k_off[kb][kd]);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) s_cur[kb][qb] = mma16<E>(ok, qf[qb][kd], s_cur[kb][qb]);
+      for (int qb = 0; qb < QB; ++qb) s_cur[kb][qb] = mma16<E>(ok, qf[qb][kd], s_cur[kb][qb]);
     }
-  half8 pa_prev[2];
+  half8 pa_prev[QB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int e = 0; e < 8; ++e) pa_prev[qb][e] = (half_t)0.f;
 
@@ -997,16 +1008,18 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
     c_key += T::KT;
 
     // Unit modes (wave-uniform): keys all past the queries (or past N_kv), or
-    // a diagonal / tail unit whose masked scores become -inf.
+    // a diagonal / tail unit whose masked scores become -inf. Units start at
+    // multiples of 32 keys and the wave's queries at a multiple of 16 QB, so
+    // a live unit holds a key past a query exactly when ka + 32 > q0w.
     const bool dead = (CAUSAL && ka > q0w) || ka >= kv_hi;
-    float m_eff[2];
+    float m_eff[QB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) m_eff[qb] = dead ? inf : m[qb];
-    if (!dead && ((CAUSAL && ka == q0w) || ka + T::KT > kv_hi)) {
+    for (int qb = 0; qb < QB; ++qb) m_eff[qb] = dead ? inf : m[qb];
+    if (!dead && ((CAUSAL && ka + T::KT > q0w) || ka + T::KT > kv_hi)) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int key = ka + 16 * kb + 4 * gq + j;
@@ -1028,11 +1041,11 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
       if constexpr (t % 2 == 0) return *reinterpret_cast<const half8*>(nxt + k_off[kb][kd]);
       else return trv(prv + T::TILE, q);
     };
-    float4v s_nx[2][2];
+    float4v s_nx[2][QB];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) s_nx[kb][qb][j] = 0.f;
     auto run_task = [&](auto t_c, const half8& op) {
@@ -1040,20 +1053,20 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
       constexpr int q = t / 2;
       constexpr int kb = q / KD, kd = q % KD;
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         if constexpr (t % 2 == 0) s_nx[kb][qb] = mma16<E>(op, qf[qb][kd], s_nx[kb][qb]);
         else o[q][qb] = mma16<E>(op, pa_prev[qb], o[q][qb]);
       }
     };
-    half8 pa[2];
-    float pexp[16];
-    float targ[16];    // s c - m of the pairs whose exp runs in the next group
-    float lsum[2][2];  // per query block, set by its first pair
-    // Vector work on value pairs (v = 2 pr, 2 pr + 1: block kb = pr / 4,
-    // qb = pr / 2 % 2, j = 2 (pr % 2) + e) in stages placed in different
+    half8 pa[QB];
+    float pexp[2 * NPAIR];
+    float targ[2 * NPAIR];  // s c - m of the pairs whose exp runs in the next group
+    float lsum[QB][2];      // per query block, set by its first pair
+    // Vector work on value pairs (v = 2 pr, 2 pr + 1: block kb = pr / (2 QB),
+    // qb = pr / 2 % QB, j = 2 (pr % 2) + e) in stages placed in different
     // groups:  F: s c - m   A: p = exp2(F)   B: row sums, fp16 P^T.
     auto stage_f = [&](int pr) {
-      const int kb = pr >> 2, qb = (pr >> 1) & 1, j0 = 2 * (pr & 1);
+      const int kb = pr / (2 * QB), qb = (pr >> 1) % QB, j0 = 2 * (pr & 1);
 #pragma unroll
       for (int e = 0; e < 2; ++e) targ[2 * pr + e] = fmaf(s_cur[kb][qb][j0 + e], c, -m_eff[qb]);
       asm volatile("" : "+v"(targ[2 * pr]), "+v"(targ[2 * pr + 1]));
@@ -1067,7 +1080,7 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
       pexp[2 * pr + 1] = p2[1];
     };
     auto stage_b = [&](int pr) {
-      const int kb = pr >> 2, qb = (pr >> 1) & 1, j0 = 2 * (pr & 1);
+      const int kb = pr / (2 * QB), qb = (pr >> 1) % QB, j0 = 2 * (pr & 1);
       const bool first = kb == 0 && (pr & 1) == 0;  // the block's first pair
       half2v pp;
 #pragma unroll
@@ -1082,38 +1095,43 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
 
     half8 op[NTASK];
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" : "+v"(m_eff[0]), "+v"(m_eff[1]));
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) asm volatile("" : "+v"(m_eff[qb]));
     fwd_static_for<0, (kLead < NTASK ? kLead : NTASK)>(
         [&](auto t_c) { op[decltype(t_c)::value] = load_op(t_c); });
 #pragma unroll
-    for (int pr = 0; pr < 8; ++pr)
-      if ((2 * pr * NTASK) / 16 == 0) stage_f(pr);
+    for (int pr = 0; pr < NPAIR; ++pr)
+      if ((pr * NTASK) / NPAIR == 0) stage_f(pr);
     __builtin_amdgcn_sched_barrier(0);
     fwd_static_for<0, NTASK>([&](auto i_c) {
       constexpr int i = decltype(i_c)::value;
       if constexpr (i + kLead < NTASK) op[i + kLead] = load_op(fic<i + kLead>{});
       run_task(i_c, op[i]);
 #pragma unroll
-      for (int pr = 0; pr < 8; ++pr) {
-        const int ga = (2 * pr * NTASK) / 16;
+      for (int pr = 0; pr < NPAIR; ++pr) {
+        const int ga = (pr * NTASK) / NPAIR;
         const int gb = ga + 1 < NTASK ? ga + 1 : NTASK - 1;
         if (ga == i) stage_a(pr);
         if (gb == i) stage_b(pr);
       }
 #pragma unroll
-      for (int pr = 0; pr < 8; ++pr)
-        if ((2 * pr * NTASK) / 16 == i + 1) stage_f(pr);
+      for (int pr = 0; pr < NPAIR; ++pr)
+        if ((pr * NTASK) / NPAIR == i + 1) stage_f(pr);
       __builtin_amdgcn_sched_barrier(0);
     });
 
     // Row sums of unit u; a rare branch moves the reference maxima (for both
     // query blocks: the branch is wave-uniform).
-    float l_u[2];
+    float l_u[QB];
+    bool over = false;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) l_u[qb] = lsum[qb][0] + lsum[qb][1];
-    if (!dead && __builtin_amdgcn_ballot_w64(!(l_u[0] <= kSumLimit) || !(l_u[1] <= kSumLimit)) != 0) {
+    for (int qb = 0; qb < QB; ++qb) {
+      l_u[qb] = lsum[qb][0] + lsum[qb][1];
+      over = over || !(l_u[qb] <= kSumLimit);
+    }
+    if (!dead && __builtin_amdgcn_ballot_w64(over) != 0) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < QB; ++qb) {
         float mt = s_cur[0][qb][0];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -1138,14 +1156,14 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
       }
     }
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) l[qb] += l_u[qb];
+    for (int qb = 0; qb < QB; ++qb) l[qb] += l_u[qb];
 
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) s_cur[kb][qb] = s_nx[kb][qb];
+      for (int qb = 0; qb < QB; ++qb) s_cur[kb][qb] = s_nx[kb][qb];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) pa_prev[qb] = pa[qb];
+    for (int qb = 0; qb < QB; ++qb) pa_prev[qb] = pa[qb];
   };
 
   // One barrier step per unit (tiling 6's pipeline): issue the unit AHEAD
@@ -1168,7 +1186,7 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
   for (int dd = 0; dd < DD; ++dd) {
     const half8 op = trv(lds + (NS - 1) * T::STAGE + T::TILE, dd);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) o[dd][qb] = mma16<E>(op, pa_prev[qb], o[dd][qb]);
+    for (int qb = 0; qb < QB; ++qb) o[dd][qb] = mma16<E>(op, pa_prev[qb], o[dd][qb]);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
@@ -1176,7 +1194,7 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
   // d = 16 dd + 4 G + j of query 16 qb + c16.
   const bool split_mode = a.nsplit > 1;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const float lt = quarters_sum(l[qb]);
     const bool seen = lt > 0.f;
     const float inv = seen ? 1.0f / lt : 0.f;
@@ -1305,8 +1323,9 @@ hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Tiling 6 on 16x16x32 MFMAs (fwd_pipe16_body), grid form.
-template <int D, bool CAUSAL, class E = F16>
+// Tiling 6 on 16x16x32 MFMAs (fwd_pipe16_body), grid form; QB query blocks
+// of 16 rows per wave (64 QB queries per work-group).
+template <int D, bool CAUSAL, class E = F16, int QB = 2>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(FwdPipeTile<D, 4, 1, 1>::WAVES_PER_SIMD)))
 void fwd_pipe16_kernel(FwdArgs a) {
@@ -1317,29 +1336,39 @@ void fwd_pipe16_kernel(FwdArgs a) {
   const TileHead th = decode_block_grouped(blockIdx.x - split * a.num_tiles * row_wgs, row_wgs,
                                            a.group / a.pack);
   const int qtile = CAUSAL ? (a.num_tiles - 1 - th.tile_rank) : th.tile_rank;
-  fwd_pipe16_body<D, CAUSAL, E>(a, split, qtile, th.head, lds);
+  fwd_pipe16_body<D, CAUSAL, E, QB>(a, split, qtile, th.head, lds);
 }
 
-template <int D, bool CAUSAL, class E>
+template <int D, bool CAUSAL, class E, int QB>
 hipError_t fwd_pipe16_launch(const FwdArgs& a, hipStream_t stream) {
   using T = FwdPipeTile<D, 4, 1, 1>;
+  constexpr int BM = 64 * QB;  // query rows per work-group
   FwdArgs b = a;
   if (b.pack < 1 || 4 % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
-  b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
+  b.num_tiles = (a.N + BM / b.pack - 1) / (BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
       (int64_t)b.nsplit * b.split_keys < a.Nkv)
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
-  hipLaunchKernelGGL((fwd_pipe16_kernel<D, CAUSAL, E>), dim3((unsigned)blocks), dim3(T::NT), 0,
-                     stream, b);
+  hipLaunchKernelGGL((fwd_pipe16_kernel<D, CAUSAL, E, QB>), dim3((unsigned)blocks), dim3(T::NT),
+                     0, stream, b);
   return hipGetLastError();
 }
 
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 constexpr void* fwd_pipe16_entry() {
   if constexpr (D <= 64 && NW == 4 && UPS == 1 && fwd_pipe_tiling_ok<D, 4, 1>())
-    return (void*)&fwd_pipe16_launch<D, CAUSAL, E>;
+    return (void*)&fwd_pipe16_launch<D, CAUSAL, E, 2>;
+  else
+    return nullptr;
+}
+
+// The same with one 16-row query block per wave (64 queries per work-group).
+template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
+constexpr void* fwd_pipe16_half_entry() {
+  if constexpr (D <= 64 && NW == 4 && UPS == 1 && fwd_pipe_tiling_ok<D, 4, 1>())
+    return (void*)&fwd_pipe16_launch<D, CAUSAL, E, 1>;
   else
     return nullptr;
 }
@@ -1491,6 +1520,10 @@ static const Variant kFwdVariants[] = {
      kSplitsKv | kJobs, FwdPipeTile<64, 4, 1>::WGS_PER_CU},
     // 10: tiling 6 on 16x16x32 MFMAs (D <= 64)
     {4, 128, 32, {FA_ENTRIES(fwd_pipe16_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe16_entry, BF16, 4, 1)},
+     kSplitsKv},
+    // 11: tiling 10 with one 16-row query block per wave, 64 queries per work-group (D <= 64)
+    {4, 64, 32,
+     {FA_ENTRIES(fwd_pipe16_half_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe16_half_entry, BF16, 4, 1)},
      kSplitsKv},
 };
 
