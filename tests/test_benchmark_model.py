@@ -141,10 +141,13 @@ def test_tiling_ab_parses_shapes_and_rejects_bad_arguments() -> None:
     from benchmarks.tiling_ab import main, parse_shape
 
     assert parse_shape("4,16,16,4096,64,causal") == {
-        "B": 4, "Hq": 16, "Hkv": 16, "N": 4096, "D": 64, "causal": True, "dtype": "float16"}
+        "B": 4, "Hq": 16, "Hkv": 16, "N": 4096, "Nkv": 4096, "D": 64, "causal": True,
+        "dtype": "float16"}
     assert parse_shape("2,16,4,2049,32,noncausal,bfloat16")["dtype"] == "bfloat16"
+    assert parse_shape("8,32,8,1,64,noncausal,float16,8192")["Nkv"] == 8192
     for bad in ("4,16,16,4096,64", "4,16,16,4096,64,sliding", "4,16,16,4096,48,causal",
-                "4,6,4,4096,64,causal", "4,16,16,4096,64,causal,float32"):
+                "4,6,4,4096,64,causal", "4,16,16,4096,64,causal,float32",
+                "4,16,16,1,64,noncausal,float16,0"):
         with pytest.raises(ValueError):
             parse_shape(bad)
     with pytest.raises(SystemExit):

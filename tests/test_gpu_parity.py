@@ -756,6 +756,47 @@ def test_small_causal_forward_rule_runs_the_64_query_tiling():
                              tag=f"fwd tiling 11 B1 Hq6 Hkv2 N333 D{D} causal={causal}")
 
 
+def test_decoding_forward_rule_runs_the_64_query_tiling():
+    """Launches of at most 32 queries at D <= 64 (decoding) whose queries fit
+    one 64-query work-group of packed heads (N_q <= 64 / P, P = gcd(Hq / Hkv,
+    4) heads per work-group) run tiling 11: O and LSE are bit-identical to
+    tiling 11 forced (to tiling 6 past that bound, and to the 4-wave tiling 2
+    that short queries take at D = 128),
+    tiling 11 agrees with 6 to fp32 summation order and, at a small shape,
+    matches the oracle. Split-KV (long keys) and packed GQA included."""
+    for (B, Hq, Hkv, Nq, Nkv, D, dtype, expect) in [
+            (8, 32, 8, 1, 8192, 64, torch.float16, 11),     # P = 4: up to 16 queries
+            (8, 32, 8, 16, 8192, 64, torch.bfloat16, 11),
+            (8, 32, 8, 17, 8192, 64, torch.float16, 6),     # two query tiles per head
+            (4, 16, 8, 32, 4096, 32, torch.float16, 11),    # P = 2: up to 32 queries
+            (2, 16, 16, 32, 16384, 64, torch.float16, 11),  # MHA, split keys
+            (8, 32, 8, 1, 8192, 128, torch.float16, 2)]:    # D = 128: short-query rule
+        tag = f"decode rule B={B} Hq={Hq} Hkv={Hkv} N_q={Nq} N_kv={Nkv} D={D} {dtype}"
+        print(tag, flush=True)
+        q, k, v, _ = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, Nq, D, seed=Nq + Nkv + D,
+                                                       n_kv=Nkv, dtype=dtype))
+        scale = D ** -0.5
+        rule = _ops.flash_fwd(q, k, v, False, scale)
+        forced = {}
+        for variant in ({expect, 6} if expect == 11 else {expect}):
+            _lib.set_tiling(_lib.KERNEL_FWD, D, False, variant)
+            try:
+                forced[variant] = _ops.flash_fwd(q, k, v, False, scale)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_FWD, D, False, -1)
+        torch.cuda.synchronize()
+        same = forced[expect]
+        assert torch.equal(rule[0], same[0]) and torch.equal(rule[1], same[1]), tag
+        if expect == 11:
+            tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+                dict(max_abs=1e-2, rel_l2=4e-3)
+            assert_close(tag + " o 64- vs 128-query", rule[0].float(), forced[6][0].float(), **tol)
+            assert float((rule[1] - forced[6][1]).abs().max()) <= 1e-5, tag
+    q, k, v, do = make_inputs(2, 8, 2, 5, 64, seed=6066, n_kv=777)
+    got = run_kernel(q, k, v, do, False)
+    check_against_oracle(got, q, k, v, do, False, tag="decode B2 Hq8 Hkv2 N_q5 N_kv777 D64")
+
+
 def test_forward_without_grad_matches_the_autograd_path():
     """Inputs that need no gradient (or calls under torch.no_grad()) take the
     forward launch without the autograd Function: bit-identical output, no

@@ -12,8 +12,9 @@ to the first one named; with ``--markdown`` also a table.
     python -m benchmarks.tiling_ab --kernel fwd --variants 6,10 \\
         --shape 4,16,16,4096,32,causal --shape 8,16,16,2048,32,causal,bfloat16
 
-A shape is ``B,Hq,Hkv,N,D,mask[,dtype]`` with mask ``causal`` or
-``noncausal`` and dtype ``float16`` (default) or ``bfloat16``. A tiling with no
+A shape is ``B,Hq,Hkv,N,D,mask[,dtype[,N_kv]]`` with mask ``causal`` or
+``noncausal``, dtype ``float16`` (default) or ``bfloat16``, and N_kv keys
+(default N; decoding shapes have few queries against many keys). A tiling with no
 build for the shape's head size or dtype runs the table's tiling
 (``fa_set_tiling``), so name compiled ones (``tiling_sweep`` lists them). The
 table is restored afterwards, also after an error.
@@ -35,18 +36,19 @@ KERNELS = {"fwd": _lib.KERNEL_FWD, "dkdv": _lib.KERNEL_DKDV, "dq": _lib.KERNEL_D
 
 def parse_shape(text: str) -> dict[str, Any]:
     parts = [p.strip() for p in text.split(",")]
-    if len(parts) not in (6, 7):
-        raise ValueError(f"shape {text!r}: expected B,Hq,Hkv,N,D,mask[,dtype]")
+    if len(parts) not in (6, 7, 8):
+        raise ValueError(f"shape {text!r}: expected B,Hq,Hkv,N,D,mask[,dtype[,N_kv]]")
     B, Hq, Hkv, N, D = (int(p) for p in parts[:5])
     mask = parts[5]
-    dtype = parts[6] if len(parts) == 7 else "float16"
+    dtype = parts[6] if len(parts) >= 7 else "float16"
+    Nkv = int(parts[7]) if len(parts) == 8 else N
     if mask not in ("causal", "noncausal"):
         raise ValueError(f"shape {text!r}: mask must be causal or noncausal")
     if dtype not in ("float16", "bfloat16"):
         raise ValueError(f"shape {text!r}: dtype must be float16 or bfloat16")
-    if min(B, Hq, Hkv, N) <= 0 or Hq % Hkv or D not in (32, 64, 128):
+    if min(B, Hq, Hkv, N, Nkv) <= 0 or Hq % Hkv or D not in (32, 64, 128):
         raise ValueError(f"shape {text!r}: positive sizes, Hq a multiple of Hkv, D in 32/64/128")
-    return {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": D, "causal": mask == "causal",
+    return {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "Nkv": Nkv, "D": D, "causal": mask == "causal",
             "dtype": dtype}
 
 
@@ -54,11 +56,12 @@ def ab(kernel: str, variants: list[int], shape: dict[str, Any], rounds: int = 7,
        reps: int = 20, seed: int = 1) -> dict[str, Any]:
     """Medians (µs) of each tiling over interleaved rounds, and ratios to the first."""
     B, Hq, Hkv, N, D, causal = (shape[k] for k in ("B", "Hq", "Hkv", "N", "D", "causal"))
+    Nkv = shape.get("Nkv", N)
     dtype = getattr(torch, shape["dtype"])
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(seed)
     q, do = (torch.randn(B, Hq, N, D, device=dev, generator=g).to(dtype) for _ in range(2))
-    k, v = (torch.randn(B, Hkv, N, D, device=dev, generator=g).to(dtype) for _ in range(2))
+    k, v = (torch.randn(B, Hkv, Nkv, D, device=dev, generator=g).to(dtype) for _ in range(2))
     scale = D ** -0.5
     o, lse = _ops.flash_fwd(q, k, v, causal, scale)
     delta = _ops.flash_bwd_preprocess(o, do)
@@ -98,7 +101,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--variants", required=True,
                         help="comma-separated tiling indices (two or more)")
     parser.add_argument("--shape", action="append", required=True,
-                        help="B,Hq,Hkv,N,D,mask[,dtype]; repeat for more shapes")
+                        help="B,Hq,Hkv,N,D,mask[,dtype[,N_kv]]; repeat for more shapes")
     parser.add_argument("--rounds", type=int, default=7)
     parser.add_argument("--reps", type=int, default=20, help="launches per timing")
     parser.add_argument("--markdown", action="store_true", help="also print a table")
@@ -123,7 +126,8 @@ def main(argv: list[str] | None = None) -> int:
         print(f"| shape | {cols} | " + " | ".join(f"{v} / {variants[0]}" for v in variants[1:]) + " |")
         print("|---|" + "---:|" * (2 * len(variants) - 1))
         for r in rows:
-            name = (f"B{r['B']} Hq{r['Hq']} Hkv{r['Hkv']} N{r['N']} D{r['D']} "
+            kv = f" N_kv{r['Nkv']}" if r["Nkv"] != r["N"] else ""
+            name = (f"B{r['B']} Hq{r['Hq']} Hkv{r['Hkv']} N{r['N']}{kv} D{r['D']} "
                     f"{'causal' if r['causal'] else 'bidirectional'} {r['dtype']}")
             us = " | ".join(str(r["us"][str(v)]) for v in variants)
             ratios = " | ".join(f"{r['ratio'][str(v)]:.3f}" for v in variants[1:])

@@ -231,8 +231,20 @@ constexpr int kFwd16Variant = 10;
 // W = 1024 10-22 % slower. Measured from 2048 queries; shorter launches (and
 // decoding, where W counts heads only) keep the other rules.
 constexpr int kFwd16HalfVariant = 11;
+// Decoding at D <= 64 (at most 32 queries; packed GQA: P = gcd(group, 4)
+// heads per work-group) takes tiling 11 too while its 64 / P rows per head
+// hold all the queries: the same K/V passes as the 128-query tilings with
+// half their padding rows. MI355X, interleaved, B8 Hq32 against 8192 keys,
+// library (tiling 6) vs 11, us: D = 64 Hkv8 Nq 1 / 8 / 16 26.0 / 25.2, 27.8 /
+// 26.3, 30.0 / 27.3; Hkv4 Nq 1 / 16 24.3 / 19.6, 28.6 / 22.1; Hkv16 Nq 32
+// 52.6 / 51.8; Hkv32 Nq 1 98.6 / 96.9; D = 32 Hkv8 Nq 1 / 16 20.5 / 16.7,
+// 23.0 / 18.2; Hkv32 Nq 32 55.9 / 47.1. With more queries than that (Hkv8 Nq
+// 17, 32: two query tiles per head, twice the K/V passes) 10-17 % slower.
+constexpr int64_t kFwdDecodeQueries = 32;
 
-const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt) {
+int fwd_pack(const fa::Variant& var, int64_t group, int64_t N);  // below
+
+const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int64_t group, int dt) {
   int index = -1;
   const int ov = override_of(fa::kFwd, di, causal);
   const fa::Variant* var = select(fa::kFwd, di, causal, ov, &index, dt);
@@ -245,6 +257,10 @@ const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int dt)
   if (index == kFwdWideVariant) {
     if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
     return pick(kFwdNarrowVariant);
+  }
+  if (N <= kFwdDecodeQueries && di != fa::head_dim_index(128)) {
+    const fa::Variant* half = pick(kFwd16HalfVariant);
+    if (half != var && N <= half->rows / fwd_pack(*half, group, N)) return half;
   }
   if (causal && di != fa::head_dim_index(128)) {
     const int64_t W = (N + 127) / 128 * BH;
@@ -674,7 +690,7 @@ static int fwd_check(int dt, const char* name, const fa_half_t* q, const fa_half
   if ((rc = check_kv_length(Nkv, D))) return rc;
   if ((rc = check_aligned(name, {q, k, v, o, lse}))) return rc;
   if ((rc = check_scale(scale))) return rc;
-  *var = select_fwd(fa::head_dim_index(D), causal, N, B * Hq, dt);
+  *var = select_fwd(fa::head_dim_index(D), causal, N, B * Hq, Hq / Hkv, dt);
   if (!*var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
   const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, fwd_pack(**var, Hq / Hkv, N));
   *need = fwd_workspace_bytes(sp, B, Hq, N, D);
@@ -736,7 +752,7 @@ int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, 
   // Enough for either element type (their tilings can differ when overridden).
   int64_t bytes = 0;
   for (int dt : {fa::kF16, fa::kBF16}) {
-    const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, dt);
+    const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, Hq / Hkv, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_workspace_bytes: no kernel for the selected tiling");
     const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, fwd_pack(*var, Hq / Hkv, N_q));
     bytes = std::max(bytes, fwd_workspace_bytes(sp, B, Hq, N_q, D));
@@ -750,7 +766,7 @@ int fa_fwd_plan_info(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_
   int rc = check_common(B, Hq, Hkv, N_q, D);
   if (rc) return rc;
   if ((rc = check_kv_length(N_kv, D))) return rc;
-  const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, fa::kF16);
+  const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, Hq / Hkv, fa::kF16);
   if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_plan_info: no kernel for the selected tiling");
   const int pack = fwd_pack(*var, Hq / Hkv, N_q);
   const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, pack);
