@@ -757,11 +757,11 @@ def test_small_causal_forward_rule_runs_the_64_query_tiling():
 
 
 def test_decoding_forward_rule_runs_the_64_query_tiling():
-    """Launches of at most 32 queries at D <= 64 (decoding) whose queries fit
+    """Launches of at most 32 queries (decoding, any head size) whose queries fit
     one 64-query work-group of packed heads (N_q <= 64 / P, P = gcd(Hq / Hkv,
     4) heads per work-group) run tiling 11: O and LSE are bit-identical to
-    tiling 11 forced (to tiling 6 past that bound, and to the 4-wave tiling 2
-    that short queries take at D = 128),
+    tiling 11 forced (past that bound to tiling 6, and at D = 128 to the
+    4-wave tiling 2 that short queries take),
     tiling 11 agrees with 6 to fp32 summation order and, at a small shape,
     matches the oracle. Split-KV (long keys) and packed GQA included."""
     for (B, Hq, Hkv, Nq, Nkv, D, dtype, expect) in [
@@ -770,7 +770,9 @@ def test_decoding_forward_rule_runs_the_64_query_tiling():
             (8, 32, 8, 17, 8192, 64, torch.float16, 6),     # two query tiles per head
             (4, 16, 8, 32, 4096, 32, torch.float16, 11),    # P = 2: up to 32 queries
             (2, 16, 16, 32, 16384, 64, torch.float16, 11),  # MHA, split keys
-            (8, 32, 8, 1, 8192, 128, torch.float16, 2)]:    # D = 128: short-query rule
+            (8, 32, 8, 1, 8192, 128, torch.float16, 11),    # D = 128: 96 KiB ring
+            (4, 16, 16, 32, 4096, 128, torch.bfloat16, 11),
+            (8, 32, 8, 17, 8192, 128, torch.float16, 2)]:   # past the bound: short-query rule
         tag = f"decode rule B={B} Hq={Hq} Hkv={Hkv} N_q={Nq} N_kv={Nkv} D={D} {dtype}"
         print(tag, flush=True)
         q, k, v, _ = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, Nq, D, seed=Nq + Nkv + D,
@@ -778,7 +780,8 @@ def test_decoding_forward_rule_runs_the_64_query_tiling():
         scale = D ** -0.5
         rule = _ops.flash_fwd(q, k, v, False, scale)
         forced = {}
-        for variant in ({expect, 6} if expect == 11 else {expect}):
+        base = 6 if D <= 64 else 2  # the 128-query tiling decoding took before
+        for variant in ({expect, base} if expect == 11 else {expect}):
             _lib.set_tiling(_lib.KERNEL_FWD, D, False, variant)
             try:
                 forced[variant] = _ops.flash_fwd(q, k, v, False, scale)
@@ -790,11 +793,13 @@ def test_decoding_forward_rule_runs_the_64_query_tiling():
         if expect == 11:
             tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
                 dict(max_abs=1e-2, rel_l2=4e-3)
-            assert_close(tag + " o 64- vs 128-query", rule[0].float(), forced[6][0].float(), **tol)
-            assert float((rule[1] - forced[6][1]).abs().max()) <= 1e-5, tag
-    q, k, v, do = make_inputs(2, 8, 2, 5, 64, seed=6066, n_kv=777)
-    got = run_kernel(q, k, v, do, False)
-    check_against_oracle(got, q, k, v, do, False, tag="decode B2 Hq8 Hkv2 N_q5 N_kv777 D64")
+            assert_close(tag + " o 64- vs 128-query", rule[0].float(), forced[base][0].float(),
+                         **tol)
+            assert float((rule[1] - forced[base][1]).abs().max()) <= 1e-5, tag
+    for D in (64, 128):
+        q, k, v, do = make_inputs(2, 8, 2, 5, D, seed=6066 + D, n_kv=777)
+        got = run_kernel(q, k, v, do, False)
+        check_against_oracle(got, q, k, v, do, False, tag=f"decode B2 Hq8 Hkv2 N_q5 N_kv777 D{D}")
 
 
 def test_forward_without_grad_matches_the_autograd_path():

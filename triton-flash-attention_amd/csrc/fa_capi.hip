@@ -231,15 +231,19 @@ constexpr int kFwd16Variant = 10;
 // W = 1024 10-22 % slower. Measured from 2048 queries; shorter launches (and
 // decoding, where W counts heads only) keep the other rules.
 constexpr int kFwd16HalfVariant = 11;
-// Decoding at D <= 64 (at most 32 queries; packed GQA: P = gcd(group, 4)
-// heads per work-group) takes tiling 11 too while its 64 / P rows per head
-// hold all the queries: the same K/V passes as the 128-query tilings with
-// half their padding rows. MI355X, interleaved, B8 Hq32 against 8192 keys,
-// library (tiling 6) vs 11, us: D = 64 Hkv8 Nq 1 / 8 / 16 26.0 / 25.2, 27.8 /
-// 26.3, 30.0 / 27.3; Hkv4 Nq 1 / 16 24.3 / 19.6, 28.6 / 22.1; Hkv16 Nq 32
-// 52.6 / 51.8; Hkv32 Nq 1 98.6 / 96.9; D = 32 Hkv8 Nq 1 / 16 20.5 / 16.7,
-// 23.0 / 18.2; Hkv32 Nq 32 55.9 / 47.1. With more queries than that (Hkv8 Nq
-// 17, 32: two query tiles per head, twice the K/V passes) 10-17 % slower.
+// Decoding (at most 32 queries; packed GQA: P = gcd(group, 4) heads per
+// work-group) takes tiling 11 too while its 64 / P rows per head hold all the
+// queries: the same K/V passes as the 128-query tilings with half their
+// padding rows (at D = 128 against the 4-wave classic tiling 2, which short
+// queries took before, with a 6-unit DMA ring in place of its staging).
+// MI355X, interleaved, B8 Hq32 against 8192 keys, library vs 11, us: D = 64
+// Hkv8 Nq 1 / 8 / 16 26.0 / 25.2, 27.8 / 26.3, 30.0 / 27.3; Hkv4 Nq 1 / 16
+// 24.3 / 19.6, 28.6 / 22.1; Hkv16 Nq 32 52.6 / 51.8; Hkv32 Nq 1 98.6 / 96.9;
+// D = 32 Hkv8 Nq 1 / 16 20.5 / 16.7, 23.0 / 18.2; Hkv32 Nq 32 55.9 / 47.1;
+// D = 128 Hkv8 Nq 1 / 8 / 16 48.3 / 44.6, 49.8 / 48.2, 54.6 / 52.9, Hkv32
+// Nq 1 199.7 / 186.9, Hkv16 Nq 32 124.5 / 117.2, B1 Hkv8 Nq 1 against 32768
+// keys 31.4 / 27.2. With more queries than that (Hkv8 Nq 17, 32: two query
+// tiles per head, twice the K/V passes) 10-17 % slower at D = 64.
 constexpr int64_t kFwdDecodeQueries = 32;
 
 int fwd_pack(const fa::Variant& var, int64_t group, int64_t N);  // below
@@ -254,13 +258,13 @@ const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int64_t
   auto pick = [&](int v) {
     return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var;
   };
+  if (N <= kFwdDecodeQueries) {
+    const fa::Variant* half = pick(kFwd16HalfVariant);
+    if (half != var && N <= half->rows / fwd_pack(*half, group, N)) return half;
+  }
   if (index == kFwdWideVariant) {
     if (N >= 512 && (N + var->rows - 1) / var->rows * BH >= 128) return var;
     return pick(kFwdNarrowVariant);
-  }
-  if (N <= kFwdDecodeQueries && di != fa::head_dim_index(128)) {
-    const fa::Variant* half = pick(kFwd16HalfVariant);
-    if (half != var && N <= half->rows / fwd_pack(*half, group, N)) return half;
   }
   if (causal && di != fa::head_dim_index(128)) {
     const int64_t W = (N + 127) / 128 * BH;

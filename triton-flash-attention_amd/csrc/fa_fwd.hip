@@ -396,10 +396,10 @@ struct FwdPipeTile {
   static constexpr int NSTAGE = UPS == 2 ? 8 : 6;
   static constexpr int AHEAD = UPS == 2 ? 5 : 4;  // units issued before step 0
   // Work-groups per CU: three 4-wave work-groups with one unit per barrier,
-  // two with two; an 8-wave work-group (D = 128: 16 KiB units) takes a CU
-  // alone; with two key groups (two rings) two at D = 32 and one at D = 64.
+  // two with two; at D = 128 (16 KiB units, a 96 KiB ring) a work-group takes
+  // a CU alone; with two key groups (two rings) two at D = 32 and one at D = 64.
   static constexpr int WGS_PER_CU =
-      KG == 2 ? (D <= 32 ? 2 : 1) : (NW == 8 ? 1 : (UPS == 2 ? 2 : 3));
+      KG == 2 ? (D <= 32 ? 2 : 1) : (NW == 8 || D == 128 ? 1 : (UPS == 2 ? 2 : 3));
   static constexpr int WAVES_PER_SIMD = WGS_PER_CU * NW / 4;
   static_assert(UPS == 1 || UPS == 2, "units per step");
   static_assert(KG == 1 || (KG == 2 && UPS == 1 && NW == 8), "two 4-wave key groups, one unit each");
@@ -833,13 +833,15 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
   constexpr int NW = 4;
   using T = FwdPipeTile<D, NW, 1, 1>;
   using Dma = DmaStager<D, T::KT, NW>;
-  static_assert(Dma::PER_WAVE == 1, "one tile piece per wave");
-  static_assert(D == 32 || D == 64, "16x16x32 forward: D <= 64");
+  static_assert(Dma::PER_WAVE == 1 || Dma::PER_WAVE == 2, "one or two tile pieces per wave");
+  static_assert(D == 32 || D == 64 || (D == 128 && QB == 1),
+                "16x16x32 forward: D <= 64, and D = 128 with one query block per wave");
   static_assert(QB == 1 || QB == 2, "one or two 16-row query blocks per wave");
+  static_assert(T::WGS_PER_CU * T::NSTAGE * T::STAGE * 2 <= 160 * 1024, "ring fits the LDS");
   constexpr int BM = 4 * 16 * QB;  // query rows per work-group
   constexpr int NPAIR = 4 * QB;    // score value pairs per lane and unit
   constexpr int NS = T::NSTAGE;
-  constexpr int IPU = 2;   // this wave's DMA instructions per unit: K, V
+  constexpr int IPU = 2 * Dma::PER_WAVE;  // this wave's DMA instructions per unit: K, V
   constexpr int KD = D / 32;  // 32-wide d chunks: k-steps of S^T
   constexpr int DD = D / 16;  // 16-row d blocks of O^T
 
@@ -899,16 +901,36 @@ __device__ __forceinline__ void fwd_pipe16_body(const FwdArgs& a, int split, int
     const uint32_t vt = (uint32_t)row0 * (D * 2u) + dma.voff[0];
     const uint32_t base = lds0 + (uint32_t)slot * (T::STAGE * 2u) + (uint32_t)dma.piece0 * 1024u;
     uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %4\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-        "s_mov_b32 m0, %5\n\t"
-        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
-        : "memory");
+    if constexpr (Dma::PER_WAVE == 1) {
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %4\n\t"
+          "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+          "s_mov_b32 m0, %5\n\t"
+          "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(vt), "s"(r_k), "s"(r_v), "s"(base), "s"(base + T::TILE * 2u)
+          : "memory");
+    } else {
+      // D = 128: the wave's two consecutive 1 KiB pieces of the K and the V unit
+      const uint32_t vt1 = (uint32_t)row0 * (D * 2u) + dma.voff[1];
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %5\n\t"
+          "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %6\n\t"
+          "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+          "s_mov_b32 m0, %7\n\t"
+          "buffer_load_dwordx4 %1, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %8\n\t"
+          "buffer_load_dwordx4 %2, %4, 0 offen lds\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(vt), "v"(vt1), "s"(r_k), "s"(r_v), "s"(base), "s"(base + 1024u),
+            "s"(base + T::TILE * 2u), "s"(base + T::TILE * 2u + 1024u)
+          : "memory");
+    }
     i_row += T::KT;
   };
 #pragma unroll
@@ -1364,10 +1386,11 @@ constexpr void* fwd_pipe16_entry() {
     return nullptr;
 }
 
-// The same with one 16-row query block per wave (64 queries per work-group).
+// The same with one 16-row query block per wave (64 queries per work-group);
+// also at D = 128, where a work-group takes a CU alone (a 96 KiB ring).
 template <int D, bool CAUSAL, int NW, int UPS, class E = F16>
 constexpr void* fwd_pipe16_half_entry() {
-  if constexpr (D <= 64 && NW == 4 && UPS == 1 && fwd_pipe_tiling_ok<D, 4, 1>())
+  if constexpr (NW == 4 && UPS == 1 && (D == 128 || fwd_pipe_tiling_ok<D, 4, 1>()))
     return (void*)&fwd_pipe16_launch<D, CAUSAL, E, 1>;
   else
     return nullptr;

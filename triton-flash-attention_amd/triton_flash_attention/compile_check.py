@@ -33,8 +33,9 @@ SUPPORTED_ARCHS = ("gfx950",)
 # mask modes and both element types (at D = 128 the forward takes the 8-wave
 # pipelined kernel, and the 4-wave one for short queries; at D = 32 causal
 # launches over few heads take the two-key-group forward, and the other causal
-# launches from 512 queries its 16x16x32 form; small causal launches at D <= 64
-# the 16x16x32 form with 64-query work-groups; at D <= 64 a backward
+# launches from 512 queries its 16x16x32 form; small causal launches at D <= 64,
+# and decoding at every head size, the 16x16x32 form with 64-query work-groups;
+# at D <= 64 a backward
 # whose dK/dV launch splits next to a short dQ launch runs the combined dK/dV + dQ
 # kernel; dQ takes the pipelined kernel at D = 128 for short causal launches, and
 # dQ and dK/dV their 16x16x32 forms at D = 64 and, without the mask, D = 32).
@@ -65,7 +66,8 @@ def _defaults() -> tuple[str, ...]:
                 names += [f"fa::dq_pipe16_kernel<64, true, 4, {e}, {t}>" for t in ("false", "true")]
         names.append(f"fa::fwd_pipe_kernel<32, true, 8, 1, {e}, 2>")
         names.append(f"fa::fwd_pipe16_kernel<32, true, {e}, 2>")
-        names += [f"fa::fwd_pipe16_kernel<{d}, true, {e}, 1>" for d in (32, 64)]
+        names += [f"fa::fwd_pipe16_kernel<{d}, {c}, {e}, 1>"
+                  for d in (32, 64, 128) for c in ("false", "true")]
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
     return tuple(names)
