@@ -80,7 +80,9 @@ int override_of(int kind, int di, int causal) {
 //         run as a persistent grid of bin-packed jobs under the causal mask when
 //         its job plan beats the grid's modelled tail (D <= 64; fwd_launch_plan;
 //         measured slower than 6 at every shape where a plan forms, so the table
-//         does not take it)
+//         does not take it); 10 = tiling 6 on 16x16x32 MFMAs (D <= 64); 11 = 10
+//         with 64-query work-groups (all D; select_fwd takes it for small causal
+//         launches at D <= 64 and for decoding)
 //         (not every variant exists for every D)
 //   dkdv: 0 = 4 waves x 32 keys, 64-query tiles; 1 = 4 waves, 32; 2 = 2 waves, 64;
 //         3 = 8 waves, 64; 4 = 4 waves, 32-query units, software-pipelined (all D;

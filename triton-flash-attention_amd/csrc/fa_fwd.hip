@@ -808,11 +808,13 @@ __device__ __forceinline__ void fwd_pipe_body(const FwdArgs& a, int split, int q
 
 // --------------------------------------------------------------------------
 // The pipelined forward of tiling 6 (4 waves, 32-key units, one unit per
-// barrier, a 6-slot ring, three work-groups per CU) on 16x16x32 MFMAs
-// (D <= 64), with QB 16-row query blocks per wave: QB = 2 is tiling 6's
+// barrier, a 6-slot ring, three work-groups per CU at D <= 64) on 16x16x32
+// MFMAs, with QB 16-row query blocks per wave: QB = 2 is tiling 6's
 // 32 queries per wave (tiling 10), QB = 1 halves the work-group to 64
 // queries (tiling 11: twice the work-groups and half the work per unit, for
-// launches too small to fill the GPU, whose time is their longest key loop).
+// launches too small to fill the GPU, whose time is their longest key loop,
+// and for decoding; at D = 128 too, with two DMA pieces per wave and a 96 KiB
+// ring, one work-group per CU).
 // Each 32-key unit against a query block is two 16 x 16 score blocks (key
 // block kb); each K row read and each transposed V read from LDS feeds QB
 // MFMAs, so with QB = 2 LDS traffic, vector work and FLOP are tiling 6's.
@@ -1544,7 +1546,8 @@ static const Variant kFwdVariants[] = {
     // 10: tiling 6 on 16x16x32 MFMAs (D <= 64)
     {4, 128, 32, {FA_ENTRIES(fwd_pipe16_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe16_entry, BF16, 4, 1)},
      kSplitsKv},
-    // 11: tiling 10 with one 16-row query block per wave, 64 queries per work-group (D <= 64)
+    // 11: tiling 10 with one 16-row query block per wave, 64 queries per work-group
+    // (all D; at D = 128 one work-group per CU)
     {4, 64, 32,
      {FA_ENTRIES(fwd_pipe16_half_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe16_half_entry, BF16, 4, 1)},
      kSplitsKv},
