@@ -441,6 +441,17 @@ int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, i
 // ones (partials and merge cost more than the extra parallelism returns).
 constexpr int64_t kFwdSplitBelowWorkgroups = 512;
 constexpr int64_t kFwdSplitTargetWorkgroups = 768;
+// The 64-query forward (kFewSplits) decodes at D >= 64 faster with one
+// work-group per CU than with three: its key ranges run quicker, so partials
+// and the merge weigh more, and at D = 128 one work-group fills a CU (MI355X,
+// interleaved, targets 768 vs 256, us: B32 Hq32 Hkv8 1 query against 2048
+// keys D128 45.4 / 42.3 (no split, no merge), B8 Hq32 Hkv8 16 queries against
+// 8192 keys 51.4 / 49.1, B2 Hq32 Hkv32 1 query against 16384 keys 98.6 / 93.7,
+// B4 Hq16 Hkv16 1 query against 16384 keys D64 47.9 / 43.1; B8 Hq32 Hkv8 1
+// query against 8192 keys D128 45.0 / 46.6; 384 is worse than both: 1.5
+// rounds of work-groups). At D = 32 (half the bytes per key) three stay
+// faster (16.2 vs 21.4 us at B8 Hq32 Hkv8 against 8192 keys).
+constexpr int64_t kFwdSplitTargetFew = 256;
 constexpr int64_t kFwdMinSplitKeys = 1024;
 constexpr int kMaxFwdSplit = 32;
 
@@ -457,11 +468,13 @@ int fwd_pack(const fa::Variant& var, int64_t group, int64_t N) {
   return (int)std::gcd<int64_t>(group, var.waves);
 }
 
-// Key split of a launch of `wgs` work-groups over Nkv keys (forward and dQ).
-FwdSplit key_split(int64_t wgs, int64_t Nkv, bool can_split) {
+// Key split of a launch of `wgs` work-groups over Nkv keys (forward and dQ),
+// aiming at about `target` work-groups.
+FwdSplit key_split(int64_t wgs, int64_t Nkv, bool can_split,
+                   int64_t target = kFwdSplitTargetWorkgroups) {
   const int whole = (int)((Nkv + 127) / 128 * 128);
   if (wgs >= kFwdSplitBelowWorkgroups || !can_split) return {1, whole};
-  int64_t s = (kFwdSplitTargetWorkgroups + wgs - 1) / wgs;
+  int64_t s = (target + wgs - 1) / wgs;
   s = std::min<int64_t>(s, std::max<int64_t>(1, Nkv / kFwdMinSplitKeys));
   s = std::min<int64_t>(s, kMaxFwdSplit);
   if (s <= 1) return {1, whole};
@@ -470,9 +483,11 @@ FwdSplit key_split(int64_t wgs, int64_t Nkv, bool can_split) {
 }
 
 FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv,
-                   int pack) {
+                   int64_t D, int pack) {
   const int64_t rows = var.rows / pack;  // query rows per head and work-group
-  return key_split((N + rows - 1) / rows * B * Hq / pack, Nkv, var.flags & fa::kSplitsKv);
+  const int64_t target = (var.flags & fa::kFewSplits) && D >= 64 ? kFwdSplitTargetFew
+                                                                : kFwdSplitTargetWorkgroups;
+  return key_split((N + rows - 1) / rows * B * Hq / pack, Nkv, var.flags & fa::kSplitsKv, target);
 }
 
 // dQ: the same split of its key loop; the partials (fp32 dQ) are summed.
@@ -698,7 +713,7 @@ static int fwd_check(int dt, const char* name, const fa_half_t* q, const fa_half
   if ((rc = check_scale(scale))) return rc;
   *var = select_fwd(fa::head_dim_index(D), causal, N, B * Hq, Hq / Hkv, dt);
   if (!*var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-  const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, fwd_pack(**var, Hq / Hkv, N));
+  const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, D, fwd_pack(**var, Hq / Hkv, N));
   *need = fwd_workspace_bytes(sp, B, Hq, N, D);
   return FA_OK;
 }
@@ -728,7 +743,7 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   hipStream_t s = static_cast<hipStream_t>(stream);
   a.pack = fwd_pack(*var, Hq / Hkv, N);
-  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv, a.pack);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv, D, a.pack);
   a.nsplit = 1;
   a.split_keys = (int)((Nkv + 127) / 128 * 128);
   a.part = nullptr;
@@ -760,7 +775,7 @@ int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, 
   for (int dt : {fa::kF16, fa::kBF16}) {
     const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, Hq / Hkv, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_workspace_bytes: no kernel for the selected tiling");
-    const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, fwd_pack(*var, Hq / Hkv, N_q));
+    const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, D, fwd_pack(*var, Hq / Hkv, N_q));
     bytes = std::max(bytes, fwd_workspace_bytes(sp, B, Hq, N_q, D));
   }
   return bytes;
@@ -775,7 +790,7 @@ int fa_fwd_plan_info(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_
   const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, Hq / Hkv, fa::kF16);
   if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_plan_info: no kernel for the selected tiling");
   const int pack = fwd_pack(*var, Hq / Hkv, N_q);
-  const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, pack);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, D, pack);
   const int64_t grid_wgs = (N_q + var->rows / pack - 1) / (var->rows / pack) * (B * Hq / pack);
   const auto plan = fwd_launch_plan(*var, causal, pack, sp.nsplit, B * Hq, N_q, N_kv,
                                     compute_units);

@@ -1550,7 +1550,7 @@ static const Variant kFwdVariants[] = {
     // (all D; at D = 128 one work-group per CU)
     {4, 64, 32,
      {FA_ENTRIES(fwd_pipe16_half_entry, F16, 4, 1), FA_ENTRIES(fwd_pipe16_half_entry, BF16, 4, 1)},
-     kSplitsKv},
+     kSplitsKv | kFewSplits},
 };
 
 const Variant* fwd_variants(int* count) {

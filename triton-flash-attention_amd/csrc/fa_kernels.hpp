@@ -110,7 +110,7 @@ struct Variant {
   int rows;
   int tile;
   void* fn[2][3][2];  // [element type: fp16, bf16][D index: 32, 64, 128][causal]; null = not compiled
-  int flags;          // kFusesDelta, kSplitsKv, kPairs, kKeyGroups, kJobs
+  int flags;          // kFusesDelta, kSplitsKv, kPairs, kKeyGroups, kJobs, kFewSplits
   int per_cu = 0;     // kJobs: work-groups resident per CU (the plan's slots per CU)
 };
 
@@ -138,6 +138,9 @@ constexpr int kKeyGroups = 8;
 // The forward variant runs a causal one-pass launch as a persistent grid when
 // the host attaches a job plan (FwdArgs::jobs), else as the grid form.
 constexpr int kJobs = 16;
+// The forward variant's split-KV launches at D >= 64 aim at one work-group per
+// CU (fewer, longer key ranges) instead of three.
+constexpr int kFewSplits = 32;
 
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);
