@@ -453,7 +453,7 @@ constexpr int64_t kFwdSplitTargetWorkgroups = 768;
 // faster (16.2 vs 21.4 us at B8 Hq32 Hkv8 against 8192 keys).
 constexpr int64_t kFwdSplitTargetFew = 256;
 constexpr int64_t kFwdMinSplitKeys = 1024;
-constexpr int kMaxFwdSplit = 32;
+constexpr int kMaxFwdSplit = fa::kMaxFwdSplitKv;
 
 struct FwdSplit {
   int nsplit;

@@ -1438,7 +1438,11 @@ hipError_t fwd_launch(const FwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Merge of the split-KV partials: one thread per 4 columns of a query row.
+// Merge of the split-KV partials: one thread per 4 columns of a query row. All
+// of a row's partials (at most kMaxFwdSplitKv) are loaded at once, so the merge
+// waits on one round of load latency rather than one per split; the max, the
+// weights and the weighted sum then run in split order (the summation order
+// is fixed).
 template <int D, class E>
 __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restrict__ part,
                                                           half_t* __restrict__ o,
@@ -1450,22 +1454,29 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const float* __restric
   const int64_t row = i / CPR;
   const int c = (int)(i - row * CPR);
   const float* plse = part + (int64_t)nsplit * rows * D;
-  // Unrolled so that several splits' loads are in flight at once (the loop is
-  // a chain of dependent-latency loads otherwise); the summation order is fixed.
+  float ls[kMaxFwdSplitKv];
+  float4v v[kMaxFwdSplitKv];
+#pragma unroll
+  for (int sp = 0; sp < kMaxFwdSplitKv; ++sp) {
+    if (sp < nsplit) {
+      ls[sp] = plse[(int64_t)sp * rows + row];
+      v[sp] = *reinterpret_cast<const float4v*>(part + ((int64_t)sp * rows + row) * D + 4 * c);
+    }
+  }
   float mx = -INFINITY;
-#pragma unroll 8
-  for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, plse[(int64_t)sp * rows + row]);
+#pragma unroll
+  for (int sp = 0; sp < kMaxFwdSplitKv; ++sp)
+    if (sp < nsplit) mx = fmaxf(mx, ls[sp]);
   float wsum = 0.f;
   float4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-  for (int sp = 0; sp < nsplit; ++sp) {
-    const float ls = plse[(int64_t)sp * rows + row];
-    const float w = ls == -INFINITY ? 0.f : exp2_fast(ls - mx);
-    wsum += w;
-    const float4v v =
-        *reinterpret_cast<const float4v*>(part + ((int64_t)sp * rows + row) * D + 4 * c);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = fmaf(w, v[e], acc[e]);
+  for (int sp = 0; sp < kMaxFwdSplitKv; ++sp) {
+    if (sp < nsplit) {
+      const float w = ls[sp] == -INFINITY ? 0.f : exp2_fast(ls[sp] - mx);
+      wsum += w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(w, v[sp][e], acc[e]);
+    }
   }
   const float inv = 1.0f / wsum;
   half4 h;
@@ -1479,7 +1490,8 @@ template <int D, class E>
 hipError_t fwd_combine_launch(const float* part, half_t* o, float* lse, int64_t rows, int nsplit,
                               hipStream_t stream) {
   const int64_t blocks = (rows * (D / 4) + 255) / 256;
-  if (nsplit < 2 || blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+  if (nsplit < 2 || nsplit > kMaxFwdSplitKv || blocks <= 0 || blocks > 0x7fffffff)
+    return hipErrorInvalidValue;
   hipLaunchKernelGGL((fwd_combine_kernel<D, E>), dim3((unsigned)blocks), dim3(256), 0, stream,
                      part, o, lse, rows, nsplit);
   return hipGetLastError();

@@ -142,6 +142,10 @@ constexpr int kJobs = 16;
 // CU (fewer, longer key ranges) instead of three.
 constexpr int kFewSplits = 32;
 
+// Most key ranges a split-KV forward uses; its merge holds one partial per
+// range in registers.
+constexpr int kMaxFwdSplitKv = 32;
+
 // Registries defined in the kernel translation units.
 const Variant* fwd_variants(int* count);
 const Variant* dkdv_variants(int* count);
