@@ -138,7 +138,7 @@ def test_cross_attention_flops_count_top_left_visible_pairs() -> None:
 def test_tiling_ab_parses_shapes_and_rejects_bad_arguments() -> None:
     import pytest
 
-    from benchmarks.tiling_ab import main, parse_shape
+    from benchmarks.tiling_ab import label, main, parse_shape, parse_variants
 
     assert parse_shape("4,16,16,4096,64,causal") == {
         "B": 4, "Hq": 16, "Hkv": 16, "N": 4096, "Nkv": 4096, "D": 64, "causal": True,
@@ -156,3 +156,11 @@ def test_tiling_ab_parses_shapes_and_rejects_bad_arguments() -> None:
         main(["--kernel", "fwd", "--variants", "6,6", "--shape", "1,1,1,64,64,causal"])
     with pytest.raises(SystemExit):
         main(["--kernel", "fwd", "--variants", "6,10", "--shape", "1,1,1,64,65,causal"])
+    # auto is the library's own choice (no tiling set: -1); it counts as one tiling
+    assert parse_variants("auto, 4,1") == [-1, 4, 1]
+    assert [label(v) for v in (-1, 0, 5)] == ["auto", "0", "5"]
+    for bad in ("-2,4", "four,4"):
+        with pytest.raises(ValueError):
+            parse_variants(bad)
+    with pytest.raises(SystemExit):
+        main(["--kernel", "dq", "--variants", "auto,auto", "--shape", "1,1,1,64,64,causal"])

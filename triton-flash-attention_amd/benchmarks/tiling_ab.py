@@ -16,8 +16,9 @@ A shape is ``B,Hq,Hkv,N,D,mask[,dtype[,N_kv]]`` with mask ``causal`` or
 ``noncausal``, dtype ``float16`` (default) or ``bfloat16``, and N_kv keys
 (default N; decoding shapes have few queries against many keys). A tiling with no
 build for the shape's head size or dtype runs the table's tiling
-(``fa_set_tiling``), so name compiled ones (``tiling_sweep`` lists them). The
-table is restored afterwards, also after an error.
+(``fa_set_tiling``), so name compiled ones (``tiling_sweep`` lists them). ``auto``
+names the library's own choice (the table and its shape rules, as with no tiling
+set). The table is restored afterwards, also after an error.
 """
 
 from __future__ import annotations
@@ -52,9 +53,28 @@ def parse_shape(text: str) -> dict[str, Any]:
             "dtype": dtype}
 
 
+def label(variant: int) -> str:
+    return "auto" if variant < 0 else str(variant)
+
+
+def parse_variants(text: str) -> list[int]:
+    """Comma-separated tiling indices; ``auto`` (-1) is the library's own choice."""
+    out = []
+    for x in (t.strip() for t in text.split(",")):
+        if not x:
+            continue
+        v = -1 if x == "auto" else int(x)
+        if v < -1:
+            raise ValueError(f"tiling {x!r}: an index >= 0 or auto")
+        out.append(v)
+    return out
+
+
 def ab(kernel: str, variants: list[int], shape: dict[str, Any], rounds: int = 7,
        reps: int = 20, seed: int = 1) -> dict[str, Any]:
-    """Medians (µs) of each tiling over interleaved rounds, and ratios to the first."""
+    """Medians (µs) of each tiling over interleaved rounds, and ratios to the first.
+
+    A variant of -1 runs with no tiling set: the library's table and shape rules."""
     B, Hq, Hkv, N, D, causal = (shape[k] for k in ("B", "Hq", "Hkv", "N", "D", "causal"))
     Nkv = shape.get("Nkv", N)
     dtype = getattr(torch, shape["dtype"])
@@ -91,15 +111,16 @@ def ab(kernel: str, variants: list[int], shape: dict[str, Any], rounds: int = 7,
     med = {var: statistics.median(t) for var, t in times.items()}
     first = variants[0]
     return {"kernel": kernel, **shape,
-            "us": {str(var): round(m, 1) for var, m in med.items()},
-            "ratio": {str(var): round(m / med[first], 3) for var, m in med.items()}}
+            "us": {label(var): round(m, 1) for var, m in med.items()},
+            "ratio": {label(var): round(m / med[first], 3) for var, m in med.items()}}
 
 
 def main(argv: list[str] | None = None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--kernel", choices=tuple(KERNELS), required=True)
     parser.add_argument("--variants", required=True,
-                        help="comma-separated tiling indices (two or more)")
+                        help="comma-separated tiling indices (two or more); auto = the "
+                             "library's own choice")
     parser.add_argument("--shape", action="append", required=True,
                         help="B,Hq,Hkv,N,D,mask[,dtype[,N_kv]]; repeat for more shapes")
     parser.add_argument("--rounds", type=int, default=7)
@@ -107,7 +128,7 @@ def main(argv: list[str] | None = None) -> int:
     parser.add_argument("--markdown", action="store_true", help="also print a table")
     args = parser.parse_args(argv)
     try:
-        variants = [int(x) for x in args.variants.split(",") if x.strip()]
+        variants = parse_variants(args.variants)
         shapes = [parse_shape(s) for s in args.shape]
     except ValueError as e:
         raise SystemExit(str(e))
@@ -122,15 +143,16 @@ def main(argv: list[str] | None = None) -> int:
         rows.append(ab(args.kernel, variants, shape, args.rounds, args.reps))
         print(json.dumps(rows[-1]), flush=True)
     if args.markdown:
-        cols = " | ".join(f"tiling {v} µs" for v in variants)
-        print(f"| shape | {cols} | " + " | ".join(f"{v} / {variants[0]}" for v in variants[1:]) + " |")
+        cols = " | ".join(f"tiling {label(v)} µs" for v in variants)
+        print(f"| shape | {cols} | "
+              + " | ".join(f"{label(v)} / {label(variants[0])}" for v in variants[1:]) + " |")
         print("|---|" + "---:|" * (2 * len(variants) - 1))
         for r in rows:
             kv = f" N_kv{r['Nkv']}" if r["Nkv"] != r["N"] else ""
             name = (f"B{r['B']} Hq{r['Hq']} Hkv{r['Hkv']} N{r['N']}{kv} D{r['D']} "
                     f"{'causal' if r['causal'] else 'bidirectional'} {r['dtype']}")
-            us = " | ".join(str(r["us"][str(v)]) for v in variants)
-            ratios = " | ".join(f"{r['ratio'][str(v)]:.3f}" for v in variants[1:])
+            us = " | ".join(str(r["us"][label(v)]) for v in variants)
+            ratios = " | ".join(f"{r['ratio'][label(v)]:.3f}" for v in variants[1:])
             print(f"| {name} | {us} | {ratios} |")
     return 0
 

@@ -835,6 +835,29 @@ __device__ __forceinline__ void dq_pipe_body(const BwdArgs& a, const unsigned bl
   constexpr int kInFlight = (T::AHEAD - 3) * IPU;
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(kInFlight) : "memory");
 
+  // A wave whose 32 queries are all past N (in the last query tile, or in a
+  // launch of few queries) has no dQ row to produce. It still issues its
+  // share of every unit's loads and meets every barrier, exactly as the steps
+  // below do (same slots, same order, same waits), but runs no body and
+  // stores nothing: 3 of the 4 waves at 16 queries.
+  if (q0w >= N) {
+    auto idle_step = [&](auto p_c) __attribute__((always_inline)) {
+      constexpr int P = decltype(p_c)::value;
+      issue((2 * P + T::AHEAD) % NS);
+      issue((2 * P + T::AHEAD + 1) % NS);
+      wait_vm_and_barrier<kInFlight>();
+    };
+    if (npad > 0) {
+      bwd_static_for<0, NS / 2>([&](auto p_c) {
+        if (decltype(p_c)::value >= p0) idle_step(p_c);
+      });
+      for (int u = NS; u < npad; u += NS)
+        bwd_static_for<0, NS / 2>([&](auto p_c) { idle_step(p_c); });
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+
   int r_off[D / 16];  // row reads: row row_perm(ql), chunk 2*kk + g
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk) r_off[kk] = swz_offset<D>(row_perm(ql), 2 * kk + g);
