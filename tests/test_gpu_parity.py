@@ -541,6 +541,42 @@ def test_short_query_dq_rule_matches_oracle_and_the_pipelined_tiling():
         torch.testing.assert_close(delta_rule, delta_pipe, rtol=1e-5, atol=1e-5, msg=tag)
 
 
+@pytest.mark.parametrize("head_dim", [32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+def test_pipelined_dq_waves_without_queries_match_oracle(head_dim, causal):
+    """The pipelined dQ tilings (4, and its 16x16x32 form 5) with waves that own
+    no query row: 16, 40 and 96 queries leave 3, 2 and 1 of a 128-row
+    work-group's four 32-row waves empty. Those waves only feed the shared K/V
+    ring. dQ and Delta against the oracle, in split mode (16 and 96 queries
+    against 4096 and 2500 keys) and in one pass (40 against 300), and the two
+    tilings against each other."""
+    scale = head_dim ** -0.5
+    for B, Hq, Hkv, N, Nkv in ((1, 4, 1, 16, 4096), (2, 4, 2, 40, 300), (1, 2, 1, 96, 2500)):
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, head_dim, seed=3 * N + Nkv, mult=0.5, n_kv=Nkv)
+        qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+        o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
+        torch.cuda.synchronize()
+        ref = oracle.attention(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal, scale,
+                               o16=o.cpu().numpy(), fold_bwd=True)
+        got = {}
+        for var in (4, 5):
+            tag = f"dq variant {var} B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} D={head_dim} " \
+                  f"causal={causal}"
+            _note(tag)
+            _lib.set_tiling(_lib.KERNEL_DQ, head_dim, causal, var)
+            try:
+                delta, dq = _ops.flash_bwd_dq_delta(qd, kd, vd, o, dod, lse, causal, scale)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_DQ, head_dim, causal, -1)
+            torch.cuda.synchronize()
+            assert_close(tag, dq.double().cpu().numpy(), ref["dq"])
+            d_err = float(np.max(np.abs(delta.double().cpu().numpy() - ref["delta"])))
+            assert d_err <= 1e-4, f"{tag} delta {d_err:.3e}"
+            got[var] = dq
+        assert_close(f"D={head_dim} N_q={N} dq variant 4 vs 5", got[4].float(), got[5].float(),
+                     max_abs=2e-3, rel_l2=1e-3)
+
+
 def test_causal_dq_rule_at_d128_matches_oracle_and_the_classic_tiling():
     """dQ at D = 128 under the mask runs the pipelined tiling for launches of at
     most 768 work-groups of 128 queries (a shape rule over the table's classic

@@ -190,6 +190,28 @@ __device__ __forceinline__ void dq_pipe16_body(const BwdArgs& a, const unsigned 
   constexpr int kInFlight = (T::AHEAD - 3) * IPU;
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(kInFlight) : "memory");
 
+  // A wave whose 32 queries are all past N has no dQ row to produce: it keeps
+  // issuing its share of the ring's loads and meets every barrier, exactly as
+  // the steps below do, but runs no body and stores nothing (as in
+  // dq_pipe_body).
+  if (q0w >= N) {
+    auto idle_step = [&](auto p_c) __attribute__((always_inline)) {
+      constexpr int P = decltype(p_c)::value;
+      issue((2 * P + T::AHEAD) % NS);
+      issue((2 * P + T::AHEAD + 1) % NS);
+      wait_vm_and_barrier<kInFlight>();
+    };
+    if (npad > 0) {
+      bwd_static_for<0, NS / 2>([&](auto p_c) {
+        if (decltype(p_c)::value >= p0) idle_step(p_c);
+      });
+      for (int u = NS; u < npad; u += NS)
+        bwd_static_for<0, NS / 2>([&](auto p_c) { idle_step(p_c); });
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+
   // Row reads of K and V (A operands of S^T and dP^T): key row 16 kb + c16,
   // 16-byte chunk 4 kd + sg.
   int r_off[2][KD];
