@@ -40,6 +40,24 @@ def test_resource_report_parsing():
     assert "fa::dkdv_pipe_kernel<64, true, 4, fa::BF16>" in missing
 
 
+def test_spill_allowance_is_per_kernel_and_capped():
+    """A default kernel listed in ALLOWED_SPILLS may spill up to its measured
+    bytes per lane and no more; every other default kernel may not spill."""
+    name, cap = next(iter(compile_check.ALLOWED_SPILLS.items()))
+    assert name in compile_check.DEFAULT_KERNELS
+    other = "fa::dq_kernel<128, false, 4, 32, fa::F16>"
+    assert other in compile_check.DEFAULT_KERNELS and other not in compile_check.ALLOWED_SPILLS
+
+    def spills(scratch_of):
+        ks = [compile_check.KernelUsage(name=f"{n}(fa::BwdArgs)", scratch=scratch_of.get(n, 0))
+              for n in compile_check.DEFAULT_KERNELS]
+        return [k.name.split("(")[0] for k in compile_check.spilling_defaults(ks)[0]]
+
+    assert spills({name: cap}) == []
+    assert spills({name: cap + 4}) == [name]
+    assert spills({other: 4}) == [other]
+
+
 def test_fallback_names_for_undemangled_kernels():
     assert compile_check._short_name("_ZN2fa17preprocess_kernelILi128ENS_4BF16EEEvPKDF16_S3_Pfl") == \
         "fa::preprocess_kernel<128, fa::BF16>(...)"

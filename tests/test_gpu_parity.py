@@ -541,6 +541,53 @@ def test_short_query_dq_rule_matches_oracle_and_the_pipelined_tiling():
         torch.testing.assert_close(delta_rule, delta_pipe, rtol=1e-5, atol=1e-5, msg=tag)
 
 
+def test_short_query_dkdv_rule_at_d128_runs_the_classic_tiling():
+    """dK/dV at D = 128 without the mask runs the classic 4 x 32 tiling (at two
+    waves per SIMD) for at most 128 queries: the public API's dK, dV agree with
+    the oracle, the op layer's are bit-identical to that tiling forced by
+    fa_set_tiling (the table's pipelined tiling 4 past 128 queries, under the
+    mask and in bf16) and agree with the other to fp32 summation order, and the
+    whole backward (fa_bwd) gives the same. One pass and split launches (bf16
+    has no build of the classic tiling: forcing it runs the table's)."""
+    cases = [(8, 32, 8, 16, 2048, False, torch.float16, True),  # 1024 key tiles: one pass
+             (2, 8, 2, 100, 700, False, torch.float16, True),
+             (1, 32, 1, 128, 600, False, torch.float16, True),  # 5 key tiles: 4 chunks
+             (1, 8, 8, 128, 1500, False, torch.float16, True),
+             (1, 8, 2, 129, 1000, False, torch.float16, False),
+             (2, 8, 2, 64, 900, True, torch.float16, False),
+             (2, 8, 2, 64, 900, False, torch.bfloat16, False)]
+    for (B, Hq, Hkv, N, Nkv, causal, dtype, takes) in cases:
+        D = 128
+        tag = f"short-query dkdv rule B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} causal={causal} {dtype}"
+        _note(tag)
+        q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + Nkv, mult=0.5, n_kv=Nkv, dtype=dtype)
+        if dtype == torch.float16:
+            check_against_oracle(run_kernel(q, k, v, do, causal), q, k, v, do, causal, tag=tag)
+        qd, kd, vd, dod = (t.to(DEV) for t in (q, k, v, do))
+        scale = D ** -0.5
+        o, lse = _ops.flash_fwd(qd, kd, vd, causal, scale)
+        delta = _ops.flash_bwd_preprocess(o, dod)
+        rule = _ops.flash_bwd_dkdv(qd, kd, vd, dod, lse, delta, causal, scale)
+        whole = _ops.flash_bwd(qd, kd, vd, o, lse, dod, causal, scale)
+        forced = {}
+        for variant in (1, 4):
+            _lib.set_tiling(_lib.KERNEL_DKDV, D, causal, variant)
+            try:
+                forced[variant] = _ops.flash_bwd_dkdv(qd, kd, vd, dod, lse, delta, causal, scale)
+            finally:
+                _lib.set_tiling(_lib.KERNEL_DKDV, D, causal, -1)
+        torch.cuda.synchronize()
+        same = forced[1] if takes else forced[4]
+        assert torch.equal(rule[0], same[0]) and torch.equal(rule[1], same[1]), tag
+        tol = dict(max_abs=2e-3, rel_l2=1e-3) if dtype == torch.float16 else \
+            dict(max_abs=1e-2, rel_l2=4e-3)
+        for i, name in ((0, "dk"), (1, "dv")):
+            assert_close(f"{tag} {name} classic vs pipelined", forced[1][i].float(),
+                         forced[4][i].float(), **tol)
+            assert_close(f"{tag} {name} whole backward", whole[i + 1].float(), rule[i].float(),
+                         **tol)
+
+
 @pytest.mark.parametrize("head_dim", [32, 64])
 @pytest.mark.parametrize("causal", [False, True])
 def test_pipelined_dq_waves_without_queries_match_oracle(head_dim, causal):

@@ -191,8 +191,16 @@ constexpr bool dkdv_tiling_ok() {
          3 * (2 * QT * D + 256) * 2 <= 160 * 1024;
 }
 
+// Waves per SIMD the classic dK/dV asks the compiler for.
+template <int D, bool CAUSAL, int NW, int QT>
+constexpr int dkdv_classic_waves_per_simd() {
+  return D == 128 && !CAUSAL && NW == 4 && QT == 32 ? 2 : 1;
+}
+
 template <int D, bool CAUSAL, int NW, int QT, class E = F16>
-__global__ __launch_bounds__(64 * NW) void dkdv_kernel(BwdArgs a) {
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(dkdv_classic_waves_per_simd<D, CAUSAL, NW, QT>())))
+void dkdv_kernel(BwdArgs a) {
   using T = DkdvTile<D, NW, QT>;
   using Dma = DmaStager<D, QT, NW>;
   constexpr int NB = QT / 32;                 // 32-query blocks per tile

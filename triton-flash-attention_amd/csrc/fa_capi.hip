@@ -185,7 +185,6 @@ const fa::Variant* select_dq(int di, int causal, int64_t N, int64_t BH, int dt) 
                       (N + 127) / 128 * BH >= kDq16MinWorkgroups;
     return take ? pick(kDq16Variant) : var;
   }
-  if (di != fa::head_dim_index(128)) return var;
   if (!causal) return N < 128 ? pick(kDqShortQueryVariant) : var;
   if (N >= 128 && (N + 127) / 128 * BH <= kDqPipelinedMaxWorkgroups)
     return pick(kDqPipelinedVariant);
@@ -415,18 +414,33 @@ int dkdv_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t Hkv, int64
 // to take). Launches that split keep tiling 4, whose body the combined dK/dV +
 // dQ launch also runs (B2 Hq16 Hkv4 N2049 causal, split, 61.7 vs 62.7).
 constexpr int kDkdv16Variant = 5;
+// Short-query launches at D = 128 without the mask (at most 128 queries: each
+// 128-key work-group sees only a few 32-query units, so its fixed cost of
+// loading K/V and storing dK/dV dominates) run the classic 4 waves x 32
+// tiling, which fits two waves per SIMD there (dkdv_classic_waves_per_simd,
+// fa_bwd.hip): two work-groups per CU overlap one's loads with the other's
+// work, where the pipelined kernel holds one. MI355X, one box, interleaved,
+// tiling 4 vs 1, us: B8 Hq32 Hkv8 N_q 16 N_kv 8192 238.4 vs 206.1; B4 Hq32
+// Hkv8 N_q 32 N_kv 8192 122.0 vs 103.9; B2 H16 N_q 64 N_kv 16384 214.3 vs
+// 185.1; B16 Hq32 Hkv8 N_q 4 N_kv 4096 234.2 vs 204.8; B1 Hq32 Hkv8 N_q 128
+// N_kv 32768 200.8 vs 195.3. Longer query loops favour the pipelined kernel:
+// B1 Hq32 Hkv8 N_q 512 N_kv 16384 280.0 vs 306.8, B2 H32 N 8192 4186 vs 4692.
+constexpr int kDkdvShortQueryVariant = 1;
+constexpr int64_t kDkdvShortQueryMax = 128;
 
 const fa::Variant* select_dkdv(int di, int causal, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
                                int64_t Nkv, int dt) {
   const int ov = override_of(fa::kDkdv, di, causal);
   const fa::Variant* var = select(fa::kDkdv, di, causal, ov, nullptr, dt);
   if (!var || ov >= 0) return var;
-  if (di != fa::head_dim_index(64) && (di != fa::head_dim_index(32) || causal)) return var;
-  if (dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal) != 1) return var;
   int count = 0;
   const fa::Variant* vs = registry(fa::kDkdv, &count);
-  return kDkdv16Variant < count && usable(vs[kDkdv16Variant], di, causal, dt) ? &vs[kDkdv16Variant]
-                                                                             : var;
+  auto pick = [&](int v) { return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var; };
+  if (di == fa::head_dim_index(128))
+    return !causal && N <= kDkdvShortQueryMax ? pick(kDkdvShortQueryVariant) : var;
+  if (di != fa::head_dim_index(64) && (di != fa::head_dim_index(32) || causal)) return var;
+  if (dkdv_split(*var, B, Hq, Hkv, N, Nkv, causal) != 1) return var;
+  return pick(kDkdv16Variant);
 }
 
 int64_t split_workspace_bytes(int nsplit, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D) {

@@ -38,7 +38,9 @@ SUPPORTED_ARCHS = ("gfx950",)
 # at D <= 64 a backward
 # whose dK/dV launch splits next to a short dQ launch runs the combined dK/dV + dQ
 # kernel; dQ takes the pipelined kernel at D = 128 for short causal launches, and
-# dQ and dK/dV their 16x16x32 forms at D = 64 and, without the mask, D = 32).
+# dQ and dK/dV their 16x16x32 forms at D = 64 and, without the mask, D = 32;
+# short-query launches at D = 128 without the mask run the classic 4 x 32 dQ
+# and dK/dV, fp16 only, as bf16 is built for the table's tilings).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
@@ -70,10 +72,17 @@ def _defaults() -> tuple[str, ...]:
                   for d in (32, 64, 128) for c in ("false", "true")]
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
+    names += ["fa::dq_kernel<128, false, 4, 32, fa::F16>", "fa::dkdv_kernel<128, false, 4, 32, fa::F16>"]
     return tuple(names)
 
 
 DEFAULT_KERNELS = _defaults()
+# Default kernels allowed a measured spill (bytes per lane, at most): the
+# short-query dK/dV at D = 128 asks for two waves per SIMD (256 registers) and
+# reloads two 16-byte values per 32-query unit; with them it is 13-15 % faster
+# than the pipelined kernel at one wave per SIMD for 4-64 queries (select_dkdv,
+# csrc/fa_capi.hip). Any other spill, or a larger one, fails --strict.
+ALLOWED_SPILLS = {"fa::dkdv_kernel<128, false, 4, 32, fa::F16>": 52}
 # The same table as (kernel kind, head_dim, causal) -> default variant index,
 # for the test that keeps this list in step with kDefault (kinds: 0 fwd,
 # 1 dK/dV, 2 dQ).
@@ -182,13 +191,14 @@ def compile_library(arch: str = "gfx950") -> tuple[list[KernelUsage], str]:
 
 
 def spilling_defaults(kernels: list[KernelUsage]) -> tuple[list[KernelUsage], list[str]]:
-    """(default kernels that use scratch, default kernels missing from the report)."""
+    """(default kernels that use scratch beyond ALLOWED_SPILLS, default kernels
+    missing from the report)."""
     spills, missing = [], []
     for prefix in DEFAULT_KERNELS:
         found = [k for k in kernels if k.name.startswith(prefix + "(")]
         if not found:
             missing.append(prefix)
-        spills += [k for k in found if k.scratch != 0]
+        spills += [k for k in found if k.scratch > ALLOWED_SPILLS.get(prefix, 0)]
     return spills, missing
 
 
@@ -217,7 +227,8 @@ def main(argv: list[str] | None = None) -> int:
         return 1
     print(f"compile check passed for {args.arch}: {len(kernels)} kernels (forward, preprocess, "
           f"dK/dV, dQ, split reduce; causal/bidirectional; D 32/64/128; MHA/GQA)"
-          + ("; no scratch in the default tilings" if args.strict else ""))
+          + ("; no scratch in the default tilings beyond the measured allowance"
+             if args.strict else ""))
     return 0
 
 
