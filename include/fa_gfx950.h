@@ -349,8 +349,7 @@ int fa_abi_version(void);
  * A dK/dV launch that does not split runs the pipelined tiling on 16x16x32
  * MFMAs (variant 5) at D = 64, and at D = 32 without the mask, unless a
  * tiling was set; at D = 128 without the mask, launches of at most 128
- * queries run the classic 4 x 32 tiling (variant 1, fp16; bf16 keeps the
- * table's).
+ * queries run the classic 4 x 32 tiling (variant 1).
  * Three shape rules refine the dQ entries unless a tiling was set: launches
  * of at least 769 work-groups of 128 queries run the pipelined tiling on
  * 16x16x32 MFMAs (variant 5) at D = 64, and at D = 32 without the mask; at

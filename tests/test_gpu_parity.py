@@ -545,17 +545,17 @@ def test_short_query_dkdv_rule_at_d128_runs_the_classic_tiling():
     """dK/dV at D = 128 without the mask runs the classic 4 x 32 tiling (at two
     waves per SIMD) for at most 128 queries: the public API's dK, dV agree with
     the oracle, the op layer's are bit-identical to that tiling forced by
-    fa_set_tiling (the table's pipelined tiling 4 past 128 queries, under the
-    mask and in bf16) and agree with the other to fp32 summation order, and the
-    whole backward (fa_bwd) gives the same. One pass and split launches (bf16
-    has no build of the classic tiling: forcing it runs the table's)."""
+    fa_set_tiling (the table's pipelined tiling 4 past 128 queries and under
+    the mask) and agree with the other to fp32 summation order, and the
+    whole backward (fa_bwd) gives the same. One pass and split launches, fp16
+    and bf16."""
     cases = [(8, 32, 8, 16, 2048, False, torch.float16, True),  # 1024 key tiles: one pass
              (2, 8, 2, 100, 700, False, torch.float16, True),
              (1, 32, 1, 128, 600, False, torch.float16, True),  # 5 key tiles: 4 chunks
              (1, 8, 8, 128, 1500, False, torch.float16, True),
              (1, 8, 2, 129, 1000, False, torch.float16, False),
              (2, 8, 2, 64, 900, True, torch.float16, False),
-             (2, 8, 2, 64, 900, False, torch.bfloat16, False)]
+             (2, 8, 2, 64, 900, False, torch.bfloat16, True)]
     for (B, Hq, Hkv, N, Nkv, causal, dtype, takes) in cases:
         D = 128
         tag = f"short-query dkdv rule B={B} Hq={Hq} Hkv={Hkv} N_q={N} N_kv={Nkv} causal={causal} {dtype}"

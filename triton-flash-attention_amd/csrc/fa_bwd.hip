@@ -870,7 +870,7 @@ constexpr void* dq_entry() {
 
 static const Variant kDkdvVariants[] = {
     FA_BWD_VARIANT(dkdv_entry, 4, 64, 0),
-    FA_BWD_VARIANT(dkdv_entry, 4, 32, 0),
+    FA_BWD_VARIANT_BF(dkdv_entry, 4, 32, 0),
     FA_BWD_VARIANT(dkdv_entry, 2, 64, 0),
     FA_BWD_VARIANT(dkdv_entry, 8, 64, 0),
     FA_BWD_VARIANT_BF(dkdv_pipe_entry, 4, 32, kPairs),

@@ -40,7 +40,7 @@ SUPPORTED_ARCHS = ("gfx950",)
 # kernel; dQ takes the pipelined kernel at D = 128 for short causal launches, and
 # dQ and dK/dV their 16x16x32 forms at D = 64 and, without the mask, D = 32;
 # short-query launches at D = 128 without the mask run the classic 4 x 32 dQ
-# and dK/dV, fp16 only, as bf16 is built for the table's tilings).
+# and dK/dV).
 def _defaults() -> tuple[str, ...]:
     names = []
     for e in ("fa::F16", "fa::BF16"):
@@ -72,7 +72,8 @@ def _defaults() -> tuple[str, ...]:
                   for d in (32, 64, 128) for c in ("false", "true")]
         names += [f"fa::preprocess_kernel<{d}, {e}>" for d in (32, 64, 128)]
         names.append(f"fa::split_reduce_kernel<{e}>")
-    names += ["fa::dq_kernel<128, false, 4, 32, fa::F16>", "fa::dkdv_kernel<128, false, 4, 32, fa::F16>"]
+    names += [f"fa::{k}_kernel<128, false, 4, 32, {e}>" for k in ("dq", "dkdv")
+              for e in ("fa::F16", "fa::BF16")]
     return tuple(names)
 
 
@@ -82,7 +83,7 @@ DEFAULT_KERNELS = _defaults()
 # reloads two 16-byte values per 32-query unit; with them it is 13-15 % faster
 # than the pipelined kernel at one wave per SIMD for 4-64 queries (select_dkdv,
 # csrc/fa_capi.hip). Any other spill, or a larger one, fails --strict.
-ALLOWED_SPILLS = {"fa::dkdv_kernel<128, false, 4, 32, fa::F16>": 52}
+ALLOWED_SPILLS = {f"fa::dkdv_kernel<128, false, 4, 32, {e}>": 52 for e in ("fa::F16", "fa::BF16")}
 # The same table as (kernel kind, head_dim, causal) -> default variant index,
 # for the test that keeps this list in step with kDefault (kinds: 0 fwd,
 # 1 dK/dV, 2 dQ).
