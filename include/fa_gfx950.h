@@ -365,7 +365,8 @@ int fa_abi_version(void);
  * the pipelined 16x16x32 tiling with 64-query work-groups (variant 11), and
  * so do launches of at most 32 queries (decoding, any head size) whose queries
  * fit one of its work-groups (at most 64 / P queries, P = gcd(Hq / Hkv, 4)
- * query heads packed per work-group), ahead of the D = 128 rule above;
+ * query heads packed per work-group), and launches of 33 to 64 queries
+ * without the mask, ahead of the D = 128 rule above;
  * otherwise at D = 32 under the mask,
  * launches over few heads (B * Hq * (query tiles of 128 + 1) < 1536) run the
  * two-key-group tiling (variant 8), and the other launches of at least 512

@@ -846,7 +846,9 @@ def test_decoding_forward_rule_runs_the_64_query_tiling():
     tiling 11 forced (past that bound to tiling 6, and at D = 128 to the
     4-wave tiling 2 that short queries take),
     tiling 11 agrees with 6 to fp32 summation order and, at a small shape,
-    matches the oracle. Split-KV (long keys) and packed GQA included."""
+    matches the oracle. Split-KV (long keys) and packed GQA included. Without
+    the mask 33-64 queries (one 64-query work-group per head, no packing) take
+    it too; under the mask they keep the previous choice."""
     for (B, Hq, Hkv, Nq, Nkv, D, dtype, expect) in [
             (8, 32, 8, 1, 8192, 64, torch.float16, 11),     # P = 4: up to 16 queries
             (8, 32, 8, 16, 8192, 64, torch.bfloat16, 11),
@@ -855,7 +857,12 @@ def test_decoding_forward_rule_runs_the_64_query_tiling():
             (2, 16, 16, 32, 16384, 64, torch.float16, 11),  # MHA, split keys
             (8, 32, 8, 1, 8192, 128, torch.float16, 11),    # D = 128: 96 KiB ring
             (4, 16, 16, 32, 4096, 128, torch.bfloat16, 11),
-            (8, 32, 8, 17, 8192, 128, torch.float16, 2)]:   # past the bound: short-query rule
+            (8, 32, 8, 17, 8192, 128, torch.float16, 2),    # past the bound: short-query rule
+            (8, 32, 8, 48, 8192, 64, torch.float16, 11),    # 33-64 queries: one work-group
+            (1, 32, 8, 64, 32768, 128, torch.bfloat16, 11),  # per head, split keys
+            (4, 16, 16, 40, 16384, 32, torch.float16, 11),
+            (8, 32, 8, 65, 8192, 64, torch.float16, 6),     # two query tiles per head
+            (4, 32, 8, 96, 8192, 128, torch.float16, 2)]:
         tag = f"decode rule B={B} Hq={Hq} Hkv={Hkv} N_q={Nq} N_kv={Nkv} D={D} {dtype}"
         print(tag, flush=True)
         q, k, v, _ = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, Nq, D, seed=Nq + Nkv + D,
@@ -883,6 +890,19 @@ def test_decoding_forward_rule_runs_the_64_query_tiling():
         q, k, v, do = make_inputs(2, 8, 2, 5, D, seed=6066 + D, n_kv=777)
         got = run_kernel(q, k, v, do, False)
         check_against_oracle(got, q, k, v, do, False, tag=f"decode B2 Hq8 Hkv2 N_q5 N_kv777 D{D}")
+    q, k, v, do = make_inputs(2, 8, 2, 50, 128, seed=6166, n_kv=900)
+    got = run_kernel(q, k, v, do, False)
+    check_against_oracle(got, q, k, v, do, False, tag="short queries B2 Hq8 Hkv2 N_q50 N_kv900 D128")
+    # under the mask 33-64 queries keep the 128-query tiling
+    q, k, v, _ = (t.to(DEV) for t in make_inputs(4, 16, 4, 48, 64, seed=48, n_kv=4096))
+    rule = _ops.flash_fwd(q, k, v, True, 0.125)
+    _lib.set_tiling(_lib.KERNEL_FWD, 64, True, 6)
+    try:
+        forced6 = _ops.flash_fwd(q, k, v, True, 0.125)
+    finally:
+        _lib.set_tiling(_lib.KERNEL_FWD, 64, True, -1)
+    torch.cuda.synchronize()
+    assert torch.equal(rule[0], forced6[0]) and torch.equal(rule[1], forced6[1])
 
 
 def test_forward_without_grad_matches_the_autograd_path():

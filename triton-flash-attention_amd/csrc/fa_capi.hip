@@ -246,6 +246,18 @@ constexpr int kFwd16HalfVariant = 11;
 // keys 31.4 / 27.2. With more queries than that (Hkv8 Nq 17, 32: two query
 // tiles per head, twice the K/V passes) 10-17 % slower at D = 64.
 constexpr int64_t kFwdDecodeQueries = 32;
+// Without the mask, 33-64 queries (no packing: one 64-query work-group per
+// head) take it as well; the 128-query tilings pad half or more of their rows.
+// MI355X, interleaved, library (tiling 2 at D = 128, 6 below) vs 11, us:
+// D = 128 B8 Hq32 Hkv8 against 8192 keys Nq 33 / 40 / 48 128.4 / 97.9,
+// 129.8 / 97.6, 133.4 / 97.2; B1 Hq32 Hkv8 Nq 64 against 32768 keys 74.4 /
+// 56.0 (bf16 74.8 / 56.2); B16 Hq32 Hkv8 Nq 64 against 4096 117.3 / 104.5;
+// B8 Hq32 Hkv32 Nq 64 221.4 / 184.4; B2 H16 Nq 48 against 16384 52.5 / 47.5;
+// D = 64 B16 Hq32 Hkv8 Nq 64 against 4096 70.0 / 50.5, B4 H16 Nq 40 against
+// 16384 48.9 / 43.4, B8 Hq32 Hkv8 Nq 64 73.1 / 69.3, Nq 48 73.2 / 75.6;
+// D = 32 B8 Hq32 Hkv8 Nq 48 / 64 59.3 / 39.4, 54.7 / 38.4. From 96 queries
+// (two work-groups per head) 13-17 % slower; with 128 a tie.
+constexpr int64_t kFwdShortQueries = 64;
 
 int fwd_pack(const fa::Variant& var, int64_t group, int64_t N);  // below
 
@@ -259,7 +271,7 @@ const fa::Variant* select_fwd(int di, int causal, int64_t N, int64_t BH, int64_t
   auto pick = [&](int v) {
     return v < count && usable(vs[v], di, causal, dt) ? &vs[v] : var;
   };
-  if (N <= kFwdDecodeQueries) {
+  if (N <= kFwdDecodeQueries || (!causal && N <= kFwdShortQueries)) {
     const fa::Variant* half = pick(kFwd16HalfVariant);
     if (half != var && N <= half->rows / fwd_pack(*half, group, N)) return half;
   }
