@@ -337,6 +337,18 @@ def test_split_forward_workspace_sizing_and_rejection(lib):
     ws = lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 32768, 128, 0)
     per_split = 1 * 32 * 1 * (128 + 1) * 4
     assert ws > 0 and ws % per_split == 0 and 2 <= ws // per_split <= 64
+    # under the (top-left) mask only the first min(N_q, N_kv) keys are seen by
+    # any query, and the key ranges cover those: 128 queries against 32768
+    # keys have too few to split (the forward and dQ split without the mask);
+    # 4096 against 32768 split the first 4096 keys into ranges of >= 1024
+    assert lib.fa_fwd_workspace_bytes(1, 32, 8, 128, 32768, 128, 0) > 0
+    assert lib.fa_fwd_workspace_bytes(1, 32, 8, 128, 32768, 128, 1) == 0
+    assert lib.fa_bwd_dq_workspace_bytes(1, 32, 8, 128, 32768, 128, 0) > 0
+    assert lib.fa_bwd_dq_workspace_bytes(1, 32, 8, 128, 32768, 128, 1) == 0
+    per_split = 1 * 2 * 4096 * (128 + 1) * 4
+    causal_ws = lib.fa_fwd_workspace_bytes(1, 2, 2, 4096, 32768, 128, 1)
+    assert causal_ws % per_split == 0 and 2 <= causal_ws // per_split <= 4
+    assert lib.fa_fwd_workspace_bytes(1, 2, 2, 4096, 32768, 128, 0) // per_split > 4
     assert lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 32768, 96, 0) == _lib.FA_ERR_HEAD_DIM
     assert lib.fa_fwd_workspace_bytes(1, 32, 8, 1, 0, 128, 0) == _lib.FA_ERR_BAD_SHAPE
     # a workspace smaller than required is rejected before any launch

@@ -1848,10 +1848,11 @@ SPLIT_FWD_CASES = [
     # (B, Hq, Hkv, N_q, N_kv, D, causal, dtype)
     (1, 32, 8, 1, 4000, 128, False, torch.float16),   # decoding, GQA
     (2, 4, 2, 16, 3000, 64, False, torch.float16),
-    (2, 4, 2, 16, 3000, 64, True, torch.float16),     # top-left causal: most splits empty
+    (1, 2, 2, 2100, 5000, 64, True, torch.float16),   # top-left causal: the ranges cover the
+                                                      # 2100 visible keys; early tiles see one
     (1, 2, 2, 2048, 2048, 32, True, torch.float16),   # self-attention with few heads
     (1, 3, 1, 77, 5000, 64, False, torch.bfloat16),
-    (1, 4, 4, 5, 2600, 128, True, torch.bfloat16),
+    (1, 4, 4, 2100, 2600, 128, True, torch.bfloat16),
 ]
 
 
@@ -2104,7 +2105,8 @@ def test_packed_gqa_every_forward_tiling(head_dim):
 SPLIT_DQ_CASES = [
     # (B, Hq, Hkv, N_q, N_kv, D, causal, dtype)
     (1, 32, 8, 128, 5000, 128, False, torch.float16),
-    (2, 4, 4, 64, 3000, 64, True, torch.float16),      # causal: later ranges empty
+    (1, 2, 2, 2100, 4000, 64, True, torch.float16),    # top-left causal: ranges over the
+                                                       # visible keys; later ones empty
     (1, 2, 2, 2048, 2048, 32, True, torch.float16),    # self-attention with few heads
     (1, 6, 3, 40, 4100, 64, False, torch.bfloat16),
 ]

@@ -4,7 +4,8 @@ called through the C ABI.
 
 The GPU test runs two decoding shapes that take the split path, the second
 smaller than the first, so the second call runs on the array the first left
-behind; each result must equal fa_fwd_ws's bit for bit (same kernels, same
+behind, then a causal launch whose key ranges cover the keys its queries see;
+each result must equal fa_fwd_ws's bit for bit (same kernels, same
 split, same summation order) and match the fp64 oracle at the north-star
 tolerances. The CPU test checks the size limit, which is enforced before any
 HIP call.
@@ -24,10 +25,11 @@ from fa_testutil import LSE_TOL, assert_close, make_inputs
 from oracle import oracle
 from triton_flash_attention import _lib
 
-# (B, Hq, Hkv, N_q, N_kv, D, causal); both take the split-KV forward.
+# (B, Hq, Hkv, N_q, N_kv, D, causal); all take the split-KV forward.
 NOALLOC_CASES = [
     (2, 8, 2, 3, 6000, 128, False),
-    (1, 4, 1, 2, 3000, 64, True),
+    (1, 4, 1, 2, 3000, 64, False),  # smaller: fewer partials than the call before
+    (1, 2, 1, 2100, 2400, 32, True),  # causal: ranges over the 2100 visible keys
 ]
 
 

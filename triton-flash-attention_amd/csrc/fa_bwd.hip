@@ -712,7 +712,7 @@ hipError_t dq_launch(const BwdArgs& a, hipStream_t stream) {
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
-      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+      (int64_t)b.nsplit * b.split_keys < visible_kv<CAUSAL>(a))
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -737,7 +737,7 @@ hipError_t dq_pipe_launch(const BwdArgs& a, hipStream_t stream) {
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
-      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+      (int64_t)b.nsplit * b.split_keys < visible_kv<CAUSAL>(a))
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -801,7 +801,7 @@ hipError_t dq_pipe16_launch(const BwdArgs& a, hipStream_t stream) {
   BwdArgs b = a;
   b.num_tiles = (a.N + T::BQ - 1) / T::BQ;
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
-      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+      (int64_t)b.nsplit * b.split_keys < visible_kv<CAUSAL>(a))
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * a.BH * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;

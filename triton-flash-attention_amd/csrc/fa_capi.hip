@@ -494,31 +494,45 @@ int fwd_pack(const fa::Variant& var, int64_t group, int64_t N) {
   return (int)std::gcd<int64_t>(group, var.waves);
 }
 
+// Keys some query can see: all N_kv, or under the (top-left) causal mask the
+// first min(N, N_kv), as query i sees keys j <= i.
+int64_t visible_keys(int64_t N, int64_t Nkv, int causal) {
+  return causal ? std::min<int64_t>(N, Nkv) : Nkv;
+}
+
 // Key split of a launch of `wgs` work-groups over Nkv keys (forward and dQ),
-// aiming at about `target` work-groups.
-FwdSplit key_split(int64_t wgs, int64_t Nkv, bool can_split,
+// aiming at about `target` work-groups. The ranges cover the `visible` keys
+// (a multiple of 128 at least that many): under the mask with fewer queries
+// than keys the rest are seen by no query, and ranges over them would only
+// add empty work-groups and partials (B1 Hq32 Hkv8, 128 queries against 32768
+// keys, D128, causal: 24 ranges, of which 23 were empty). A launch that does
+// not split keeps the whole key range.
+FwdSplit key_split(int64_t wgs, int64_t Nkv, int64_t visible, bool can_split,
                    int64_t target = kFwdSplitTargetWorkgroups) {
   const int whole = (int)((Nkv + 127) / 128 * 128);
   if (wgs >= kFwdSplitBelowWorkgroups || !can_split) return {1, whole};
   int64_t s = (target + wgs - 1) / wgs;
-  s = std::min<int64_t>(s, std::max<int64_t>(1, Nkv / kFwdMinSplitKeys));
+  s = std::min<int64_t>(s, std::max<int64_t>(1, visible / kFwdMinSplitKeys));
   s = std::min<int64_t>(s, kMaxFwdSplit);
   if (s <= 1) return {1, whole};
-  const int64_t keys = ((Nkv + s - 1) / s + 127) / 128 * 128;
-  return {(int)((Nkv + keys - 1) / keys), (int)keys};
+  const int64_t keys = ((visible + s - 1) / s + 127) / 128 * 128;
+  return {(int)((visible + keys - 1) / keys), (int)keys};
 }
 
 FwdSplit fwd_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv,
-                   int64_t D, int pack) {
+                   int64_t D, int pack, int causal) {
   const int64_t rows = var.rows / pack;  // query rows per head and work-group
   const int64_t target = (var.flags & fa::kFewSplits) && D >= 64 ? kFwdSplitTargetFew
                                                                 : kFwdSplitTargetWorkgroups;
-  return key_split((N + rows - 1) / rows * B * Hq / pack, Nkv, var.flags & fa::kSplitsKv, target);
+  return key_split((N + rows - 1) / rows * B * Hq / pack, Nkv, visible_keys(N, Nkv, causal),
+                   var.flags & fa::kSplitsKv, target);
 }
 
 // dQ: the same split of its key loop; the partials (fp32 dQ) are summed.
-FwdSplit dq_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv) {
-  return key_split((N + var.rows - 1) / var.rows * B * Hq, Nkv, true);
+FwdSplit dq_split(const fa::Variant& var, int64_t B, int64_t Hq, int64_t N, int64_t Nkv,
+                  int causal) {
+  return key_split((N + var.rows - 1) / var.rows * B * Hq, Nkv, visible_keys(N, Nkv, causal),
+                   true);
 }
 
 int64_t dq_workspace_bytes(const FwdSplit& sp, int64_t B, int64_t Hq, int64_t N, int64_t D) {
@@ -739,7 +753,7 @@ static int fwd_check(int dt, const char* name, const fa_half_t* q, const fa_half
   if ((rc = check_scale(scale))) return rc;
   *var = select_fwd(fa::head_dim_index(D), causal, N, B * Hq, Hq / Hkv, dt);
   if (!*var) return fail(FA_ERR_BAD_TILING, "%s: no kernel for the selected tiling", name);
-  const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, D, fwd_pack(**var, Hq / Hkv, N));
+  const FwdSplit sp = fwd_split(**var, B, Hq, N, Nkv, D, fwd_pack(**var, Hq / Hkv, N), causal);
   *need = fwd_workspace_bytes(sp, B, Hq, N, D);
   return FA_OK;
 }
@@ -769,7 +783,7 @@ static int fwd_impl(int dt, const char* name, const fa_half_t* q, const fa_half_
   auto fn = reinterpret_cast<fa::fwd_launch_fn>(var->fn[dt][fa::head_dim_index(D)][causal ? 1 : 0]);
   hipStream_t s = static_cast<hipStream_t>(stream);
   a.pack = fwd_pack(*var, Hq / Hkv, N);
-  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv, D, a.pack);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N, Nkv, D, a.pack, causal);
   a.nsplit = 1;
   a.split_keys = (int)((Nkv + 127) / 128 * 128);
   a.part = nullptr;
@@ -801,7 +815,7 @@ int64_t fa_fwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, 
   for (int dt : {fa::kF16, fa::kBF16}) {
     const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, Hq / Hkv, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_workspace_bytes: no kernel for the selected tiling");
-    const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, D, fwd_pack(*var, Hq / Hkv, N_q));
+    const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, D, fwd_pack(*var, Hq / Hkv, N_q), causal);
     bytes = std::max(bytes, fwd_workspace_bytes(sp, B, Hq, N_q, D));
   }
   return bytes;
@@ -816,7 +830,7 @@ int fa_fwd_plan_info(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_q, int64_t N_
   const fa::Variant* var = select_fwd(fa::head_dim_index(D), causal, N_q, B * Hq, Hq / Hkv, fa::kF16);
   if (!var) return fail(FA_ERR_BAD_TILING, "fa_fwd_plan_info: no kernel for the selected tiling");
   const int pack = fwd_pack(*var, Hq / Hkv, N_q);
-  const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, D, pack);
+  const FwdSplit sp = fwd_split(*var, B, Hq, N_q, N_kv, D, pack, causal);
   const int64_t grid_wgs = (N_q + var->rows / pack - 1) / (var->rows / pack) * (B * Hq / pack);
   const auto plan = fwd_launch_plan(*var, causal, pack, sp.nsplit, B * Hq, N_q, N_kv,
                                     compute_units);
@@ -974,7 +988,7 @@ static int dq_delta_impl(int dt, const char* name, const fa_half_t* q, const fa_
   fa::BwdArgs a = bwd_args(q, k, v, dO, lse, delta, B, Hq, Hkv, N, Nkv, scale);
   a.dq = reinterpret_cast<fa::half_t*>(dq);
   // Split mode (few work-groups, a workspace given): fp32 partial dQ per key range, then summed.
-  const FwdSplit sp = dq_split(*var, B, Hq, N, Nkv);
+  const FwdSplit sp = dq_split(*var, B, Hq, N, Nkv, causal);
   const int64_t need = dq_workspace_bytes(sp, B, Hq, N, D);
   const bool split = need > 0 && workspace != nullptr;
   if (split) {
@@ -1011,7 +1025,7 @@ int64_t fa_bwd_dq_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t N_
   for (int dt : {fa::kF16, fa::kBF16}) {
     const fa::Variant* var = select_dq(fa::head_dim_index(D), causal, N_q, B * Hq, dt);
     if (!var) return fail(FA_ERR_BAD_TILING, "fa_bwd_dq_workspace_bytes: no kernel for the selected tiling");
-    bytes = std::max(bytes, dq_workspace_bytes(dq_split(*var, B, Hq, N_q, N_kv), B, Hq, N_q, D));
+    bytes = std::max(bytes, dq_workspace_bytes(dq_split(*var, B, Hq, N_q, N_kv, causal), B, Hq, N_q, D));
   }
   return bytes;
 }
@@ -1072,7 +1086,7 @@ bool plan_bwd(int dt, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t Nkv
   p->dq = select_dq(di, causal, N, B * Hq, dt);
   p->dkdv = select_dkdv(di, causal, B, Hq, Hkv, N, Nkv, dt);
   if (!p->dq || !p->dkdv) return false;
-  p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv);
+  p->dq_split = dq_split(*p->dq, B, Hq, N, Nkv, causal);
   p->dkdv_nsplit = dkdv_split(*p->dkdv, B, Hq, Hkv, N, Nkv, causal);
   const int64_t dq_wgs = (N + p->dq->rows - 1) / p->dq->rows * B * Hq;
   p->pair = p->dkdv_nsplit > 1 && p->dq_split.nsplit == 1 && dq_wgs <= kPairMaxDqWorkgroups &&

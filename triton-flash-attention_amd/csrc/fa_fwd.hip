@@ -1338,7 +1338,7 @@ hipError_t fwd_pipe_launch(const FwdArgs& a, hipStream_t stream) {
     return hipErrorInvalidValue;
   b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
-      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+      (int64_t)b.nsplit * b.split_keys < visible_kv<CAUSAL>(a))
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -1371,7 +1371,7 @@ hipError_t fwd_pipe16_launch(const FwdArgs& a, hipStream_t stream) {
   if (b.pack < 1 || 4 % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
   b.num_tiles = (a.N + BM / b.pack - 1) / (BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && b.part == nullptr) || b.split_keys % 128 != 0 ||
-      (int64_t)b.nsplit * b.split_keys < a.Nkv)
+      (int64_t)b.nsplit * b.split_keys < visible_kv<CAUSAL>(a))
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;
@@ -1429,7 +1429,7 @@ hipError_t fwd_launch(const FwdArgs& a, hipStream_t stream) {
   if (b.pack < 1 || NW % b.pack != 0 || a.group % b.pack != 0) return hipErrorInvalidValue;
   b.num_tiles = (a.N + T::BM / b.pack - 1) / (T::BM / b.pack);
   if (b.nsplit < 1 || (b.nsplit > 1 && (b.part == nullptr || !fwd_tile_splits_kv<BN>())) ||
-      b.split_keys % 128 != 0 || (int64_t)b.nsplit * b.split_keys < a.Nkv)
+      b.split_keys % 128 != 0 || (int64_t)b.nsplit * b.split_keys < visible_kv<CAUSAL>(a))
     return hipErrorInvalidValue;
   const int64_t blocks = (int64_t)b.num_tiles * (a.BH / b.pack) * b.nsplit;
   if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidConfiguration;

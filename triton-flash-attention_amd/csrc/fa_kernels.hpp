@@ -46,7 +46,9 @@ struct FwdArgs {
   // [s * split_keys, (s + 1) * split_keys) and writes its fp32 partial O
   // ([nsplit, BH, N, D], normalised by its own row sums) and base-2 LSE
   // ([nsplit, BH, N], -inf where it saw no key) to `part`;
-  // launch_fwd_combine merges them. nsplit = 1: split_keys >= Nkv, part unused.
+  // launch_fwd_combine merges them. The ranges together cover the keys some
+  // query sees (visible_kv: all Nkv, or min(N, Nkv) under the causal mask).
+  // nsplit = 1: split_keys >= Nkv, part unused.
   int nsplit;
   int split_keys;  // a multiple of 128
   float* part;
@@ -87,8 +89,9 @@ struct BwdArgs {
   float* part;
   // dQ split mode (nsplit > 1 in a dQ launch): work-group split s covers keys
   // [s * split_keys, (s + 1) * split_keys) and writes its fp32 partial dQ
-  // (scaled) to part[split][B*Hq][N][D]; launch_split_sum adds them. With
-  // nsplit = 1, split_keys >= Nkv. Unused by the dK/dV launches.
+  // (scaled) to part[split][B*Hq][N][D]; launch_split_sum adds them. The
+  // ranges cover visible_kv keys; with nsplit = 1, split_keys >= Nkv. Unused
+  // by the dK/dV launches.
   int split_keys;
   // Fused Delta (dQ kernels whose variant has kFusesDelta): when o is set the
   // kernel computes Delta = rowsum(O * dO) itself and writes it to delta_out
@@ -96,6 +99,14 @@ struct BwdArgs {
   const half_t* o;
   float* delta_out;
 };
+
+// Keys some query can see, which a split launch's key ranges must cover: all
+// Nkv, or under the top-left causal mask the first min(N, Nkv) (query i sees
+// keys j <= i; the keys after them are masked for every query).
+template <bool CAUSAL, class Args>
+inline int64_t visible_kv(const Args& a) {
+  return CAUSAL && a.N < a.Nkv ? a.N : a.Nkv;
+}
 
 enum KernelKind { kFwd = 0, kDkdv = 1, kDq = 2, kNumKinds = 3 };
 
