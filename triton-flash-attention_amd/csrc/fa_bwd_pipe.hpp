@@ -217,10 +217,11 @@ __device__ __forceinline__ void dkdv_pipe_body(const BwdArgs& a, const unsigned 
 
   const int q_begin = CAUSAL ? k0 : 0;  // k0 is a multiple of 32
   // Under the causal mask a key tile past the last query (N < Nkv) sees no
-  // query; it still takes one unit (all rows read as zeros), so its
-  // dK = dV = 0 are written.
+  // query: it takes no unit (every chunk gets none, as the chunks past the
+  // last unit of a split tile do), the zeroed slot stands in for the last
+  // unit, and its dK = dV = 0 are written.
   const int ntq = max(1, (N - q_begin + T::QT - 1) / T::QT);
-  const int total_units = G * ntq;
+  const int total_units = CAUSAL && q_begin >= N ? 0 : G * ntq;
   const int chunk = (total_units + a.nsplit - 1) / a.nsplit;
   const int u_lo = min(split * chunk, total_units);
   const int nunits = min(chunk, total_units - u_lo);

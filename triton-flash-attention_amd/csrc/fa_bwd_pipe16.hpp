@@ -580,7 +580,7 @@ __device__ __forceinline__ void dkdv_pipe16_body(const BwdArgs& a, const unsigne
 
   const int q_begin = CAUSAL ? k0 : 0;  // k0 is a multiple of 32
   const int ntq = max(1, (N - q_begin + T::QT - 1) / T::QT);
-  const int total_units = QG * ntq;
+  const int total_units = CAUSAL && q_begin >= N ? 0 : QG * ntq;  // as in dkdv_pipe_body
   const int chunk = (total_units + a.nsplit - 1) / a.nsplit;
   const int u_lo = min(split * chunk, total_units);
   const int nunits = min(chunk, total_units - u_lo);
